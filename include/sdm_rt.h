@@ -1,0 +1,122 @@
+/* sdm_rt.h -- C ABI of the run-time SDM mixer core for AMD MI355X (gfx950).
+ *
+ * The reference exposes this path only as a PyTorch module, RunTimeSdm
+ * (experiments/track4/sdmllm/track4_onesdm_models.py:151-300); it has no FFI.  These entry points replace the
+ * part of RunTimeSdm.forward that lies between the input projections and the output map:
+ *   - product-key addressing of the write keys and read queries, softmax weights and write gate
+ *     (pk_address, track4_onesdm_models.py:134-148; RunTimeSdm.prepare, :195-213),
+ *   - the faded write and causal read of the per-head memory (RunTimeSdm._chunk / forward, :215-274),
+ *   - the mean read and the per-head output norm (RunTimeSdm.finish, :243-246, without the wo map).
+ * The projections (wk, wq, wv, wg) and the output map wo stay dense GEMMs in the caller.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller.  The library allocates no device memory; scratch
+ *     space is the caller's workspace of sdm_rt_workspace_bytes() bytes.
+ *   - Activations are row-major with one row per token, row index n = b * T + t.  In a row, head h of the
+ *     write keys / read queries occupies elements [h * addr_dim, (h + 1) * addr_dim), head h of the values and of
+ *     the output occupies [h * head_dim, (h + 1) * head_dim) and the gate logit of head h is element h.
+ *     Row strides are in elements.  Parameters are float32 and contiguous.
+ *   - Every call is asynchronous on the given stream (a hipStream_t passed as void*; NULL is the null stream)
+ *     and returns 0 on success or a negative status; sdm_rt_last_error() then describes the failure (a
+ *     thread-local string).  Arguments are validated before anything is launched.
+ *   - Calls hold no global mutable state; concurrent calls on different streams with different workspaces are
+ *     safe.
+ */
+#ifndef SDM_RT_H
+#define SDM_RT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum { SDM_RT_F32 = 0, SDM_RT_BF16 = 1 } sdm_rt_dtype;
+
+enum {
+  SDM_RT_OK = 0,
+  SDM_RT_EINVAL = -1,     /* bad dimension, pointer, stride or alignment */
+  SDM_RT_ENOSPACE = -2,   /* workspace too small */
+  SDM_RT_EUNSUPPORTED = -3, /* a shape outside what the kernels are built for */
+  SDM_RT_ELAUNCH = -4     /* a HIP launch failed */
+};
+
+/* Layer shape and options: the RunTimeSdm constructor arguments that reach the core
+ * (track4_onesdm_models.py:154-156). */
+typedef struct {
+  int32_t batch;        /* B */
+  int32_t seq_len;      /* T */
+  int32_t heads;        /* H */
+  int32_t head_dim;     /* dh = d / H, a multiple of 8 */
+  int32_t addr_dim;     /* d_a, even: two halves of d_a / 2 */
+  int32_t n_sub;        /* sub-keys per half; M = n_sub^2 locations per head */
+  int32_t top_k;        /* k: c1 = min(k, n_sub) per half, kk = min(k, c1^2) picks */
+  int32_t read_mean;    /* 1: r = num / (den + read_eps) (read_mode 'mean'); 0: r = num ('sum') */
+  int32_t out_norm;     /* 1: r * rsqrt(mean(r^2) + out_norm_eps) * onorm_w */
+  int32_t write_gate;   /* 1: write weights times sigmoid(gate logit + gate bias) */
+  float read_eps;       /* 1e-3 by default */
+  float out_norm_eps;   /* 1e-2 by default */
+} sdm_rt_dims;
+
+/* Per-layer parameters (float32, device). */
+typedef struct {
+  const float* keys1;     /* [H][n_sub][d_a/2], raw (unit-normalised inside) */
+  const float* keys2;     /* [H][n_sub][d_a/2] */
+  const float* addr_b;    /* [H][d_a] added to every key and query; may be NULL (zero) */
+  const float* log_scale; /* [H]; softmax temperature is exp(log_scale) */
+  const float* decay;     /* [H] per-head fade lambda in [0, 1] (RunTimeSdm.decay(), :192-193) */
+  const float* onorm_w;   /* [H][dh]; read only when out_norm */
+  const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
+} sdm_rt_params;
+
+/* Bytes of workspace sdm_rt_forward / sdm_rt_address need for these dimensions (0 on invalid dims). */
+size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
+
+/* Row pitch (entries per token and head) of the pick arrays sdm_rt_address writes: kk rounded up to 8. */
+int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims);
+
+/* Product-key addressing of one address set.  Replaces pk_address (track4_onesdm_models.py:134-148) plus the
+ * softmax weights and gate of RunTimeSdm.prepare (:203-207).
+ *   z            [B*T rows] of H * d_a addresses (before addr_b, which is added here), dtype in_dtype
+ *   gate_logits  [B*T rows] of H gate logits (before gate_bias) or NULL: weights are then not gated
+ *   slot_out     [B][H][T][pitch] int32 slot ids, the kk picks in descending score order, ties to the lower
+ *                index (pad entries -1)
+ *   score_out    same layout, float32 scores (v1 + v2) / 2; may be NULL
+ *   weight_out   same layout, float32 softmax(exp(log_scale) * score) (times the gate); may be NULL */
+int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                   const void* z, int64_t z_row_stride,
+                   const void* gate_logits, int64_t gate_row_stride,
+                   sdm_rt_dtype in_dtype,
+                   int32_t* slot_out, float* score_out, float* weight_out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* The SDM core of RunTimeSdm.forward (track4_onesdm_models.py:195-274 between the projections and wo, with
+ * finish :243-246 minus wo), reset = None.
+ *   kz, qz       [B*T rows] write keys / read queries (H * d_a each, before addr_b), dtype in_dtype
+ *   v            [B*T rows] values (H * dh), dtype in_dtype
+ *   gate_logits  [B*T rows] gate logits (H, before gate_bias), dtype in_dtype; may be NULL when write_gate is 0
+ *   *_row_stride    element stride between consecutive rows of each input (they may be column slices of one
+ *                fused projection output)
+ *   r_out        [B*T rows] of H * dh read-outs, dtype out_dtype, row stride out_row_stride
+ *   state_in_mem / state_in_cnt    [B][H][M][dh] / [B][H][M] float32 state to start from, or both NULL to
+ *                start from an empty memory (the reference always starts empty, :257-258)
+ *   state_out_mem / state_out_cnt  where to write the state after the last position, or NULL (the
+ *                reference's last_state side effect, :273) */
+int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                   const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
+                   const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
+                   sdm_rt_dtype in_dtype,
+                   void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                   const float* state_in_mem, const float* state_in_cnt,
+                   float* state_out_mem, float* state_out_cnt,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* sdm_rt_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDM_RT_H */

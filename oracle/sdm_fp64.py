@@ -1,0 +1,218 @@
+"""float64 numpy restatement of the run-time SDM mixer -- TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Every function names the reference lines it restates (``OM`` = experiments/track4/sdmllm/track4_onesdm_models.py,
+``SM`` = experiments/track4/sdmllm/track4_sdmllm_models.py).  Ties in every top-k are broken towards the lowest
+index (a stable descending sort), the rule the product kernels implement.
+
+Shapes: B batch rows, T positions, H heads, dh = d / H value width, d_a address width (two halves), n_sub sub-keys
+per half, M = n_sub**2 locations per head, k picks per token and head.
+"""
+import numpy as np
+
+
+def normalize_rows(x, eps=1e-12):
+    """x / max(||x||_2, eps) along the last axis (torch.nn.functional.normalize, used at OM:137-140)."""
+    n = np.sqrt(np.sum(x * x, axis=-1, keepdims=True))
+    return x / np.maximum(n, eps)
+
+
+def stable_topk_desc(v, k):
+    """Top-k along the last axis, sorted descending, equal values ordered by lowest index first."""
+    order = np.argsort(-v, axis=-1, kind="stable")[..., :k]
+    return np.take_along_axis(v, order, axis=-1), order
+
+
+def half_scores(z, keys1, keys2):
+    """Cosine of each address half against every unit sub-key (OM:136-140).
+
+    z (N, H, d_a); keys (H, n_sub, d_a/2) -> s1, s2 (N, H, n_sub) float64."""
+    z = np.asarray(z, np.float64)
+    half = z.shape[-1] // 2
+    u1 = normalize_rows(z[..., :half])
+    u2 = normalize_rows(z[..., half:])
+    k1 = normalize_rows(np.asarray(keys1, np.float64))
+    k2 = normalize_rows(np.asarray(keys2, np.float64))
+    return np.einsum("nhd,hsd->nhs", u1, k1), np.einsum("nhd,hsd->nhs", u2, k2)
+
+
+def pk_address(z, keys1, keys2, k):
+    """Exact product-key top-k (OM:134-148): top c1 = min(k, n_sub) per half, combine the c1 x c1 grid with score
+    (v1 + v2) / 2, keep the top kk = min(k, c1^2), slot id = i1 * n_sub + i2.
+
+    Returns sv (N, H, kk) descending and si (N, H, kk) int64."""
+    n_sub = keys1.shape[1]
+    s1, s2 = half_scores(z, keys1, keys2)
+    c1 = min(k, n_sub)
+    v1, i1 = stable_topk_desc(s1, c1)
+    v2, i2 = stable_topk_desc(s2, c1)
+    comb = ((v1[..., :, None] + v2[..., None, :]) * 0.5).reshape(*v1.shape[:-1], c1 * c1)
+    kk = min(k, c1 * c1)
+    sv, sc = stable_topk_desc(comb, kk)
+    a, b = sc // c1, sc % c1
+    si = np.take_along_axis(i1, a, -1) * n_sub + np.take_along_axis(i2, b, -1)
+    return sv, si
+
+
+def full_grid(z, keys1, keys2):
+    """Every location's score (s1[i] + s2[j]) / 2 at flat index i * n_sub + j: (N, H, n_sub^2)."""
+    s1, s2 = half_scores(z, keys1, keys2)
+    g = (s1[..., :, None] + s2[..., None, :]) * 0.5
+    return g.reshape(*g.shape[:-2], -1)
+
+
+def pk_address_bruteforce(z, keys1, keys2, k):
+    """Top-k over the whole n_sub^2 grid (the brute-force search of the reference self-test, OM:694-702)."""
+    n_sub = keys1.shape[1]
+    kk = min(k, min(k, n_sub) ** 2)
+    return stable_topk_desc(full_grid(z, keys1, keys2), kk)
+
+
+def topk_margin(z, keys1, keys2, k):
+    """fp64 gap between the kk-th and (kk+1)-th best location score (inf when every location is picked).
+
+    A pick that differs from another implementation's by float32 rounding can only occur where this is tiny."""
+    n_sub = keys1.shape[1]
+    kk = min(k, min(k, n_sub) ** 2)
+    g = full_grid(z, keys1, keys2)
+    if g.shape[-1] <= kk:
+        return np.full(g.shape[:-1], np.inf)
+    part = -np.sort(-g, axis=-1)
+    return part[..., kk - 1] - part[..., kk]
+
+
+def softmax(x, axis=-1):
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def rms_norm(x, w, eps=1e-6):
+    """RMSNorm (SM:63-71): x * rsqrt(mean(x^2) + eps) * w, in float64."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+
+
+def address_weights(sv, log_scale, gate=None):
+    """softmax(e^{log_scale} * score) over the k picks, times the write gate when given (OM:203-207).
+
+    sv (N, H, kk); log_scale (H,); gate (N, H) or None."""
+    w = softmax(sv * np.exp(np.asarray(log_scale, np.float64))[None, :, None], axis=-1)
+    if gate is not None:
+        w = w * gate[..., None]
+    return w
+
+
+def scan_recurrence(siw, ww, sir, wr, V, lam, state=None):
+    """The token recurrence of the memory (OM:276-300), read first then write.
+
+    siw, sir (B, H, T, k) int; ww, wr (B, H, T, k); V (B, H, T, dh); lam (H,).
+    state: optional (mem (B, H, M, dh), cnt (B, H, M)) to start from; M is taken from it or from max slot id.
+    Returns num (B, H, T, dh), den (B, H, T), mem, cnt (the state after the last write)."""
+    B, H, T, k = siw.shape
+    dh = V.shape[-1]
+    if state is None:
+        M = int(max(siw.max(initial=0), sir.max(initial=0))) + 1
+        mem = np.zeros((B, H, M, dh))
+        cnt = np.zeros((B, H, M))
+    else:
+        mem = np.array(state[0], np.float64)
+        cnt = np.array(state[1], np.float64)
+    lam = np.asarray(lam, np.float64)
+    bi = np.arange(B)[:, None, None]
+    hi = np.arange(H)[None, :, None]
+    num = np.zeros((B, H, T, dh))
+    den = np.zeros((B, H, T))
+    for t in range(T):
+        rows = sir[:, :, t]                                  # (B, H, k)
+        got = mem[bi, hi, rows]                              # (B, H, k, dh)
+        num[:, :, t] = np.einsum("bhk,bhkd->bhd", wr[:, :, t], got)
+        den[:, :, t] = np.einsum("bhk,bhk->bh", wr[:, :, t], cnt[bi, hi, rows])
+        mem *= lam[None, :, None, None]
+        cnt *= lam[None, :, None]
+        wrow = siw[:, :, t]
+        np.add.at(mem, (bi, hi, wrow), ww[:, :, t, :, None] * V[:, :, t, None, :])
+        np.add.at(cnt, (bi, hi, wrow), ww[:, :, t])
+    return num, den, mem, cnt
+
+
+def scan_closed_form(siw, ww, sir, wr, V, lam):
+    """The same read written as the double sum of the closed form (O(T^2 k^2), tiny inputs only):
+    num_t = sum_{s<t} lam^(t-1-s) sum_{i,j} wr[t,i] ww[s,j] [sir[t,i] == siw[s,j]] V_s; den with V -> 1."""
+    B, H, T, k = siw.shape
+    num = np.zeros(V.shape)
+    den = np.zeros((B, H, T))
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                for s in range(t):
+                    match = (sir[b, h, t][:, None] == siw[b, h, s][None, :])
+                    c = float(np.sum(wr[b, h, t][:, None] * ww[b, h, s][None, :] * match))
+                    f = float(lam[h]) ** (t - 1 - s)
+                    num[b, h, t] += f * c * V[b, h, s]
+                    den[b, h, t] += f * c
+    return num, den
+
+
+def finish(num, den, read_mode="mean", read_eps=1e-3, out_norm=True, onorm_w=None, out_norm_eps=1e-2):
+    """Mean (or sum) read and the per-head output RMS norm (OM:243-246), before the output map.
+
+    num (B, H, T, dh), den (B, H, T) -> r (B, H, T, dh)."""
+    r = num / (den[..., None] + read_eps) if read_mode == "mean" else np.array(num)
+    if out_norm:
+        r = r / np.sqrt(np.mean(r * r, axis=-1, keepdims=True) + out_norm_eps) * onorm_w[None, :, None, :]
+    return r
+
+
+def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False):
+    """The SDM core between the projections and the output map.
+
+    kz, qz (B, T, H, d_a) already include addr_b; V (B, T, H, dh); gate_logits (B, T, H) or None (gate off).
+    p: dict with keys1, keys2, log_scale, decay, onorm_w.  cfg: dict with k, read_mode, read_eps, out_norm,
+    out_norm_eps.  Returns r (B, T, H, dh) in float64."""
+    B, T, H, d_a = kz.shape
+    k = cfg["k"]
+    N = B * T
+    svw, siw = pk_address(np.asarray(kz, np.float64).reshape(N, H, d_a), p["keys1"], p["keys2"], k)
+    svr, sir = pk_address(np.asarray(qz, np.float64).reshape(N, H, d_a), p["keys1"], p["keys2"], k)
+    gate = None if gate_logits is None else sigmoid(np.asarray(gate_logits, np.float64).reshape(N, H))
+    ww = address_weights(svw, p["log_scale"], gate)
+    wr = address_weights(svr, p["log_scale"], None)
+    kk = siw.shape[-1]
+
+    def bh(a):
+        return a.reshape(B, T, H, kk).transpose(0, 2, 1, 3)
+    Vb = np.asarray(V, np.float64).transpose(0, 2, 1, 3)
+    n_sub = p["keys1"].shape[1]
+    M = n_sub * n_sub
+    state = (np.zeros((B, H, M, Vb.shape[-1])), np.zeros((B, H, M)))
+    num, den, mem, cnt = scan_recurrence(bh(siw), bh(ww), bh(sir), bh(wr), Vb, p["decay"], state)
+    r = finish(num, den, cfg.get("read_mode", "mean"), cfg.get("read_eps", 1e-3), cfg.get("out_norm", True),
+               p.get("onorm_w"), cfg.get("out_norm_eps", 1e-2)).transpose(0, 2, 1, 3)
+    if return_parts:
+        return r, dict(svw=svw, siw=siw, svr=svr, sir=sir, ww=ww, wr=wr, num=num, den=den, mem=mem, cnt=cnt)
+    return r
+
+
+def layer_forward(x, p, cfg):
+    """Whole RunTimeSdm.forward in float64 (OM:195-213 prepare, OM:249-274 forward, OM:243-247 finish).
+
+    x (B, T, d); p holds the module's parameters under their state_dict names ('norm.w', 'wk.weight', ...,
+    'decays_fixed' as 'decay').  Returns y (B, T, d)."""
+    x = np.asarray(x, np.float64)
+    B, T, d = x.shape
+    H = cfg["heads"]
+    d_a = cfg["d_a"]
+    dh = d // H
+    hx = rms_norm(x, p["norm.w"])
+    kz = (hx @ p["wk.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
+    qz = (hx @ p["wq.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
+    V = (hx @ p["wv.weight"].T).reshape(B, T, H, dh)
+    g = (hx @ p["wg.weight"].T + p["wg.bias"]) if cfg.get("write_gate", True) else None
+    core_p = dict(keys1=p["keys1"], keys2=p["keys2"], log_scale=p["log_scale"], decay=p["decay"],
+                  onorm_w=p.get("onorm_w"))
+    r = core_forward(kz, qz, V, g, core_p, cfg)
+    return r.reshape(B, T, d) @ p["wo.weight"].T

@@ -1,0 +1,8 @@
+"""sdmchat_amd -- the run-time SDM mixer (RunTimeSdm) of SDMCHAT on AMD MI355X (gfx950).
+
+``RunTimeSdm``      drop-in nn.Module (same constructor, state_dict and forward signature as the reference's)
+``core``            torch-facing wrappers of the C ABI (addressing, the SDM core)
+``synthetic``       seeded synthetic parameters and inputs of the layer workloads
+``build``           compiles ``csrc/sdm_rt.hip`` into ``lib/libsdm_rt.so``
+"""
+from .runtime_sdm import RMSNorm, RunTimeSdm  # noqa: F401

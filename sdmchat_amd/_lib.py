@@ -1,0 +1,91 @@
+"""ctypes binding of ``libsdm_rt.so`` (the C ABI declared in include/sdm_rt.h).
+
+The library is loaded from ``sdmchat_amd/lib/libsdm_rt.so`` (built by ``python -m sdmchat_amd.build``).  There is no
+fallback: if the library is missing or a symbol is absent, loading raises.
+"""
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsdm_rt.so")
+
+SDM_RT_F32 = 0
+SDM_RT_BF16 = 1
+
+# every function the header declares, with its ctypes signature
+c_void_p = ctypes.c_void_p
+c_i64 = ctypes.c_int64
+
+
+class SdmRtDims(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("addr_dim", ctypes.c_int32),
+        ("n_sub", ctypes.c_int32),
+        ("top_k", ctypes.c_int32),
+        ("read_mean", ctypes.c_int32),
+        ("out_norm", ctypes.c_int32),
+        ("write_gate", ctypes.c_int32),
+        ("read_eps", ctypes.c_float),
+        ("out_norm_eps", ctypes.c_float),
+    ]
+
+
+class SdmRtParams(ctypes.Structure):
+    _fields_ = [
+        ("keys1", c_void_p),
+        ("keys2", c_void_p),
+        ("addr_b", c_void_p),
+        ("log_scale", c_void_p),
+        ("decay", c_void_p),
+        ("onorm_w", c_void_p),
+        ("gate_bias", c_void_p),
+    ]
+
+
+SIGNATURES = {
+    "sdm_rt_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
+    "sdm_rt_pick_pitch": (ctypes.c_int32, [ctypes.POINTER(SdmRtDims)]),
+    "sdm_rt_address": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                      c_void_p, c_i64, c_void_p, c_i64, ctypes.c_int,
+                                      c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_forward": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                      c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                                      ctypes.c_int,
+                                      c_void_p, c_i64, ctypes.c_int,
+                                      c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_last_error": (ctypes.c_char_p, []),
+}
+
+_LIB = None
+
+
+def load(path=None):
+    """Load (once) and return the library with every declared signature set."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(f"run-time SDM HIP library not built: {p} is missing (python -m sdmchat_amd.build)")
+    lib = ctypes.CDLL(p)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+class SdmRtError(RuntimeError):
+    pass
+
+
+def check(rc, lib=None):
+    if rc != 0:
+        lib = lib or load()
+        raise SdmRtError(f"sdm_rt status {rc}: {lib.sdm_rt_last_error().decode()}")

@@ -1,0 +1,156 @@
+"""torch-facing wrappers of the C ABI: the SDM core on device tensors.
+
+Tensors must live on a ROCm device.  Activations are [B, T, width] with unit stride in the last dimension and a
+uniform row stride (a slice of a wider fused projection output is fine).  All work is queued on the current torch
+stream; nothing synchronises.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.SDM_RT_F32, torch.bfloat16: _lib.SDM_RT_BF16}
+
+
+def make_dims(B, T, heads, head_dim, addr_dim, n_sub, k, read_mode="mean", out_norm=True, write_gate=True,
+              read_eps=1e-3, out_norm_eps=1e-2):
+    return _lib.SdmRtDims(int(B), int(T), int(heads), int(head_dim), int(addr_dim), int(n_sub), int(k),
+                          1 if read_mode == "mean" else 0, 1 if out_norm else 0, 1 if write_gate else 0,
+                          float(read_eps), float(out_norm_eps))
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _f32(t, device):
+    if t is None:
+        return None
+    return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+def _rows(x, name, B, T, width):
+    """Row stride (elements) of a [B, T, >=width] activation whose B*T rows are uniformly strided."""
+    if x.dim() != 3 or x.shape[0] != B or x.shape[1] != T or x.shape[2] < width:
+        raise ValueError(f"{name}: expected [B={B}, T={T}, >={width}], got {tuple(x.shape)}")
+    if x.dtype not in _DT:
+        raise ValueError(f"{name}: dtype {x.dtype} is not float32 or bfloat16")
+    if x.numel() == 0:
+        return width
+    if x.stride(2) != 1:
+        raise ValueError(f"{name}: last dimension must have unit stride")
+    if B > 1 and T > 0 and x.stride(0) != T * x.stride(1):
+        raise ValueError(f"{name}: rows must be uniformly strided (stride(0) == T * stride(1))")
+    return x.stride(1)
+
+
+def _params(device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias):
+    held = [_f32(t, device) for t in (keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)]
+    prm = _lib.SdmRtParams(*[_ptr(t) for t in held])
+    return prm, held
+
+
+def workspace_bytes(dims):
+    return _lib.load().sdm_rt_workspace_bytes(ctypes.byref(dims))
+
+
+def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_bias=None):
+    """Product-key addressing of one address set (pk_address + softmax weights [+ gate]).
+
+    z [B, T, H * d_a]; keys [H, n_sub, d_a/2].  Returns slots int32, scores and weights float32, each
+    [B, H, T, kk] (descending score order, ties to the lower index)."""
+    lib = _lib.load()
+    B, T = z.shape[0], z.shape[1]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dims = make_dims(B, T, H, 8, d_a, n_sub, k, out_norm=False, write_gate=gate_logits is not None)
+    zs = _rows(z, "z", B, T, H * d_a)
+    gs = 0
+    if gate_logits is not None:
+        if gate_logits.dtype != z.dtype:
+            raise ValueError("gate_logits must have the dtype of z")
+        gs = _rows(gate_logits, "gate_logits", B, T, H)
+    dev = z.device
+    decay = torch.zeros(H, device=dev)
+    prm, held = _params(dev, keys1, keys2, addr_b, log_scale, decay, None, gate_bias)
+    pitch = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
+    if pitch <= 0:
+        raise _lib.SdmRtError(lib.sdm_rt_last_error().decode() or "invalid dimensions")
+    kk = min(k, min(k, n_sub) ** 2)
+    slots = torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev)
+    scores = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    weights = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_address(ctypes.byref(dims), ctypes.byref(prm), _ptr(z), zs, _ptr(gate_logits), gs, _DT[z.dtype],
+                            _ptr(slots), _ptr(scores), _ptr(weights), _ptr(ws), nbytes, ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    del held
+    return slots[..., :kk], scores[..., :kk], weights[..., :kk]
+
+
+class CoreWorkspace:
+    """A reusable device workspace (grows on demand)."""
+
+    def __init__(self):
+        self.buf = None
+
+    def get(self, nbytes, device):
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr_b=None, onorm_w=None,
+                 gate_bias=None, k, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2,
+                 out_dtype=None, out=None, state_in=None, want_state=False, workspace=None, params=None):
+    """The SDM core between the projections and the output map (RunTimeSdm.forward minus wk/wq/wv/wg and wo).
+
+    kz, qz [B, T, H * d_a]; v [B, T, H * dh]; gate_logits [B, T, H] or None (no write gate); all share one dtype,
+    each with its own uniform row stride.  Returns r [B, T, H * dh] (out_dtype, default v's dtype) and, when want_state, the final
+    (mem [B, H, M, dh], cnt [B, H, M]) float32 state.  ``params`` may carry a prepared (SdmRtParams, held) pair."""
+    lib = _lib.load()
+    B, T = v.shape[0], v.shape[1]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    width = v.shape[2]
+    dh = width // H
+    dims = make_dims(B, T, H, dh, d_a, n_sub, k, read_mode, out_norm, gate_logits is not None, read_eps, out_norm_eps)
+    dt = v.dtype
+    for name, x in (("kz", kz), ("qz", qz), ("gate_logits", gate_logits)):
+        if x is not None and x.dtype != dt:
+            raise ValueError(f"{name} has dtype {x.dtype}, expected {dt}")
+    vs = _rows(v, "v", B, T, H * dh)
+    ks = _rows(kz, "kz", B, T, H * d_a)
+    qs = _rows(qz, "qz", B, T, H * d_a)
+    gs = 0 if gate_logits is None else _rows(gate_logits, "gate_logits", B, T, H)
+    dev = v.device
+    if params is None:
+        params = _params(dev, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)
+    prm = params[0]
+    out_dtype = out_dtype or dt
+    if out is None:
+        out = torch.empty(B, T, H * dh, dtype=out_dtype, device=dev)
+    ostride = _rows(out, "out", B, T, H * dh)
+    M = n_sub * n_sub
+    mem_in = cnt_in = mem_out = cnt_out = None
+    if state_in is not None:
+        mem_in = state_in[0].to(device=dev, dtype=torch.float32).contiguous()
+        cnt_in = state_in[1].to(device=dev, dtype=torch.float32).contiguous()
+        if tuple(mem_in.shape) != (B, H, M, dh) or tuple(cnt_in.shape) != (B, H, M):
+            raise ValueError("state_in must be (mem [B, H, M, dh], cnt [B, H, M])")
+    if want_state:
+        mem_out = torch.empty(B, H, M, dh, dtype=torch.float32, device=dev)
+        cnt_out = torch.empty(B, H, M, dtype=torch.float32, device=dev)
+    nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))  # 0 for invalid dims: the call below reports why
+    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
+                            _ptr(gate_logits), gs, _DT[dt], _ptr(out), ostride, _DT[out_dtype], _ptr(mem_in), _ptr(cnt_in),
+                            _ptr(mem_out), _ptr(cnt_out), _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    if want_state:
+        return out, (mem_out, cnt_out)
+    return out

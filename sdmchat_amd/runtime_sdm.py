@@ -1,0 +1,166 @@
+"""RunTimeSdm: drop-in replacement of the reference's run-time SDM mixer, backed by HIP kernels for gfx950.
+
+Mirrors ``RunTimeSdm`` of experiments/track4/sdmllm/track4_onesdm_models.py:151-300: the same constructor arguments,
+parameter and buffer names and shapes (so ``load_state_dict(strict=True)`` accepts the reference's checkpoints under
+``mems.{i}.<name>``), the same default initialisation (nn.Linear layers built in the same order, sub-keys and
+address bias drawn from ``torch.Generator().manual_seed(4321 + seed)``, :159-185) and the same
+``forward(x, reset=None) -> Tensor[B, T, d]`` in ``x.dtype``.
+
+What runs where: the input RMSNorm and the four input projections (one fused GEMM) and the output map ``wo`` are
+dense torch ops (hipBLASLt); the SDM core between them -- product-key addressing, softmax weights, write gate, the
+faded write / causal read of the memory and the mean read with its per-head norm -- is one call into
+``libsdm_rt.so`` (sdm_rt_forward).  There is no CPU or pure-torch fallback: a missing library, a CPU tensor or an
+unsupported option raises.
+
+Forward only.  Gradients are not implemented: calling with autograd recording raises.  ``reset`` (segment resets at
+BOS) is not implemented yet and raises.
+"""
+import math
+
+import torch
+import torch.nn as nn
+
+from . import core
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm with a weight named ``w`` (track4_sdmllm_models.py:63-71): float math, cast back, times w."""
+
+    def __init__(self, d, eps=1e-6):
+        super().__init__()
+        self.w = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.w
+
+
+class RunTimeSdm(nn.Module):
+    """A Kanerva memory with M = n_sub^2 locations per head, written and read while the sequence is read."""
+
+    def __init__(self, d, heads=4, n_sub=32, d_a=32, k=16, decays=(0.0, 0.8, 0.99, 1.0), learn_decay=False,
+                 write_gate=True, gate_bias=0.0, read_mode="mean", out_norm=True, addr_scale=8.0, learn_scale=True,
+                 chunk=128, read_eps=1e-3, mem_in_grad=1.0, out_norm_eps=1e-2, addr_bias=0.0, seed=0):
+        super().__init__()
+        if d % heads != 0 or d_a % 2 != 0 or len(decays) != heads or read_mode not in ("mean", "sum"):
+            raise ValueError("need d % heads == 0, even d_a, one decay per head and read_mode 'mean' or 'sum'")
+        gen = torch.Generator().manual_seed(4321 + seed)
+        self.d, self.h, self.dh, self.k, self.d_a, self.n_sub = d, heads, d // heads, k, d_a, n_sub
+        self.M = n_sub * n_sub
+        self.chunk, self.read_mode, self.read_eps, self.mem_in_grad = chunk, read_mode, read_eps, mem_in_grad
+        self.write_gate, self.out_norm, self.learn_decay = write_gate, out_norm, learn_decay
+        self.out_norm_eps = out_norm_eps
+        self.enabled = True
+        self.keep_state = False   # set True to fill last_state (costs one state write per call)
+        self.norm = RMSNorm(d)
+        self.wk = nn.Linear(d, heads * d_a, bias=False)
+        self.wq = nn.Linear(d, heads * d_a, bias=False)
+        self.wv = nn.Linear(d, d, bias=False)
+        self.wg = nn.Linear(d, heads, bias=True)
+        self.wo = nn.Linear(d, d, bias=False)
+        self.keys1 = nn.Parameter(torch.randn(heads, n_sub, d_a // 2, generator=gen))
+        self.keys2 = nn.Parameter(torch.randn(heads, n_sub, d_a // 2, generator=gen))
+        self.addr_b = nn.Parameter(torch.randn(heads, d_a, generator=gen) * addr_bias)
+        self.log_scale = nn.Parameter(torch.full((heads,), math.log(addr_scale)), requires_grad=learn_scale)
+        lam = torch.tensor(decays, dtype=torch.float32)
+        if learn_decay:
+            self.decay_logit = nn.Parameter(torch.logit(lam.clamp(1e-4, 1 - 1e-4)))
+        else:
+            self.register_buffer("decays_fixed", lam, persistent=True)
+        if out_norm:
+            self.onorm_w = nn.Parameter(torch.ones(heads, self.dh))
+        self.gate_bias0 = gate_bias
+        self.last_gate = None
+        self.last_state = None
+        self._fused = None
+        self._ws = core.CoreWorkspace()
+
+    def reset_init(self):
+        """Zero output map and gate weights, constant gate bias (track4_onesdm_models.py:187-190)."""
+        nn.init.zeros_(self.wo.weight)
+        nn.init.zeros_(self.wg.weight)
+        nn.init.constant_(self.wg.bias, self.gate_bias0)
+
+    def decay(self):
+        """Per-head fade (track4_onesdm_models.py:192-193)."""
+        return torch.sigmoid(self.decay_logit) if self.learn_decay else self.decays_fixed
+
+    # -- fused input projection ----------------------------------------------------------------------------------
+    def _fused_weight(self, dtype):
+        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 64), cached until a weight changes."""
+        ws = (self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight)
+        key = (dtype, ws[0].device) + tuple((w.data_ptr(), w._version) for w in ws)
+        if self._fused is not None and self._fused[0] == key:
+            return self._fused[1], self._fused[2]
+        rows = sum(w.shape[0] for w in ws)
+        padded = (rows + 63) // 64 * 64
+        W = torch.zeros(padded, self.d, dtype=dtype, device=ws[0].device)
+        W[:rows].copy_(torch.cat([w.detach() for w in ws], 0))
+        wo = self.wo.weight.detach().to(dtype)
+        self._fused = (key, W, wo)
+        return W, wo
+
+    def _check(self, x, reset):
+        if reset is not None:
+            raise NotImplementedError("RunTimeSdm HIP core: reset (BOS segment masks) is not implemented")
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise RuntimeError("RunTimeSdm HIP core is forward-only: call it under torch.no_grad() or "
+                               "torch.inference_mode()")
+        if x.device.type != "cuda":
+            raise RuntimeError("RunTimeSdm HIP core needs a ROCm device tensor")
+        if x.dim() != 3 or x.shape[-1] != self.d:
+            raise ValueError(f"expected x of shape [B, T, {self.d}], got {tuple(x.shape)}")
+
+    def _compute_dtype(self, x):
+        if x.dtype == torch.bfloat16:
+            return torch.bfloat16
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return torch.bfloat16
+        if x.dtype == torch.float32:
+            return torch.float32
+        raise ValueError(f"unsupported input dtype {x.dtype}")
+
+    def _project(self, x, dt):
+        """RMSNorm then one fused GEMM for wk, wq, wv, wg (prepare, track4_onesdm_models.py:197-206).  Returns views
+        kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer;
+        addr_b and the gate bias are added inside the core."""
+        H, d_a, d = self.h, self.d_a, self.d
+        hx = self.norm(x).float()
+        W = self._fused_weight(dt)[0]
+        proj = torch.matmul(hx.to(dt), W.t())                          # [B, T, padded rows]
+        o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
+        g = proj[..., o_g:o_g + H] if self.write_gate else None
+        return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
+
+    def forward(self, x, reset=None):
+        """x [B, T, d] -> y [B, T, d] in x.dtype; every call starts from an empty memory
+        (track4_onesdm_models.py:249-274).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)."""
+        B, T, _ = x.shape
+        if not self.enabled:
+            return torch.zeros_like(x)
+        self._check(x, reset)
+        dt = self._compute_dtype(x)
+        H = self.h
+        with torch.autocast("cuda", enabled=False):
+            kz, qz, V, g = self._project(x, dt)
+            wo = self._fused_weight(dt)[1]
+            res = core.core_forward(
+                kz, qz, V, g, keys1=self.keys1, keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(),
+                addr_b=self.addr_b, onorm_w=self.onorm_w if self.out_norm else None,
+                gate_bias=self.wg.bias if self.write_gate else None, k=self.k, read_mode=self.read_mode,
+                out_norm=self.out_norm, read_eps=self.read_eps, out_norm_eps=self.out_norm_eps, out_dtype=dt,
+                want_state=self.keep_state, workspace=self._ws)
+            r, state = (res if self.keep_state else (res, None))
+            y = torch.matmul(r, wo.t()).to(x.dtype)
+        if self.write_gate:
+            self.last_gate = torch.sigmoid(g.float() + self.wg.bias.detach().float())
+        else:
+            self.last_gate = torch.ones(B, T, H, device=x.device)
+        self.last_state = state
+        return y
+
+    def forward_sequential(self, x, reset=None):
+        """The token recurrence of the reference (track4_onesdm_models.py:276-300).  It is the same function as
+        forward; the HIP core computes it once, so this is forward."""
+        return self.forward(x, reset)

@@ -1,0 +1,58 @@
+"""Seeded synthetic layer parameters and inputs for the run-time SDM mixer workloads.
+
+Everything is drawn with numpy's PCG64 from an integer seed, so the same arrays are produced on any machine.
+Parameter names and shapes are the state_dict of the reference's ``RunTimeSdm`` (track4_onesdm_models.py:154-185):
+2-D weights Xavier-uniform U(+-sqrt(6 / (fan_in + fan_out))), wg.bias 0, norm.w = onorm_w = 1, keys1/keys2 ~ N(0, 1),
+addr_b 0, log_scale ln 8, per-head fades decays_fixed ~ U(0.9, 0.999); inputs x ~ N(0, 1).
+"""
+import math
+
+import numpy as np
+
+# The single-layer workloads: a fp32 validation shape and the bf16 throughput shape.
+LAYER_SMALL = dict(B=1, T=256, d=768, heads=12, n_sub=32, d_a=64, k=8)
+LAYER_BENCH = dict(B=8, T=2048, d=768, heads=12, n_sub=32, d_a=64, k=8)
+
+
+def layer_cfg(d=768, heads=12, n_sub=32, d_a=64, k=8, chunk=128, **extra):
+    """Constructor-style configuration of one layer (mean read, out-norm on, write gate on)."""
+    cfg = dict(d=d, heads=heads, n_sub=n_sub, d_a=d_a, k=k, chunk=chunk, read_mode="mean", read_eps=1e-3,
+               out_norm=True, out_norm_eps=1e-2, write_gate=True)
+    cfg.update(extra)
+    return cfg
+
+
+def xavier(rng, fan_out, fan_in):
+    bound = math.sqrt(6.0 / (fan_in + fan_out))
+    return rng.uniform(-bound, bound, size=(fan_out, fan_in)).astype(np.float32)
+
+
+def layer_params(cfg, seed=0, decay_range=(0.9, 0.999), decays=None):
+    """float32 numpy parameters keyed by state_dict name."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    d, H, n_sub, d_a = cfg["d"], cfg["heads"], cfg["n_sub"], cfg["d_a"]
+    dh = d // H
+    p = {
+        "norm.w": np.ones(d, np.float32),
+        "wk.weight": xavier(rng, H * d_a, d),
+        "wq.weight": xavier(rng, H * d_a, d),
+        "wv.weight": xavier(rng, d, d),
+        "wg.weight": xavier(rng, H, d),
+        "wg.bias": np.zeros(H, np.float32),
+        "wo.weight": xavier(rng, d, d),
+        "keys1": rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+        "keys2": rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+        "addr_b": np.zeros((H, d_a), np.float32),
+        "log_scale": np.full(H, math.log(8.0), np.float32),
+        "onorm_w": np.ones((H, dh), np.float32),
+    }
+    if decays is None:
+        p["decays_fixed"] = rng.uniform(decay_range[0], decay_range[1], size=H).astype(np.float32)
+    else:
+        p["decays_fixed"] = np.asarray(decays, np.float32)
+    return p
+
+
+def layer_input(B, T, d, seed=1):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.standard_normal((B, T, d)).astype(np.float32)

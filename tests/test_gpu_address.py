@@ -1,0 +1,98 @@
+"""GPU parity of the product-key addressing kernel (sdm_rt_address) against the golden vectors and the fp64 oracle.
+
+References: pk_address (track4_onesdm_models.py:134-148), softmax weights and gate (:203-207).  Picks must be
+identical to the reference's wherever the fp64 margin between the kk-th and (kk+1)-th location exceeds 1e-6; at
+exact ties the kernels keep the lowest index (the reference's topk order there is unspecified).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sdm_fp64 as O
+from tests._gpu_util import DELTA, bf16_round, gpu_address, say, valid_picks
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(g, H):
+    return dict(keys1=g["keys1"], keys2=g["keys2"], addr_b=np.zeros((H, g["z"].shape[-1]), np.float32),
+                log_scale=np.full(H, np.log(8.0), np.float32), decay=np.zeros(H, np.float32),
+                onorm_w=np.ones((H, 8), np.float32), gate_bias=np.zeros(H, np.float32))
+
+
+def _as_tokens(a):
+    """(B, H, T, kk) -> (B*T, H, kk)."""
+    B, H, T, kk = a.shape
+    return a.transpose(0, 2, 1, 3).reshape(B * T, H, kk)
+
+
+@pytest.mark.parametrize("name", ["layer", "default16", "tiny6", "selftest9", "k_gt_nsub", "all_picked", "ties",
+                                  "sign_halves"])
+def test_golden_vectors(golden, name):
+    g = golden[name]
+    N, H, d_a = g["z"].shape
+    k = int(g["k"])
+    say("golden", name, g["z"].shape, "k", k)
+    slots, scores, _ = gpu_address(g["z"].reshape(1, N, H * d_a), _params(g, H), k)
+    si, sv = _as_tokens(slots), _as_tokens(scores)
+    assert si.shape == g["si"].shape
+    margin = O.topk_margin(g["z"], g["keys1"], g["keys2"], k)
+    same = np.all(np.sort(si, -1) == np.sort(g["si"], -1), -1)
+    assert np.all(same | (margin < DELTA)), f"{(~same & (margin >= DELTA)).sum()} picks differ away from ties"
+    # near a tie any equally good pick set is valid; where every score is exactly 0 (a zero address) the kernel's
+    # lowest-index rule picks slots 0..kk-1
+    assert np.all(valid_picks(g["z"], g["keys1"], g["keys2"], k, si))
+    zero = np.all(g["z"] == 0, -1)
+    if zero.any():
+        assert np.all(si[zero] == np.arange(si.shape[-1]))
+    np.testing.assert_allclose(sv, g["sv"], atol=3e-7, rtol=0)
+    assert np.all(np.diff(sv, axis=-1) <= 0)
+
+
+def test_bf16_addresses_match_oracle_on_the_same_values():
+    rng = np.random.Generator(np.random.PCG64(31))
+    H, n_sub, d_a, B, T = 12, 32, 64, 2, 300
+    z = bf16_round(rng.standard_normal((B, T, H * d_a)))
+    p = dict(keys1=rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+             keys2=rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+             addr_b=(rng.standard_normal((H, d_a)) * 0.3).astype(np.float32),
+             log_scale=rng.uniform(1.5, 2.5, H).astype(np.float32), decay=np.zeros(H, np.float32),
+             onorm_w=np.ones((H, 8), np.float32), gate_bias=rng.uniform(-1, 1, H).astype(np.float32))
+    gate = bf16_round(rng.standard_normal((B, T, H)))
+    slots, scores, weights = gpu_address(z, p, 8, dtype=torch.bfloat16, gate=gate)
+    zz = z.astype(np.float64).reshape(B * T, H, d_a) + p["addr_b"]
+    sv, si = O.pk_address(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), 8)
+    margin = O.topk_margin(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), 8)
+    gsi = _as_tokens(slots)
+    same = np.all(np.sort(gsi, -1) == np.sort(si, -1), -1)
+    assert np.all(same | (margin < DELTA))
+    np.testing.assert_allclose(_as_tokens(scores), sv, atol=3e-7)
+    gl = gate.astype(np.float64).reshape(B * T, H) + p["gate_bias"]
+    w = O.address_weights(sv, p["log_scale"].astype(np.float64), O.sigmoid(gl))
+    np.testing.assert_allclose(_as_tokens(weights)[same], w[same], atol=2e-6, rtol=2e-6)
+
+
+def test_full_bench_shape_picks():
+    """All 2 x 196,608 addresses of the B=8, T=2048, H=12 workload (bf16 inputs) against the fp64 oracle."""
+    rng = np.random.Generator(np.random.PCG64(32))
+    H, n_sub, d_a, B, T = 12, 32, 64, 8, 2048
+    p = dict(keys1=rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+             keys2=rng.standard_normal((H, n_sub, d_a // 2)).astype(np.float32),
+             addr_b=np.zeros((H, d_a), np.float32), log_scale=np.full(H, np.log(8.0), np.float32),
+             decay=np.zeros(H, np.float32), onorm_w=np.ones((H, 8), np.float32), gate_bias=np.zeros(H, np.float32))
+    z = bf16_round(rng.standard_normal((B, T, H * d_a)))
+    say("bench-shape addressing", z.shape)
+    slots, scores, _ = gpu_address(z, p, 8, dtype=torch.bfloat16)
+    zz = z.astype(np.float64).reshape(B * T, H, d_a)
+    sv, si = O.pk_address(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), 8)
+    gsi = _as_tokens(slots)
+    same = np.all(np.sort(gsi, -1) == np.sort(si, -1), -1)
+    bad = np.argwhere(~same)
+    if len(bad):
+        rows = np.unique(bad[:, 0])
+        m = O.topk_margin(zz[rows], p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), 8)
+        for (n, h) in bad:
+            j = np.searchsorted(rows, n)
+            assert m[j, h] < DELTA, f"token {n} head {h}: picks differ with margin {m[j, h]}"
+    say("mismatched picks (all at near-ties):", len(bad), "of", same.size)
+    np.testing.assert_allclose(_as_tokens(scores), sv, atol=3e-7)

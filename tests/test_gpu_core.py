@@ -1,0 +1,111 @@
+"""GPU parity of the SDM core (sdm_rt_forward: addressing + scan + finish) against the fp64 oracle.
+
+References: RunTimeSdm.prepare / _chunk / forward / finish (track4_onesdm_models.py:195-274, :243-246) and
+forward_sequential (:276-300), whose token recurrence the oracle restates.
+
+Each case is checked in two parts (tests/_gpu_util.check_core): the picks and weights of the addressing kernel
+against the oracle's (picks identical wherever the fp64 top-k margin is >= 1e-6, weights within 2e-6), then the
+read-out against the fp64 recurrence driven by those picks -- plus the fully independent oracle when no pick
+differs.  Tolerances: float32 1e-5 (abs and rel); bfloat16 2e-3, plus half a bfloat16 ulp for outputs that are
+themselves rounded to bfloat16.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests._gpu_util import bf16_round, check_core, core_inputs, gpu_core, say
+
+pytestmark = pytest.mark.gpu
+
+
+def test_layer_small_fp32():
+    """The fp32 validation workload: B=1, T=256, H=12, dh=64, d_a=64, M=1024, k=8."""
+    check_core(*core_inputs(1, 256, 12, 64, 64, 32, seed=41), 8)
+
+
+def test_layer_small_bf16():
+    kz, qz, V, g, p = core_inputs(1, 256, 12, 64, 64, 32, seed=42)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3)
+
+
+def test_bf16_inputs_fp32_out_and_fused_layout():
+    """bf16 activations read from one fused buffer, read-out kept in float32: the arithmetic between the bf16 inputs
+    and the output is float32, so the float32 tolerance applies."""
+    kz, qz, V, g, p = core_inputs(2, 100, 12, 64, 64, 32, seed=43)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, out_dtype=torch.float32, tol=1e-5, fused=True)
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 130, 200])
+def test_ragged_lengths_and_extreme_fades(T):
+    """Lengths around the 64-position chunk, with fades 0 (previous-token head) and 1 (never fades)."""
+    decays = [0.0, 1.0, 0.5, 0.9, 0.99, 0.999, 0.0, 1.0]
+    check_core(*core_inputs(2, T, 8, 16, 16, 8, seed=44 + T, decays=decays, addr_bias=0.3), 8)
+
+
+@pytest.mark.parametrize("read_mode,out_norm,gate", [("sum", True, True), ("mean", False, True), ("sum", False, False),
+                                                     ("mean", True, False)])
+def test_read_modes_norm_and_gate(read_mode, out_norm, gate):
+    check_core(*core_inputs(1, 150, 4, 32, 32, 16, seed=45, gate=gate), 8, read_mode=read_mode, out_norm=out_norm)
+
+
+def test_small_fades_rescale_the_slab_often():
+    """Fades 0.05-0.3 push the slab multiplier below 2^-60 every chunk, exercising the rescale path."""
+    check_core(*core_inputs(1, 400, 4, 16, 16, 8, seed=52, decays=(0.05, 0.1, 0.2, 0.3)), 8)
+
+
+def test_reference_selftest_shape():
+    """d=32, 4 heads of width 8, n_sub 6 (36 locations), d_a 8, k 5, fades (0, 0.7, 0.95, 1) -- the reference's
+    self-test layer (track4_onesdm_models.py:704)."""
+    check_core(*core_inputs(2, 23, 4, 8, 8, 6, seed=46, decays=(0.0, 0.7, 0.95, 1.0)), 5)
+
+
+def test_reference_default_shape_k16():
+    """The reference's default mixer: 4 heads of width 64, d_a 32, n_sub 32, k 16, fades (0, 0.8, 0.99, 1)."""
+    check_core(*core_inputs(2, 160, 4, 64, 32, 32, seed=47, decays=(0.0, 0.8, 0.99, 1.0)), 16)
+
+
+def test_state_carry_equals_one_pass():
+    """Starting from the state another call left equals one pass over the concatenated sequence (kernel against
+    itself, float32)."""
+    kz, qz, V, g, p = core_inputs(2, 300, 6, 16, 16, 12, seed=48, decays=(0.0, 0.6, 0.9, 0.99, 1.0, 0.95))
+    r_all, (m_all, c_all) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
+    cut = 137
+    r1, st = gpu_core(kz[:, :cut], qz[:, :cut], V[:, :cut], g[:, :cut], p, 8, want_state=True)
+    r2, (m2, c2) = gpu_core(kz[:, cut:], qz[:, cut:], V[:, cut:], g[:, cut:], p, 8, state_in=st, want_state=True)
+    np.testing.assert_allclose(np.concatenate([r1, r2], 1), r_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(m2, m_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(c2, c_all, atol=1e-5, rtol=1e-5)
+
+
+def test_final_state_matches_oracle_recurrence():
+    from oracle import sdm_fp64 as O
+    from tests._gpu_util import gpu_address
+    kz, qz, V, g, p = core_inputs(2, 150, 4, 16, 16, 8, seed=53, decays=(0.0, 0.5, 0.97, 1.0))
+    _, (mem, cnt) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
+    siw, _, ww = gpu_address(kz, p, 8, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8)
+    Vb = V.astype(np.float64).reshape(2, 150, 4, 16).transpose(0, 2, 1, 3)
+    _, _, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                       wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
+                                       (np.zeros((2, 4, 64, 16)), np.zeros((2, 4, 64))))
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+
+
+def test_zero_length_and_empty_batch():
+    kz, qz, V, g, p = core_inputs(2, 0, 4, 8, 8, 4, seed=49)
+    r, (m, c) = gpu_core(kz, qz, V, g, p, 4, want_state=True)
+    assert r.shape == (2, 0, 32) and np.all(m == 0) and np.all(c == 0)
+    kz, qz, V, g, p = core_inputs(0, 5, 4, 8, 8, 4, seed=50)
+    assert gpu_core(kz, qz, V, g, p, 4).shape == (0, 5, 32)
+
+
+def test_bench_shape_bf16():
+    """B=8, T=2048, H=12, bf16: every pick against the oracle, and the read-out of three (batch row, head) slabs
+    against the fp64 recurrence."""
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=51)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, slabs=[(0, 0), (3, 7), (7, 11)])
+    say("bench-shape picks that differ from the oracle (all at near-ties):", flips)

@@ -1,0 +1,88 @@
+"""The C-ABI library loads and exports every function include/sdm_rt.h declares; argument validation runs on the host
+before anything is launched, so it is checked here without a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from sdmchat_amd import _lib, core
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(sdm_rt_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(_lib.LIB_PATH), "build the library first (python -m sdmchat_amd.build)"
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    names = declared_functions()
+    assert {"sdm_rt_forward", "sdm_rt_address", "sdm_rt_workspace_bytes", "sdm_rt_last_error"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def _dims(**over):
+    d = dict(B=8, T=2048, heads=12, head_dim=64, addr_dim=64, n_sub=32, k=8)
+    d.update(over)
+    return core.make_dims(d["B"], d["T"], d["heads"], d["head_dim"], d["addr_dim"], d["n_sub"], d["k"])
+
+
+def test_workspace_and_pitch():
+    lib = _lib.load()
+    dims = _dims()
+    ws = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))
+    picks = 8 * 2048 * 12 * 8
+    assert ws >= picks * (2 + 2 + 4 + 4) + 8 * 2048 * 12 * 64 * 4
+    assert lib.sdm_rt_pick_pitch(ctypes.byref(dims)) == 8
+    assert lib.sdm_rt_pick_pitch(ctypes.byref(_dims(k=16, addr_dim=32))) == 16
+    assert lib.sdm_rt_pick_pitch(ctypes.byref(_dims(k=5, n_sub=6))) == 8
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(head_dim=12), "head_dim"),
+    (dict(addr_dim=7), "addr_dim"),
+    (dict(k=0), "top_k"),
+    (dict(k=32, n_sub=32), "<= 16"),
+    (dict(n_sub=300), "65535"),
+    (dict(heads=0), "heads"),
+])
+def test_invalid_dims_are_rejected_before_launch(over, msg):
+    lib = _lib.load()
+    dims = _dims(**over)
+    assert lib.sdm_rt_workspace_bytes(ctypes.byref(dims)) == 0
+    prm = _lib.SdmRtParams()
+    one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, one, 4096, 0,
+                            None, None, None, None, one, 1 << 30, None)
+    assert rc != 0
+    assert msg in lib.sdm_rt_last_error().decode()
+
+
+def test_missing_pointers_and_small_workspace_are_rejected():
+    lib = _lib.load()
+    dims = _dims()
+    prm = _lib.SdmRtParams()
+    one = ctypes.c_void_p(16)
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, one, 4096, 0,
+                            None, None, None, None, one, 1 << 30, None)
+    assert rc == -1 and "keys1" in lib.sdm_rt_last_error().decode()
+    prm = _lib.SdmRtParams(one, one, None, one, one, one, None)
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, one, 4096, 0,
+                            None, None, None, None, one, 1024, None)
+    assert rc == -2 and "workspace" in lib.sdm_rt_last_error().decode()
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, one, 4096, 0,
+                            None, None, None, None, one, 1 << 30, None)
+    assert rc == -1 and "gate_logits" in lib.sdm_rt_last_error().decode()
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 7, one, 4096, 0,
+                            None, None, None, None, one, 1 << 30, None)
+    assert rc == -1 and "dtype" in lib.sdm_rt_last_error().decode()

@@ -1,0 +1,141 @@
+"""Pins the oracle's memory scan and layer forward (CPU only).
+
+References: RunTimeSdm._chunk / forward / forward_sequential / finish (track4_onesdm_models.py:215-300) and the
+reference self-test's chunked = sequential, previous-token head and gate checks (:728-792).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sdm_fp64 as O
+from oracle import sdm_torch32 as R
+from sdmchat_amd import synthetic as S
+
+
+def _distinct_ids(rng, shape, k, M):
+    out = np.empty(shape + (k,), np.int64)
+    for idx in np.ndindex(*shape):
+        out[idx] = rng.choice(M, size=k, replace=False)
+    return out
+
+
+@pytest.mark.parametrize("lams", [(0.0, 0.5, 1.0), (0.9, 0.99, 0.999)])
+def test_recurrence_equals_closed_form_double_sum(lams):
+    rng = np.random.Generator(np.random.PCG64(21))
+    B, H, T, k, M, dh = 2, 3, 14, 3, 7, 5
+    siw = _distinct_ids(rng, (B, H, T), k, M)
+    sir = _distinct_ids(rng, (B, H, T), k, M)
+    ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
+    V = rng.standard_normal((B, H, T, dh))
+    lam = np.array(lams)
+    num, den, _, _ = O.scan_recurrence(siw, ww, sir, wr, V, lam,
+                                       state=(np.zeros((B, H, M, dh)), np.zeros((B, H, M))))
+    cn, cd = O.scan_closed_form(siw, ww, sir, wr, V, lam)
+    np.testing.assert_allclose(num, cn, atol=1e-12)
+    np.testing.assert_allclose(den, cd, atol=1e-12)
+    assert np.all(num[:, :, 0] == 0) and np.all(den[:, :, 0] == 0)
+
+
+def test_recurrence_state_carry_is_the_same_as_one_pass():
+    rng = np.random.Generator(np.random.PCG64(22))
+    B, H, T, k, M, dh = 1, 2, 20, 2, 9, 4
+    siw = _distinct_ids(rng, (B, H, T), k, M)
+    sir = _distinct_ids(rng, (B, H, T), k, M)
+    ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
+    V = rng.standard_normal((B, H, T, dh))
+    lam = np.array([0.7, 1.0])
+    z = (np.zeros((B, H, M, dh)), np.zeros((B, H, M)))
+    n_all, d_all, m_all, c_all = O.scan_recurrence(siw, ww, sir, wr, V, lam, state=z)
+    n1, d1, m1, c1 = O.scan_recurrence(siw[:, :, :8], ww[:, :, :8], sir[:, :, :8], wr[:, :, :8], V[:, :, :8], lam,
+                                       state=z)
+    n2, d2, m2, c2 = O.scan_recurrence(siw[:, :, 8:], ww[:, :, 8:], sir[:, :, 8:], wr[:, :, 8:], V[:, :, 8:], lam,
+                                       state=(m1, c1))
+    np.testing.assert_allclose(np.concatenate([n1, n2], 2), n_all, atol=1e-12)
+    np.testing.assert_allclose(m2, m_all, atol=1e-12)
+    np.testing.assert_allclose(c2, c_all, atol=1e-12)
+
+
+def _small_layer(seed=3, **over):
+    cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8, **over)
+    p = S.layer_params(cfg, seed=seed, decays=(0.0, 0.6, 0.97, 1.0))
+    return cfg, p
+
+
+def _p64(p):
+    q = {k: v.astype(np.float64) for k, v in p.items()}
+    q["decay"] = q["decays_fixed"]
+    return q
+
+
+@pytest.mark.parametrize("chunk", [1, 5, 7, 23, 64, 128, 77])
+def test_torch_chunked_equals_fp64_recurrence(chunk):
+    cfg, p = _small_layer()
+    x = S.layer_input(2, 77, 64, seed=4)
+    pt = {k: torch.from_numpy(v) for k, v in p.items()}
+    y32 = R.forward(torch.from_numpy(x), pt, cfg, chunk=chunk).numpy()
+    y64 = O.layer_forward(x, _p64(p), cfg)
+    np.testing.assert_allclose(y32, y64, atol=1e-5, rtol=1e-4)
+
+
+def test_torch_sequential_equals_fp64():
+    cfg, p = _small_layer(seed=5)
+    x = S.layer_input(1, 40, 64, seed=6)
+    pt = {k: torch.from_numpy(v) for k, v in p.items()}
+    np.testing.assert_allclose(R.forward_sequential(torch.from_numpy(x), pt, cfg).numpy(),
+                               O.layer_forward(x, _p64(p), cfg), atol=1e-5, rtol=1e-4)
+
+
+def test_previous_token_head_closed_form():
+    """Fade 0, zero key/query maps: every token addresses the same k locations; position t reads exactly what t-1
+    wrote through the mean read: y[t] = V[t-1] * (1/k) / (1/k + eps), y[0] = 0 (reference self-test :773-785)."""
+    cfg = S.layer_cfg(d=8, heads=1, n_sub=4, d_a=4, k=4, write_gate=False, out_norm=False)
+    p = S.layer_params(cfg, seed=7, decays=(0.0,))
+    p["wk.weight"][:] = 0
+    p["wq.weight"][:] = 0
+    p["wo.weight"] = np.eye(8, dtype=np.float32)
+    x = S.layer_input(1, 9, 8, seed=8)
+    y = O.layer_forward(x, _p64(p), cfg)
+    hx = O.rms_norm(x, np.ones(8))
+    V = hx @ p["wv.weight"].T.astype(np.float64)
+    want = V[0, :-1] * 0.25 / (0.25 + 1e-3)
+    np.testing.assert_allclose(y[0, 1:], want, atol=1e-12)
+    assert np.all(y[0, 0] == 0)
+
+
+def test_never_fading_head_is_a_running_mean():
+    """Fade 1 with one shared address: r[t] = (sum_{s<t} V_s / k) / (t / k + eps)."""
+    cfg = S.layer_cfg(d=8, heads=1, n_sub=4, d_a=4, k=4, write_gate=False, out_norm=False)
+    p = S.layer_params(cfg, seed=9, decays=(1.0,))
+    p["wk.weight"][:] = 0
+    p["wq.weight"][:] = 0
+    p["wo.weight"] = np.eye(8, dtype=np.float32)
+    x = S.layer_input(1, 12, 8, seed=10)
+    y = O.layer_forward(x, _p64(p), cfg)
+    V = O.rms_norm(x, np.ones(8)) @ p["wv.weight"].T.astype(np.float64)
+    csum = np.cumsum(V[0], 0)
+    t = np.arange(1, 12)[:, None]
+    np.testing.assert_allclose(y[0, 1:], (csum[:-1] / 4) / (t / 4 + 1e-3), atol=1e-12)
+
+
+def test_gate_near_zero_gives_zero_reads():
+    cfg, p = _small_layer(seed=11)
+    p["wg.weight"][:] = 0
+    p["wg.bias"][:] = -30.0
+    x = S.layer_input(1, 30, 64, seed=12)
+    y = O.layer_forward(x, _p64(p), dict(cfg, out_norm=False))
+    assert np.abs(y).max() < 1e-6
+
+
+def test_zero_output_map_gives_exact_zero():
+    cfg, p = _small_layer(seed=13)
+    p["wo.weight"][:] = 0
+    x = S.layer_input(1, 30, 64, seed=14)
+    assert np.all(O.layer_forward(x, _p64(p), cfg) == 0)
+
+
+def test_finish_closed_form():
+    num = np.array([[[[3.0, 4.0]]]])
+    den = np.array([[[1.0]]])
+    r = O.finish(num, den, "mean", 0.0, True, np.array([[2.0, 2.0]]), 0.0)
+    np.testing.assert_allclose(r[0, 0, 0], np.array([3.0, 4.0]) / np.sqrt(12.5) * 2, rtol=1e-15)
+    np.testing.assert_allclose(O.finish(num, den, "sum", 1.0, False), num)
