@@ -1,0 +1,164 @@
+"""Throughput of the run-time SDM mixer forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload: one RunTimeSdm layer forward at B=8, T=2048, d=768, 12 heads of width 64, 1,024 product-key locations
+per head, k=8, bf16 activations and weights, float32 memory state, synthetic seeded inputs and Xavier weights.  A
+step is one module forward (RMSNorm, fused input projection, SDM core, output map) over the 16,384 tokens, with
+inputs already resident in HBM.  Prints one JSON line.
+
+roofline: the SDM core (sdm_rt_forward: addressing, scan, finish) is HBM-bound.  Its algorithmic traffic is
+6,168 B per token (kz, qz, V in bf16 = 3 x 1,536 B, gate logits 24 B, read-out 1,536 B) plus 104,544 B of
+parameters per call: 101,161,056 B at this shape.  achieved = that / the core's mean call time, timed with HIP events
+on the stream the kernels run on.  traffic = HBM bytes per call from rocprofv3 FETCH_SIZE / WRITE_SIZE counters,
+read from profiles/traffic_core_bench.txt when present (null otherwise).
+
+cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle/sdm_torch32.py, the reference's
+dense chunk algorithm) on the same workload, all host cores, one warm call then best of three.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "RunTimeSdm fwd tokens/sec @B=8,T=2048,d=768 (1 GPU) + % HBM roofline"
+B, T, D, H, N_SUB, D_A, K = 8, 2048, 768, 12, 32, 64, 8
+HBM_PEAK_GBS = 8000.0
+CORE_BYTES_PER_TOKEN = 3 * H * 64 * 2 + H * 2 + H * 64 * 2          # 6,168
+CORE_PARAM_BYTES = 2 * H * N_SUB * (D_A // 2) * 4 + H * D_A * 4 + 2 * H * 4 + H * 64 * 4   # keys, addr_b, scale, fade, onorm
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    path = os.path.join(ROOT, "profiles", "traffic_core_bench.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_call:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline():
+    import numpy as np
+    import torch
+
+    from oracle import sdm_torch32 as R
+    from sdmchat_amd import synthetic as S
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cfg = S.layer_cfg(d=D, heads=H, n_sub=N_SUB, d_a=D_A, k=K)
+    p = {n: torch.from_numpy(v) for n, v in S.layer_params(cfg, seed=0).items()}
+    x = torch.from_numpy(S.layer_input(B, T, D, seed=1))
+    best = float("inf")
+    with torch.no_grad():
+        R.forward(x, p, cfg)
+        for _ in range(3):
+            t0 = time.perf_counter()
+            R.forward(x, p, cfg)
+            best = min(best, time.perf_counter() - t0)
+    del np
+    return {"value": round(B * T / best, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full workload B={B} T={T} in float32 (chunk 128), torch {torch.__version__} on the host CPU, "
+                      f"1 warm call then best of 3 ({best:.2f} s per call)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from sdmchat_amd import RunTimeSdm, core, synthetic as S
+
+    dev = torch.device("cuda:0")
+    cfg = S.layer_cfg(d=D, heads=H, n_sub=N_SUB, d_a=D_A, k=K)
+    params = S.layer_params(cfg, seed=0)
+    m = RunTimeSdm(D, heads=H, n_sub=N_SUB, d_a=D_A, k=K, decays=tuple(float(v) for v in params["decays_fixed"]))
+    m.load_state_dict({n: torch.from_numpy(v) for n, v in params.items()}, strict=True)
+    m = m.to(dev).eval()
+    x = torch.from_numpy(S.layer_input(B, T, D, seed=1)).to(dev).to(torch.bfloat16)
+
+    with torch.no_grad():
+        kz, qz, V, g = m._project(x, torch.bfloat16)
+        prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, m.wg.bias)
+        ws = core.CoreWorkspace()
+        r_out = torch.empty(B, T, D, dtype=torch.bfloat16, device=dev)
+
+        def core_call():
+            core.core_forward(kz, qz, V, g, keys1=m.keys1, keys2=m.keys2, log_scale=m.log_scale, decay=m.decay(),
+                              k=K, out=r_out, workspace=ws, params=prm)
+
+        def timed(fn, steps, warmup):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            ev0.record()
+            for _ in range(steps):
+                fn()
+            ev1.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            return ev0.elapsed_time(ev1) / steps, wall
+
+        core_ms, _ = timed(core_call, max(a.steps, 20), a.warmup)
+        log(f"core: {core_ms * 1e3:.1f} us per call")
+        if a.core_only:
+            print(json.dumps({"core_ms": core_ms}))
+            return
+        mod_ev_ms, wall = timed(lambda: m(x), a.steps, a.warmup)
+
+    ms_per_step = wall * 1e3 / a.steps
+    tokens = B * T
+    core_bytes = CORE_BYTES_PER_TOKEN * tokens + CORE_PARAM_BYTES
+    achieved = core_bytes / (core_ms * 1e-3) / 1e9
+    rec = {
+        "metric": METRIC,
+        "value": round(tokens / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, Xavier-uniform weights, N(0,1) sub-keys, fades U(0.9, 0.999))",
+        "config": {"workload": "RunTimeSdm layer forward", "batch": B, "seq_len": T, "d": D, "heads": H,
+                   "head_dim": D // H, "locations_per_head": N_SUB * N_SUB, "top_k": K,
+                   "activations": "bf16", "memory_state": "fp32"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "kernel": "SDM core (sdm_rt_forward)", "algorithmic_bytes": core_bytes,
+                     "ms_per_call": round(core_ms, 5)},
+        "core": {"ms": round(core_ms, 5), "tokens_per_s": round(tokens / (core_ms * 1e-3), 1)},
+        "module_event_ms": round(mod_ev_ms, 5),
+    }
+    if not a.no_cpu:
+        log("cpu baseline ...")
+        rec["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

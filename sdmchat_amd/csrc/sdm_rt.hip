@@ -253,164 +253,353 @@ struct ScanArgs {
   float read_eps;
 };
 
-constexpr int kCols = 8;     // value columns per workgroup
-constexpr int kChunk = 64;   // positions per chunk = lanes
+constexpr int kChunk = 64;                 // positions per chunk (one bit each in the per-location writer masks)
+constexpr size_t kLdsBytes = 160 * 1024;   // LDS per workgroup on gfx950
+constexpr int kScanThreads = 512;          // 64 positions x 8 lanes
 
-// LDS layout (floats / ints): A[M][8], cnt[M], head[M], nxt[64*KP], wq[64*KP], vc[64][8]
-__host__ __device__ inline size_t scan_lds_bytes(int M, int KP) {
-  return sizeof(float) * (static_cast<size_t>(M) * kCols + M) + sizeof(int) * M +
-         (sizeof(int) + sizeof(float)) * kChunk * KP + sizeof(float) * kChunk * kCols;
+__host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
+
+// LDS of one scan workgroup, in order: the slab A[M][CW] (CW value columns of every location), the write counts
+// cnt[M], the writer masks of the current chunk wmask[M] (bit q: position q of the chunk writes the location), the
+// chunk's picks s_iw / s_ir, read flags s_qf, write flags s_wf (u16 [64][KP]), weights s_ww / s_wr and first
+// in-chunk read coefficients s_c1 (f32 [64][KP]), values s_v[64][CW], denominators s_den[64], fade powers pw[68].
+__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW) {
+  return sizeof(float) * (static_cast<size_t>(M) * CW + pad4(M)) + sizeof(unsigned long long) * pad4(M) +
+         sizeof(uint16_t) * 4 * kChunk * KP + sizeof(float) * 3 * kChunk * KP + sizeof(float) * kChunk * CW +
+         sizeof(float) * (kChunk + 68);
 }
 
-template <int KP, typename VT, typename OutT>
-__global__ void __launch_bounds__(64) scan_kernel(ScanArgs a) {
-  extern __shared__ float lds[];
+// The KP picks of one position: slot ids (16-bit) and weights, loaded with 128-bit LDS reads.
+template <int KP>
+__device__ __forceinline__ void load_picks(const uint16_t* sl, const float* wt, int (&m)[KP], float (&w)[KP]) {
+#pragma unroll
+  for (int g = 0; g < KP / 8; ++g) {
+    const uint4 v = *reinterpret_cast<const uint4*>(sl + 8 * g);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m[8 * g + 2 * e] = static_cast<int>(u[e] & 0xffffu);
+      m[8 * g + 2 * e + 1] = static_cast<int>(u[e] >> 16);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < KP / 4; ++g) {
+    const float4 v = *reinterpret_cast<const float4*>(wt + 4 * g);
+    w[4 * g] = v.x;
+    w[4 * g + 1] = v.y;
+    w[4 * g + 2] = v.z;
+    w[4 * g + 3] = v.w;
+  }
+}
+
+// Weight with which position q (its KP slot ids sl and weights wt, the first kk live) wrote slot m (a position
+// writes a slot at most once; 0 when it did not).
+template <int KP>
+__device__ __forceinline__ float writer_weight(const uint16_t* sl, const float* wt, int m, int kk) {
+  int mq[KP];
+  float wq[KP];
+  load_picks<KP>(sl, wt, mq, wq);
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < KP; ++j) r = (j < kk && mq[j] == m) ? wq[j] : r;
+  return r;
+}
+
+// CPL consecutive floats (CPL = 4, 2, 1) of LDS, one vector access
+template <int CPL>
+struct Seg {
+  float v[CPL];
+};
+template <int CPL>
+__device__ __forceinline__ Seg<CPL> lds_seg(const float* p) {
+  Seg<CPL> r;
+  if constexpr (CPL == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    r.v[0] = t.x; r.v[1] = t.y; r.v[2] = t.z; r.v[3] = t.w;
+  } else if constexpr (CPL == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    r.v[0] = t.x; r.v[1] = t.y;
+  } else {
+    r.v[0] = *p;
+  }
+  return r;
+}
+template <int CPL>
+__device__ __forceinline__ void lds_seg_store(float* p, const Seg<CPL>& r) {
+  if constexpr (CPL == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  } else if constexpr (CPL == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
+  } else {
+    *p = r.v[0];
+  }
+}
+
+template <typename OutT, int CPL>
+__device__ __forceinline__ void store_seg(OutT* o, const float (&v)[CPL]) {
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) o[c] = from_f32<OutT>(v[c]);
+}
+
+// Sum over the 8 consecutive lanes of a position (DPP: swap neighbours, swap pairs, mirror the halves of 8).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_f<0xb1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  return v;
+}
+
+// Scan of one (batch row, head) slab over CW of its value columns, 512 threads = 64 positions x 8 lanes.
+// Per chunk of up to 64 positions, separated by barriers:
+//   P1 stage   lane (position, pick): the chunk's picks and weights, and CW/8 value columns, into LDS; the previous
+//              chunk's writer marks made from the same entries are cleared first
+//   P2 mark    each write (q, j) sets bit q of wmask[slot]
+//   P3 control lane (position, pick): the read pick's S_in count term and its earlier in-chunk writers (bits below
+//              the position in wmask; the first one's coefficient is kept, more are flagged), the position's
+//              denominator (summed over its 8 lanes), and for the write pick whether this position is the slot's
+//              lowest writer (its owner) and whether other positions write it too
+//   P4 read    lane (position, segment of CW/8 columns): mu * lam^p * S_in rows of the picks plus the in-chunk
+//              writes, divided by the denominator
+//   P5 write   the owner of each written slot adds every writer's faded value to the slot's row (one read-modify-
+//              write per lane and row: no LDS float atomics, no two threads on one row)
+// All sums are over fixed orders, so results are deterministic.
+template <int CW, int KP, typename VT, typename OutT>
+__global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
+  constexpr int CPL = CW / 8;   // value columns per data lane
+  constexpr int G = KP / 8;     // picks per control lane
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   const int M = a.M;
-  float* A = lds;                                  // [M][8]
-  float* cnt = A + static_cast<size_t>(M) * kCols; // [M]
-  int* head = reinterpret_cast<int*>(cnt + M);     // [M]
-  int* nxt = head + M;                             // [64*KP]
-  float* wq = reinterpret_cast<float*>(nxt + kChunk * KP);  // [64*KP]
-  float* vc = wq + kChunk * KP;                    // [64][8]
+  float* A = lds;
+  float* cnt = A + static_cast<size_t>(M) * CW;
+  unsigned long long* wmask = reinterpret_cast<unsigned long long*>(cnt + pad4(M));
+  uint16_t* s_iw = reinterpret_cast<uint16_t*>(wmask + pad4(M));
+  uint16_t* s_ir = s_iw + kChunk * KP;
+  uint16_t* s_qf = s_ir + kChunk * KP;
+  uint16_t* s_wf = s_qf + kChunk * KP;
+  float* s_ww = reinterpret_cast<float*>(s_wf + kChunk * KP);
+  float* s_wr = s_ww + kChunk * KP;
+  float* s_c1 = s_wr + kChunk * KP;
+  float* s_v = s_c1 + kChunk * KP;
+  float* s_den = s_v + kChunk * CW;
+  float* pw = s_den + kChunk;
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
-  const int lane = threadIdx.x;
-  const int col0 = cg * kCols;
+  const int tid = threadIdx.x;
+  const int p = tid >> 3;     // position in the chunk
+  const int l8 = tid & 7;     // pick (control) or column segment (data)
+  const int col0 = cg * CW;
   const int64_t slab = static_cast<int64_t>(b) * a.H + h;
   const float lam = a.decay[h];
+  const int kk = a.kk;
 
-  for (int m = lane; m < M; m += kChunk) {
-#pragma unroll
-    for (int c = 0; c < kCols; ++c)
-      A[m * kCols + c] = a.state_in_mem ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
+  for (int i = tid; i < M * CW; i += kScanThreads) {
+    const int m = i / CW;
+    const int c = i - m * CW;
+    A[i] = a.state_in_mem ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
+  }
+  for (int m = tid; m < M; m += kScanThreads) {
     cnt[m] = a.state_in_cnt ? a.state_in_cnt[slab * M + m] : 0.f;
-    head[m] = -1;
+    wmask[m] = 0ull;
+  }
+  if (tid <= kChunk) {
+    float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
+    for (int e = 0; e < tid; ++e) v *= lam;
+    pw[tid] = v;
   }
   float mu = 1.f;
-  __syncthreads();
+  float vreg[CPL];
 
   for (int c0 = 0; c0 < a.T; c0 += kChunk) {
     const int L = min(kChunk, a.T - c0);
-    const bool active = lane < L;
-    const int t = c0 + lane;
-
-    int iw[KP], ir[KP];
-    float ww[KP], wr[KP], v[kCols];
+    const bool active = p < L;
+    const int64_t row = static_cast<int64_t>(b) * a.T + c0 + p;
+    int iw[G], ir[G];
+    float ww[G], wr[G];
+    // P1: clear the previous chunk's marks made from this lane's entries, then stage
+    if (c0 > 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int j = l8 + 8 * g;
+        if (j < kk) wmask[s_iw[p * KP + j]] = 0ull;
+      }
+    }
     if (active) {
-      const int64_t pb = (slab * a.T + t) * KP;
+      const int64_t pb = (slab * a.T + c0 + p) * KP;
 #pragma unroll
-      for (int j = 0; j < KP; ++j) {
-        iw[j] = a.idx_w[pb + j];
-        ir[j] = a.idx_r[pb + j];
-        ww[j] = a.w_w[pb + j];
-        wr[j] = a.w_r[pb + j];
+      for (int g = 0; g < G; ++g) {
+        const int j = l8 + 8 * g;
+        iw[g] = a.idx_w[pb + j];
+        ir[g] = a.idx_r[pb + j];
+        ww[g] = a.w_w[pb + j];
+        wr[g] = a.w_r[pb + j];
+        s_iw[p * KP + j] = static_cast<uint16_t>(iw[g]);
+        s_ir[p * KP + j] = static_cast<uint16_t>(ir[g]);
+        s_ww[p * KP + j] = ww[g];
+        s_wr[p * KP + j] = wr[g];
       }
-      const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + t) * a.v_stride +
-                       static_cast<int64_t>(h) * a.dh + col0;
+      const VT* vrow = static_cast<const VT*>(a.v) + row * a.v_stride + static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
 #pragma unroll
-      for (int c = 0; c < kCols; ++c) {
-        v[c] = to_f32(vrow[c]);
-        vc[lane * kCols + c] = v[c];
-      }
-#pragma unroll
-      for (int j = 0; j < KP; ++j) {
-        if (j < a.kk) {
-          const int e = lane * KP + j;
-          nxt[e] = atomicExch(&head[iw[j]], e);
-          wq[e] = ww[j];
-        }
+      for (int c = 0; c < CPL; ++c) {
+        vreg[c] = to_f32(vrow[c]);
+        s_v[p * CW + CPL * l8 + c] = vreg[c];
       }
     }
     __syncthreads();
-
+    // P2: mark
     if (active) {
-      float acc[kCols];
-      float dacc = 0.f;
 #pragma unroll
-      for (int c = 0; c < kCols; ++c) acc[c] = 0.f;
+      for (int g = 0; g < G; ++g)
+        if (l8 + 8 * g < kk) atomicOr(&wmask[iw[g]], 1ull << p);
+    }
+    __syncthreads();
+    // P3: control
+    if (active) {
+      const float fin = mu * pw[p];
+      const unsigned long long below = (1ull << p) - 1ull;
+      float dpart = 0.f;
 #pragma unroll
-      for (int i = 0; i < KP; ++i) {
-        if (i < a.kk) {
-          const float* row = A + ir[i] * kCols;
-#pragma unroll
-          for (int c = 0; c < kCols; ++c) acc[c] = fmaf(wr[i], row[c], acc[c]);
-          dacc = fmaf(wr[i], cnt[ir[i]], dacc);
-        }
-      }
-      const float fin = mu * powf(lam, static_cast<float>(lane));
-#pragma unroll
-      for (int c = 0; c < kCols; ++c) acc[c] *= fin;
-      dacc *= fin;
-      // writes earlier in this chunk to the same locations, faded lam^(p-1-q)
-#pragma unroll
-      for (int i = 0; i < KP; ++i) {
-        if (i < a.kk) {
-          int e = head[ir[i]];
-          while (e >= 0) {
-            const int q = e / KP;
-            if (q < lane) {
-              const float f = wr[i] * wq[e] * powf(lam, static_cast<float>(lane - 1 - q));
-#pragma unroll
-              for (int c = 0; c < kCols; ++c) acc[c] = fmaf(f, vc[q * kCols + c], acc[c]);
-              dacc += f;
+      for (int g = 0; g < G; ++g) {
+        const int i = l8 + 8 * g;
+        uint16_t qf = 0xff, wf = 0;
+        float c1 = 0.f;
+        if (i < kk) {
+          const int m = ir[g];
+          const float w = wr[g];
+          dpart = fmaf(w * fin, cnt[m], dpart);
+          unsigned long long mk = wmask[m] & below;
+          if (mk) {
+            const int q = __builtin_ctzll(mk);
+            c1 = w * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m, kk) * pw[p - 1 - q];
+            dpart += c1;
+            qf = static_cast<uint16_t>(q);
+            mk &= mk - 1ull;
+            if (mk) qf |= 0x100;
+            while (mk) {
+              const int q2 = __builtin_ctzll(mk);
+              mk &= mk - 1ull;
+              dpart += w * writer_weight<KP>(s_iw + q2 * KP, s_ww + q2 * KP, m, kk) * pw[p - 1 - q2];
             }
-            e = nxt[e];
+          }
+          const unsigned long long mm = wmask[iw[g]];
+          if (__builtin_ctzll(mm) == p) wf = (mm & (mm - 1ull)) ? 3 : 1;
+        }
+        s_qf[p * KP + i] = qf;
+        s_c1[p * KP + i] = c1;
+        s_wf[p * KP + i] = wf;
+      }
+      dpart = sum8(dpart);
+      if (l8 == 0) s_den[p] = dpart;
+    }
+    __syncthreads();
+    // P4: read
+    if (active) {
+      const float fin = mu * pw[p];
+      int m[KP], qfl[KP];
+      float w[KP], c1[KP];
+      load_picks<KP>(s_ir + p * KP, s_wr + p * KP, m, w);
+      load_picks<KP>(s_qf + p * KP, s_c1 + p * KP, qfl, c1);
+      float acc[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {   // pad picks carry weight 0
+        const Seg<CPL> x = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(w[i], x.v[c], acc[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[c] *= fin;
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {
+        if ((qfl[i] & 0xff) == 0xff) continue;
+        const Seg<CPL> vq = lds_seg<CPL>(&s_v[(qfl[i] & 0xff) * CW + CPL * l8]);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c1[i], vq.v[c], acc[c]);
+        if (qfl[i] & 0x100) {   // more earlier writers of this slot in the chunk
+          unsigned long long mk = wmask[m[i]] & ((1ull << p) - 1ull);
+          mk &= mk - 1ull;
+          while (mk) {
+            const int q = __builtin_ctzll(mk);
+            mk &= mk - 1ull;
+            const float coef = w[i] * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[i], kk) * pw[p - 1 - q];
+            const Seg<CPL> v2 = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) acc[c] = fmaf(coef, v2.v[c], acc[c]);
           }
         }
       }
-      OutT* orow = static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b) * a.T + t) * a.r_stride +
-                   static_cast<int64_t>(h) * a.dh + col0;
+      if (a.read_mean) {
+        const float dv = s_den[p] + a.read_eps;
 #pragma unroll
-      for (int c = 0; c < kCols; ++c) {
-        const float r = a.read_mean ? acc[c] / (dacc + a.read_eps) : acc[c];
-        orow[c] = from_f32<OutT>(r);
+        for (int c = 0; c < CPL; ++c) acc[c] /= dv;
       }
+      store_seg<OutT, CPL>(static_cast<OutT*>(a.r_out) + row * a.r_stride + static_cast<int64_t>(h) * a.dh + col0 +
+                               CPL * l8, acc);
     }
     __syncthreads();
-
-    float mu_new = mu * powf(lam, static_cast<float>(L));
+    // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
+    float mu_new = mu * pw[L];
     if (!(mu_new >= kMuFloor)) {
-      for (int m = lane; m < M; m += kChunk) {
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) A[m * kCols + c] *= mu_new;
-        cnt[m] *= mu_new;
-      }
+      for (int i = tid; i < M * CW; i += kScanThreads) A[i] *= mu_new;
+      for (int m = tid; m < M; m += kScanThreads) cnt[m] *= mu_new;
       mu_new = 1.f;
       __syncthreads();
     }
+    // P5: write
     if (active) {
-      const float cw = powf(lam, static_cast<float>(L - 1 - lane)) / mu_new;
-#pragma unroll
-      for (int j = 0; j < KP; ++j) {
-        if (j < a.kk) {
-          const float f = cw * ww[j];
-          float* row = A + iw[j] * kCols;
-#pragma unroll
-          for (int c = 0; c < kCols; ++c) atomicAdd(&row[c], f * v[c]);
-          atomicAdd(&cnt[iw[j]], f);
-        }
-      }
-    }
-    __syncthreads();
-    if (active) {
+      const float inv_mu = 1.f / mu_new;
+      const float cpos = pw[L - 1 - p] * inv_mu;
+      int m[KP], wfl[KP];
+      float w[KP], unused[KP];
+      load_picks<KP>(s_iw + p * KP, s_ww + p * KP, m, w);
+      load_picks<KP>(s_wf + p * KP, s_ww + p * KP, wfl, unused);
+      Seg<CPL> x[KP];
 #pragma unroll
       for (int j = 0; j < KP; ++j)
-        if (j < a.kk) head[iw[j]] = -1;
+        if (wfl[j] & 1) x[j] = lds_seg<CPL>(&A[m[j] * CW + CPL * l8]);
+#pragma unroll
+      for (int j = 0; j < KP; ++j) {
+        if (!(wfl[j] & 1)) continue;
+        const float cp = cpos * w[j];
+        float dc = cp;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cp, vreg[c], x[j].v[c]);
+        if (wfl[j] & 2) {   // other (later) positions of the chunk write this slot too
+          unsigned long long rest = wmask[m[j]];
+          rest &= rest - 1ull;
+          while (rest) {
+            const int q = __builtin_ctzll(rest);
+            rest &= rest - 1ull;
+            const float cq = pw[L - 1 - q] * inv_mu * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[j], kk);
+            const Seg<CPL> vq = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cq, vq.v[c], x[j].v[c]);
+            dc += cq;
+          }
+        }
+        lds_seg_store<CPL>(&A[m[j] * CW + CPL * l8], x[j]);
+        if (l8 == 0) cnt[m[j]] += dc;
+      }
     }
     mu = mu_new;
     __syncthreads();
   }
 
   if (a.state_out_mem) {
-    for (int m = lane; m < M; m += kChunk) {
-#pragma unroll
-      for (int c = 0; c < kCols; ++c) a.state_out_mem[(slab * M + m) * a.dh + col0 + c] = mu * A[m * kCols + c];
+    for (int i = tid; i < M * CW; i += kScanThreads) {
+      const int m = i / CW;
+      const int c = i - m * CW;
+      a.state_out_mem[(slab * M + m) * a.dh + col0 + c] = mu * A[i];
     }
   }
   if (a.state_out_cnt && cg == 0) {
-    for (int m = lane; m < M; m += kChunk) a.state_out_cnt[slab * M + m] = mu * cnt[m];
+    for (int m = tid; m < M; m += kScanThreads) a.state_out_cnt[slab * M + m] = mu * cnt[m];
   }
 }
 
@@ -439,7 +628,7 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
 // ---------------------------------------------------------------------------------------------------------------
 // host side
 struct Plan {
-  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap;
+  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, scan_cw;
   // workspace offsets
   size_t off_knorm, off_iw, off_ir, off_ww, off_wr, off_rtmp, total;
 };
@@ -471,6 +660,16 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   if (p->M > 65535) return set_err(SDM_RT_EUNSUPPORTED, "n_sub^2 = %d locations exceed 65535", p->M);
   p->cap = p->c1 <= 8 && p->kk <= 8 ? 8 : 16;
   p->pitch = (p->kk + 7) / 8 * 8;
+  // widest column group per scan workgroup whose slab fits in LDS
+  p->scan_cw = 0;
+  for (int cw : {32, 16, 8}) {
+    if (p->dh % cw == 0 && scan_lds_bytes(p->M, p->pitch, cw) <= kLdsBytes) {
+      p->scan_cw = cw;
+      break;
+    }
+  }
+  if (p->scan_cw == 0)
+    return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations do not fit a slab of 8 columns in LDS", p->M);
   const size_t tok = static_cast<size_t>(p->B) * p->T;
   const size_t picks = tok * p->H * p->pitch;
   size_t o = 0;
@@ -544,17 +743,30 @@ int launch_address(const Plan& p, const AddrArgs& a, int sets, sdm_rt_dtype dt, 
   return dt == SDM_RT_BF16 ? launch_address_d<bf16_t>(p, a, sets, st) : launch_address_d<float>(p, a, sets, st);
 }
 
-template <int KP, typename VT, typename OutT>
+template <int CW, int KP, typename VT, typename OutT>
 int launch_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  const size_t lds = scan_lds_bytes(p.M, KP);
-  dim3 grid(p.dh / kCols, p.H, p.B);
-  hipLaunchKernelGGL((scan_kernel<KP, VT, OutT>), grid, dim3(kChunk), lds, st, a);
+  const size_t lds = scan_lds_bytes(p.M, KP, CW);
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<CW, KP, VT, OutT>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(kLdsBytes));
+  if (attr != hipSuccess) return set_err(SDM_RT_ELAUNCH, "scan: cannot enable %zu bytes of LDS", kLdsBytes);
+  dim3 grid(p.dh / CW, p.H, p.B);
+  hipLaunchKernelGGL((scan_kernel<CW, KP, VT, OutT>), grid, dim3(kScanThreads), lds, st, a);
   return check_launch("scan");
+}
+
+template <int CW, typename VT, typename OutT>
+int launch_scan_k(const Plan& p, const ScanArgs& a, hipStream_t st) {
+  return p.pitch == 8 ? launch_scan_t<CW, 8, VT, OutT>(p, a, st) : launch_scan_t<CW, 16, VT, OutT>(p, a, st);
 }
 
 template <typename VT, typename OutT>
 int launch_scan_v(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  return p.pitch == 8 ? launch_scan_t<8, VT, OutT>(p, a, st) : launch_scan_t<16, VT, OutT>(p, a, st);
+  switch (p.scan_cw) {
+    case 32: return launch_scan_k<32, VT, OutT>(p, a, st);
+    case 16: return launch_scan_k<16, VT, OutT>(p, a, st);
+    default: return launch_scan_k<8, VT, OutT>(p, a, st);
+  }
 }
 
 int launch_scan(const Plan& p, const ScanArgs& a, sdm_rt_dtype vt, sdm_rt_dtype ot, hipStream_t st) {
@@ -677,9 +889,6 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
     return set_err(SDM_RT_EINVAL, "state_out_mem and state_out_cnt must both be given or both be NULL");
   if (!empty && (!workspace || workspace_bytes < p.total))
     return set_err(SDM_RT_ENOSPACE, "workspace %zu bytes < required %zu", workspace_bytes, p.total);
-  const size_t lds = scan_lds_bytes(p.M, p.pitch);
-  if (lds > 160 * 1024)
-    return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations need %zu bytes of LDS (> 160 KiB)", p.M, lds);
   if (p.B == 0) return SDM_RT_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (p.T == 0) {
