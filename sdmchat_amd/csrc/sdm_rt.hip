@@ -256,17 +256,21 @@ struct ScanArgs {
 constexpr int kChunk = 64;                 // positions per chunk (one bit each in the per-location writer masks)
 constexpr size_t kLdsBytes = 160 * 1024;   // LDS per workgroup on gfx950
 constexpr int kScanThreads = 512;          // 64 positions x 8 lanes
+constexpr int kNoQ = 0x7f;                 // "no in-chunk writer" in the packed read flags
 
 __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 
 // LDS of one scan workgroup, in order: the slab A[M][CW] (CW value columns of every location), the write counts
-// cnt[M], the writer masks of the current chunk wmask[M] (bit q: position q of the chunk writes the location), the
-// chunk's picks s_iw / s_ir, read flags s_qf, write flags s_wf (u16 [64][KP]), weights s_ww / s_wr and first
-// in-chunk read coefficients s_c1 (f32 [64][KP]), values s_v[64][CW], denominators s_den[64], fade powers pw[68].
-__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW) {
+// cnt[M], the writer masks of the current chunk wmask[M] (bit q: position q of the chunk writes the location);
+// u16 [64][KP] arrays: picks s_iw / s_ir, packed read flags s_qf (first and second earlier in-chunk writer of the
+// read pick, and a bit for "three or more"), write ranks s_rk (earlier in-chunk writers of the write pick's slot);
+// f32 [64][KP]: weights s_ww / s_wr and the two in-chunk read coefficients s_c1 / s_c2; the staged values s_v[64][CW]
+// (VT: bfloat16 inputs are staged exactly as bfloat16), denominators s_den[64], fade powers pw[68], and the
+// largest write rank of the chunk.
+__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int v_bytes) {
   return sizeof(float) * (static_cast<size_t>(M) * CW + pad4(M)) + sizeof(unsigned long long) * pad4(M) +
-         sizeof(uint16_t) * 4 * kChunk * KP + sizeof(float) * 3 * kChunk * KP + sizeof(float) * kChunk * CW +
-         sizeof(float) * (kChunk + 68);
+         sizeof(uint16_t) * 4 * kChunk * KP + sizeof(float) * 4 * kChunk * KP +
+         static_cast<size_t>(v_bytes) * kChunk * CW + sizeof(float) * (kChunk + 68) + 16;
 }
 
 // The KP picks of one position: slot ids (16-bit) and weights, loaded with 128-bit LDS reads.
@@ -292,6 +296,32 @@ __device__ __forceinline__ void load_picks(const uint16_t* sl, const float* wt, 
   }
 }
 
+template <int KP>
+__device__ __forceinline__ void load_u16(const uint16_t* sl, int (&m)[KP]) {
+#pragma unroll
+  for (int g = 0; g < KP / 8; ++g) {
+    const uint4 v = *reinterpret_cast<const uint4*>(sl + 8 * g);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m[8 * g + 2 * e] = static_cast<int>(u[e] & 0xffffu);
+      m[8 * g + 2 * e + 1] = static_cast<int>(u[e] >> 16);
+    }
+  }
+}
+
+template <int KP>
+__device__ __forceinline__ void load_f32(const float* wt, float (&w)[KP]) {
+#pragma unroll
+  for (int g = 0; g < KP / 4; ++g) {
+    const float4 v = *reinterpret_cast<const float4*>(wt + 4 * g);
+    w[4 * g] = v.x;
+    w[4 * g + 1] = v.y;
+    w[4 * g + 2] = v.z;
+    w[4 * g + 3] = v.w;
+  }
+}
+
 // Weight with which position q (its KP slot ids sl and weights wt, the first kk live) wrote slot m (a position
 // writes a slot at most once; 0 when it did not).
 template <int KP>
@@ -305,7 +335,7 @@ __device__ __forceinline__ float writer_weight(const uint16_t* sl, const float* 
   return r;
 }
 
-// CPL consecutive floats (CPL = 4, 2, 1) of LDS, one vector access
+// CPL consecutive floats (CPL = 4, 2, 1) of LDS, one vector access; the bfloat16 variant converts.
 template <int CPL>
 struct Seg {
   float v[CPL];
@@ -321,6 +351,21 @@ __device__ __forceinline__ Seg<CPL> lds_seg(const float* p) {
     r.v[0] = t.x; r.v[1] = t.y;
   } else {
     r.v[0] = *p;
+  }
+  return r;
+}
+template <int CPL>
+__device__ __forceinline__ Seg<CPL> lds_seg(const bf16_t* p) {
+  Seg<CPL> r;
+  if constexpr (CPL == 4) {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    r.v[0] = __uint_as_float(t.x << 16); r.v[1] = __uint_as_float(t.x & 0xffff0000u);
+    r.v[2] = __uint_as_float(t.y << 16); r.v[3] = __uint_as_float(t.y & 0xffff0000u);
+  } else if constexpr (CPL == 2) {
+    const uint32_t t = *reinterpret_cast<const uint32_t*>(p);
+    r.v[0] = __uint_as_float(t << 16); r.v[1] = __uint_as_float(t & 0xffff0000u);
+  } else {
+    r.v[0] = to_f32(*p);
   }
   return r;
 }
@@ -353,19 +398,27 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// Workgroup barrier that orders LDS accesses only: the scan shares nothing else between its threads, so global loads
+// issued ahead (the next chunk's picks) and global stores (read-outs) need not complete at every barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Scan of one (batch row, head) slab over CW of its value columns, 512 threads = 64 positions x 8 lanes.
 // Per chunk of up to 64 positions, separated by barriers:
-//   P1 stage   lane (position, pick): the chunk's picks and weights, and CW/8 value columns, into LDS; the previous
-//              chunk's writer marks made from the same entries are cleared first
+//   P1 stage   lane (position, pick): the chunk's picks and weights (loaded one chunk ahead) and CW/8 value columns
+//              into LDS; first the previous chunk's writer marks made from the same entries are cleared
 //   P2 mark    each write (q, j) sets bit q of wmask[slot]
-//   P3 control lane (position, pick): the read pick's S_in count term and its earlier in-chunk writers (bits below
-//              the position in wmask; the first one's coefficient is kept, more are flagged), the position's
-//              denominator (summed over its 8 lanes), and for the write pick whether this position is the slot's
-//              lowest writer (its owner) and whether other positions write it too
+//   P3 control lane (position, pick): the read pick's S_in count term, its first two earlier in-chunk writers and
+//              their coefficients (a flag for more), the position's denominator (summed over its 8 lanes), and the
+//              write pick's rank = number of earlier in-chunk writers of its slot
 //   P4 read    lane (position, segment of CW/8 columns): mu * lam^p * S_in rows of the picks plus the in-chunk
 //              writes, divided by the denominator
-//   P5 write   the owner of each written slot adds every writer's faded value to the slot's row (one read-modify-
-//              write per lane and row: no LDS float atomics, no two threads on one row)
+//   P5 write   in rounds r = 0, 1, ...: the writes of rank r add their faded value to their slot's row with one
+//              128-bit read-modify-write per lane (no two writes of a round share a slot; no LDS float atomics)
 // All sums are over fixed orders, so results are deterministic.
 template <int CW, int KP, typename VT, typename OutT>
 __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
@@ -379,13 +432,15 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   uint16_t* s_iw = reinterpret_cast<uint16_t*>(wmask + pad4(M));
   uint16_t* s_ir = s_iw + kChunk * KP;
   uint16_t* s_qf = s_ir + kChunk * KP;
-  uint16_t* s_wf = s_qf + kChunk * KP;
-  float* s_ww = reinterpret_cast<float*>(s_wf + kChunk * KP);
+  uint16_t* s_rk = s_qf + kChunk * KP;
+  float* s_ww = reinterpret_cast<float*>(s_rk + kChunk * KP);
   float* s_wr = s_ww + kChunk * KP;
   float* s_c1 = s_wr + kChunk * KP;
-  float* s_v = s_c1 + kChunk * KP;
-  float* s_den = s_v + kChunk * CW;
+  float* s_c2 = s_c1 + kChunk * KP;
+  VT* s_v = reinterpret_cast<VT*>(s_c2 + kChunk * KP);
+  float* s_den = reinterpret_cast<float*>(s_v + kChunk * CW);
   float* pw = s_den + kChunk;
+  int* s_maxrank = reinterpret_cast<int*>(pw + 68);
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
@@ -413,7 +468,30 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     pw[tid] = v;
   }
   float mu = 1.f;
-  float vreg[CPL];
+
+  // this lane's picks (control role) and value columns (data role) of the next chunk, loaded one chunk ahead
+  int n_iw[G], n_ir[G];
+  float n_ww[G], n_wr[G];
+  VT n_v[CPL];
+  auto fetch = [&](int c0) {
+    if (p < min(kChunk, a.T - c0)) {
+      const int64_t pb = (slab * a.T + c0 + p) * KP;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int j = l8 + 8 * g;
+        n_iw[g] = a.idx_w[pb + j];
+        n_ir[g] = a.idx_r[pb + j];
+        n_ww[g] = a.w_w[pb + j];
+        n_wr[g] = a.w_r[pb + j];
+      }
+      const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + c0 + p) * a.v_stride +
+                       static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) n_v[c] = vrow[c];
+    }
+  };
+  fetch(0);
+  lds_barrier();
 
   for (int c0 = 0; c0 < a.T; c0 += kChunk) {
     const int L = min(kChunk, a.T - c0);
@@ -421,6 +499,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     const int64_t row = static_cast<int64_t>(b) * a.T + c0 + p;
     int iw[G], ir[G];
     float ww[G], wr[G];
+    float vreg[CPL];
     // P1: clear the previous chunk's marks made from this lane's entries, then stage
     if (c0 > 0) {
 #pragma unroll
@@ -429,81 +508,97 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         if (j < kk) wmask[s_iw[p * KP + j]] = 0ull;
       }
     }
+    if (tid == 0) *s_maxrank = 0;
     if (active) {
-      const int64_t pb = (slab * a.T + c0 + p) * KP;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int j = l8 + 8 * g;
-        iw[g] = a.idx_w[pb + j];
-        ir[g] = a.idx_r[pb + j];
-        ww[g] = a.w_w[pb + j];
-        wr[g] = a.w_r[pb + j];
+        iw[g] = n_iw[g];
+        ir[g] = n_ir[g];
+        ww[g] = n_ww[g];
+        wr[g] = n_wr[g];
         s_iw[p * KP + j] = static_cast<uint16_t>(iw[g]);
         s_ir[p * KP + j] = static_cast<uint16_t>(ir[g]);
         s_ww[p * KP + j] = ww[g];
         s_wr[p * KP + j] = wr[g];
       }
-      const VT* vrow = static_cast<const VT*>(a.v) + row * a.v_stride + static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
-        vreg[c] = to_f32(vrow[c]);
-        s_v[p * CW + CPL * l8 + c] = vreg[c];
+        vreg[c] = to_f32(n_v[c]);
+        s_v[p * CW + CPL * l8 + c] = n_v[c];
       }
     }
-    __syncthreads();
-    // P2: mark
+    lds_barrier();
+    // P2: mark; then start loading the next chunk
     if (active) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
         if (l8 + 8 * g < kk) atomicOr(&wmask[iw[g]], 1ull << p);
     }
-    __syncthreads();
+    if (c0 + kChunk < a.T) fetch(c0 + kChunk);
+    lds_barrier();
     // P3: control
     if (active) {
       const float fin = mu * pw[p];
       const unsigned long long below = (1ull << p) - 1ull;
       float dpart = 0.f;
+      int myrank = 0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int i = l8 + 8 * g;
-        uint16_t qf = 0xff, wf = 0;
-        float c1 = 0.f;
+        uint32_t qf = kNoQ | (kNoQ << 7);
+        uint16_t rk = 0;
+        float c1 = 0.f, c2 = 0.f;
         if (i < kk) {
           const int m = ir[g];
           const float w = wr[g];
           dpart = fmaf(w * fin, cnt[m], dpart);
           unsigned long long mk = wmask[m] & below;
           if (mk) {
-            const int q = __builtin_ctzll(mk);
-            c1 = w * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m, kk) * pw[p - 1 - q];
-            dpart += c1;
-            qf = static_cast<uint16_t>(q);
+            const int q1 = __builtin_ctzll(mk);
             mk &= mk - 1ull;
-            if (mk) qf |= 0x100;
-            while (mk) {
-              const int q2 = __builtin_ctzll(mk);
+            const int q2 = mk ? __builtin_ctzll(mk) : q1;
+            const float w1 = writer_weight<KP>(s_iw + q1 * KP, s_ww + q1 * KP, m, kk);
+            const float w2 = writer_weight<KP>(s_iw + q2 * KP, s_ww + q2 * KP, m, kk);
+            c1 = w * w1 * pw[p - 1 - q1];
+            dpart += c1;
+            qf = q1 | (kNoQ << 7);
+            if (mk) {
+              c2 = w * w2 * pw[p - 1 - q2];
+              dpart += c2;
+              qf = q1 | (q2 << 7);
               mk &= mk - 1ull;
-              dpart += w * writer_weight<KP>(s_iw + q2 * KP, s_ww + q2 * KP, m, kk) * pw[p - 1 - q2];
+              if (mk) qf |= 1u << 14;
+              while (mk) {   // three or more earlier writers: the rest only enters the denominator here
+                const int q = __builtin_ctzll(mk);
+                mk &= mk - 1ull;
+                dpart += w * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m, kk) * pw[p - 1 - q];
+              }
             }
           }
-          const unsigned long long mm = wmask[iw[g]];
-          if (__builtin_ctzll(mm) == p) wf = (mm & (mm - 1ull)) ? 3 : 1;
+          const unsigned long long mm = wmask[iw[g]] & below;
+          rk = static_cast<uint16_t>(__builtin_popcountll(mm));
+          myrank = max(myrank, static_cast<int>(rk));
         }
-        s_qf[p * KP + i] = qf;
+        s_qf[p * KP + i] = static_cast<uint16_t>(qf);
         s_c1[p * KP + i] = c1;
-        s_wf[p * KP + i] = wf;
+        s_c2[p * KP + i] = c2;
+        s_rk[p * KP + i] = rk;
       }
       dpart = sum8(dpart);
       if (l8 == 0) s_den[p] = dpart;
+      if (myrank > 0) atomicMax(s_maxrank, myrank);
     }
-    __syncthreads();
+    lds_barrier();
     // P4: read
     if (active) {
       const float fin = mu * pw[p];
       int m[KP], qfl[KP];
-      float w[KP], c1[KP];
+      float w[KP], c1[KP], c2[KP];
       load_picks<KP>(s_ir + p * KP, s_wr + p * KP, m, w);
-      load_picks<KP>(s_qf + p * KP, s_c1 + p * KP, qfl, c1);
+      load_u16<KP>(s_qf + p * KP, qfl);
+      load_f32<KP>(s_c1 + p * KP, c1);
+      load_f32<KP>(s_c2 + p * KP, c2);
       float acc[CPL];
 #pragma unroll
       for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
@@ -517,78 +612,87 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       for (int c = 0; c < CPL; ++c) acc[c] *= fin;
 #pragma unroll
       for (int i = 0; i < KP; ++i) {
-        if ((qfl[i] & 0xff) == 0xff) continue;
-        const Seg<CPL> vq = lds_seg<CPL>(&s_v[(qfl[i] & 0xff) * CW + CPL * l8]);
+        const int q1 = qfl[i] & kNoQ;
+        const int q2 = (qfl[i] >> 7) & kNoQ;
+        if (q1 != kNoQ) {
+          const Seg<CPL> v1 = lds_seg<CPL>(&s_v[q1 * CW + CPL * l8]);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c1[i], vq.v[c], acc[c]);
-        if (qfl[i] & 0x100) {   // more earlier writers of this slot in the chunk
-          unsigned long long mk = wmask[m[i]] & ((1ull << p) - 1ull);
+          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c1[i], v1.v[c], acc[c]);
+        }
+        if (q2 != kNoQ) {
+          const Seg<CPL> v2 = lds_seg<CPL>(&s_v[q2 * CW + CPL * l8]);
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c2[i], v2.v[c], acc[c]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {
+        if (!(qfl[i] & (1 << 14))) continue;   // three or more earlier writers (rare)
+        unsigned long long mk = wmask[m[i]] & ((1ull << p) - 1ull);
+        mk &= mk - 1ull;
+        mk &= mk - 1ull;
+        while (mk) {
+          const int q = __builtin_ctzll(mk);
           mk &= mk - 1ull;
-          while (mk) {
-            const int q = __builtin_ctzll(mk);
-            mk &= mk - 1ull;
-            const float coef = w[i] * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[i], kk) * pw[p - 1 - q];
-            const Seg<CPL> v2 = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
+          const float coef = w[i] * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[i], kk) * pw[p - 1 - q];
+          const Seg<CPL> vq = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) acc[c] = fmaf(coef, v2.v[c], acc[c]);
-          }
+          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(coef, vq.v[c], acc[c]);
         }
       }
       if (a.read_mean) {
-        const float dv = s_den[p] + a.read_eps;
+        const float inv = 1.f / (s_den[p] + a.read_eps);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] /= dv;
+        for (int c = 0; c < CPL; ++c) acc[c] *= inv;
       }
       store_seg<OutT, CPL>(static_cast<OutT*>(a.r_out) + row * a.r_stride + static_cast<int64_t>(h) * a.dh + col0 +
                                CPL * l8, acc);
     }
-    __syncthreads();
+    lds_barrier();
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
     float mu_new = mu * pw[L];
     if (!(mu_new >= kMuFloor)) {
       for (int i = tid; i < M * CW; i += kScanThreads) A[i] *= mu_new;
       for (int m = tid; m < M; m += kScanThreads) cnt[m] *= mu_new;
       mu_new = 1.f;
-      __syncthreads();
+      lds_barrier();
     }
-    // P5: write
-    if (active) {
-      const float inv_mu = 1.f / mu_new;
-      const float cpos = pw[L - 1 - p] * inv_mu;
-      int m[KP], wfl[KP];
-      float w[KP], unused[KP];
-      load_picks<KP>(s_iw + p * KP, s_ww + p * KP, m, w);
-      load_picks<KP>(s_wf + p * KP, s_ww + p * KP, wfl, unused);
-      Seg<CPL> x[KP];
+    // P5: write, in rounds of equal rank
+    const int maxrank = *s_maxrank;
+    {
+      const float cpos = active ? pw[L - 1 - p] / mu_new : 0.f;
+      int m[KP], rk[KP];
+      float w[KP];
+      if (active) {
+        load_picks<KP>(s_iw + p * KP, s_ww + p * KP, m, w);
+        load_u16<KP>(s_rk + p * KP, rk);
+      }
+      for (int r = 0; r <= maxrank; ++r) {
+        if (active) {
+          Seg<CPL> x[KP];
+          float cc[KP];
 #pragma unroll
-      for (int j = 0; j < KP; ++j)
-        if (wfl[j] & 1) x[j] = lds_seg<CPL>(&A[m[j] * CW + CPL * l8]);
+          for (int j = 0; j < KP; ++j) {
+            if (j < kk && rk[j] == r) {
+              x[j] = lds_seg<CPL>(&A[m[j] * CW + CPL * l8]);
+              if (l8 == 0) cc[j] = cnt[m[j]];
+            }
+          }
 #pragma unroll
-      for (int j = 0; j < KP; ++j) {
-        if (!(wfl[j] & 1)) continue;
-        const float cp = cpos * w[j];
-        float dc = cp;
+          for (int j = 0; j < KP; ++j) {
+            if (j < kk && rk[j] == r) {
+              const float cp = cpos * w[j];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cp, vreg[c], x[j].v[c]);
-        if (wfl[j] & 2) {   // other (later) positions of the chunk write this slot too
-          unsigned long long rest = wmask[m[j]];
-          rest &= rest - 1ull;
-          while (rest) {
-            const int q = __builtin_ctzll(rest);
-            rest &= rest - 1ull;
-            const float cq = pw[L - 1 - q] * inv_mu * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[j], kk);
-            const Seg<CPL> vq = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cq, vq.v[c], x[j].v[c]);
-            dc += cq;
+              for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cp, vreg[c], x[j].v[c]);
+              lds_seg_store<CPL>(&A[m[j] * CW + CPL * l8], x[j]);
+              if (l8 == 0) cnt[m[j]] = cc[j] + cp;
+            }
           }
         }
-        lds_seg_store<CPL>(&A[m[j] * CW + CPL * l8], x[j]);
-        if (l8 == 0) cnt[m[j]] += dc;
+        lds_barrier();
       }
     }
     mu = mu_new;
-    __syncthreads();
   }
 
   if (a.state_out_mem) {
@@ -628,7 +732,7 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
 // ---------------------------------------------------------------------------------------------------------------
 // host side
 struct Plan {
-  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, scan_cw;
+  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap;
   // workspace offsets
   size_t off_knorm, off_iw, off_ir, off_ww, off_wr, off_rtmp, total;
 };
@@ -660,15 +764,7 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   if (p->M > 65535) return set_err(SDM_RT_EUNSUPPORTED, "n_sub^2 = %d locations exceed 65535", p->M);
   p->cap = p->c1 <= 8 && p->kk <= 8 ? 8 : 16;
   p->pitch = (p->kk + 7) / 8 * 8;
-  // widest column group per scan workgroup whose slab fits in LDS
-  p->scan_cw = 0;
-  for (int cw : {32, 16, 8}) {
-    if (p->dh % cw == 0 && scan_lds_bytes(p->M, p->pitch, cw) <= kLdsBytes) {
-      p->scan_cw = cw;
-      break;
-    }
-  }
-  if (p->scan_cw == 0)
+  if (scan_lds_bytes(p->M, p->pitch, 8, sizeof(float)) > kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations do not fit a slab of 8 columns in LDS", p->M);
   const size_t tok = static_cast<size_t>(p->B) * p->T;
   const size_t picks = tok * p->H * p->pitch;
@@ -745,7 +841,7 @@ int launch_address(const Plan& p, const AddrArgs& a, int sets, sdm_rt_dtype dt, 
 
 template <int CW, int KP, typename VT, typename OutT>
 int launch_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  const size_t lds = scan_lds_bytes(p.M, KP, CW);
+  const size_t lds = scan_lds_bytes(p.M, KP, CW, sizeof(VT));
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<CW, KP, VT, OutT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(kLdsBytes));
@@ -760,12 +856,21 @@ int launch_scan_k(const Plan& p, const ScanArgs& a, hipStream_t st) {
   return p.pitch == 8 ? launch_scan_t<CW, 8, VT, OutT>(p, a, st) : launch_scan_t<CW, 16, VT, OutT>(p, a, st);
 }
 
+// widest column group per scan workgroup (32, 16 or 8 value columns) whose slab and staging fit in LDS
+template <typename VT>
+int scan_columns(const Plan& p) {
+  for (int cw : {32, 16, 8})
+    if (p.dh % cw == 0 && scan_lds_bytes(p.M, p.pitch, cw, sizeof(VT)) <= kLdsBytes) return cw;
+  return 0;
+}
+
 template <typename VT, typename OutT>
 int launch_scan_v(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  switch (p.scan_cw) {
+  switch (scan_columns<VT>(p)) {
     case 32: return launch_scan_k<32, VT, OutT>(p, a, st);
     case 16: return launch_scan_k<16, VT, OutT>(p, a, st);
-    default: return launch_scan_k<8, VT, OutT>(p, a, st);
+    case 8: return launch_scan_k<8, VT, OutT>(p, a, st);
+    default: return set_err(SDM_RT_EUNSUPPORTED, "no scan column group fits in LDS");
   }
 }
 
