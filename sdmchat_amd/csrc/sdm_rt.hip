@@ -1,15 +1,16 @@
 // sdm_rt.hip -- HIP kernels for gfx950 and the C ABI declared in include/sdm_rt.h.
 //
-// Kernels (one forward = keynorm, address x2 address sets, scan, finish):
-//   keynorm_kernel   unit-normalise every sub-key once per call (F.normalize of keys, track4_onesdm_models.py:137-140)
-//   address_kernel   per (token, head, address set): unit halves, scores against the n_sub unit sub-keys, exact
-//                    top-c1 per half, exact top-kk of the dominance-pruned c1 x c1 grid, softmax weights, gate
-//                    (pk_address :134-148, prepare :203-207)
-//   scan_kernel      per (batch row, head, group of 8 value columns): the memory slab of M x 8 float32 columns
-//                    plus the M write counts lives in LDS for the whole sequence; positions are processed 64 at
-//                    a time (one per lane): read the carried state, add the in-chunk earlier writes found through
-//                    per-location lists, then fold the chunk's faded writes into the slab (_chunk :215-241)
-//   finish_kernel    per (token, head): r * rsqrt(mean(r^2) + eps) * onorm_w (finish :243-246)
+// One forward is four launches:
+//   keynorm_kernel  unit-normalise every sub-key once per call (F.normalize of keys, track4_onesdm_models.py:137-140)
+//   plan_kernel     per (chunk of 64 positions, head, batch row): product-key addressing of the chunk's write keys
+//                   and read queries (pk_address :134-148; softmax weights and gate, prepare :203-207), then the
+//                   chunk's plan: which earlier positions of the chunk each read sees (with their faded
+//                   coefficients) and, for every location the chunk writes, the list of its writers
+//   scan_kernel     per (batch row, head, group of CW value columns): the memory slab of M x CW float32 values plus
+//                   the M write counts stays in LDS for the whole sequence; each chunk reads the carried state and
+//                   the in-chunk writes its plan lists, then adds the chunk's faded writes (_chunk :215-241)
+//   finish_kernel   per (token, head): r * rsqrt(mean(r^2) + eps) * onorm_w (finish :243-246)
+// address_kernel runs the addressing alone for sdm_rt_address.
 //
 // Decay bookkeeping in scan_kernel: the slab holds A with the true state S = mu * A (mu a per-slab scalar).  A chunk
 // of L positions reads mu * lam^p * A[slot] at offset p, then mu <- mu * lam^L and each write at offset q adds
@@ -69,6 +70,8 @@ __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
 }
 
 constexpr float kMuFloor = 8.673617379884035e-19f;  // 2^-60
+constexpr int kChunk = 64;                          // positions per chunk (one bit each in the writer masks)
+constexpr size_t kLdsBytes = 160 * 1024;            // LDS per workgroup on gfx950
 
 // ---------------------------------------------------------------------------------------------------------------
 // keynorm: out[s][:] = keys[s][:] / max(||keys[s]||, 1e-12) for the 2 * H * n_sub sub-keys
@@ -85,6 +88,8 @@ __global__ void keynorm_kernel(const float* __restrict__ keys1, const float* __r
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// addressing of one (token, head, address set)
+
 // sorted top list in registers: v[0] >= v[1] >= ...; an incoming value moves ahead of an entry only when strictly
 // greater, so among equal values the one inserted first (the lower index, as candidates arrive in index order)
 // stays ahead.  Only the first `cnt` entries are live.
@@ -106,42 +111,29 @@ __device__ __forceinline__ void top_insert(float (&v)[CAP], int (&ix)[CAP], floa
   }
 }
 
-struct AddrArgs {
-  const void* z[2];           // address rows of the two sets (0: write keys, 1: read queries)
-  int64_t z_stride[2];
-  const void* g;              // gate logit rows or nullptr (applies to set 0 only)
-  int64_t g_stride;
-  const float* gate_bias;     // [H] or nullptr
-  const float* knorm;         // [2][H][n_sub][half] unit sub-keys
-  const float* addr_b;        // [H][d_a] or nullptr
-  const float* log_scale;     // [H]
-  int B, T, H, n_sub, c1, kk, pitch;
-  // outputs, layout [B][H][T][pitch] per set
-  uint16_t* idx16[2];
-  int32_t* idx32[2];
-  float* w_out[2];
-  float* s_out[2];
+struct AddrGeom {
+  const float* knorm;      // [2][H][n_sub][half] unit sub-keys
+  const float* addr_b;     // [H][d_a] or nullptr
+  const float* log_scale;  // [H]
+  const float* gate_bias;  // [H] or nullptr
+  int H, n_sub, c1, kk;
 };
 
-// One thread per (token, head, set).  Grid: x = token tiles of 64, y = head, z = set.  Block = one wave, so the
-// head and set are uniform and the sub-key reads are scalar loads.
+// Picks of one address (pk_address, track4_onesdm_models.py:134-148): z (2*HALF values of type InT, plus addr_b)
+// split in two unit halves, each scored against the n_sub unit sub-keys of its half, exact top-c1 per half, exact
+// top-kk of the dominance-pruned c1 x c1 grid of mean scores, slot = i1 * n_sub + i2; weights
+// softmax(exp(log_scale) * score) (prepare :203-206) times `gate`.  Pad entries (>= kk): slot 0, weight 0, score 0.
+// kn: the head's unit sub-keys, [2][n_sub][HALF] (staged in LDS by the caller).
 template <int HALF, int CAP, typename InT>
-__global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
-  const int set = blockIdx.z;
-  const int h = blockIdx.y;
-  const int64_t N = static_cast<int64_t>(a.B) * a.T;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-  if (a.z[set] == nullptr || n >= N) return;
+__device__ __forceinline__ void address_one(const AddrGeom& g, int h, const float* kn, const InT* zrow, float gate,
+                                            int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
   constexpr int DA = 2 * HALF;
-
-  const InT* zrow = static_cast<const InT*>(a.z[set]) + n * a.z_stride[set] + static_cast<int64_t>(h) * DA;
   float z[DA];
 #pragma unroll
   for (int d = 0; d < DA; ++d) {
-    const float bias = a.addr_b ? a.addr_b[h * DA + d] : 0.f;
+    const float bias = g.addr_b ? g.addr_b[h * DA + d] : 0.f;
     z[d] = to_f32(zrow[d]) + bias;
   }
-
   float hv[2][CAP];
   int hi[2][CAP];
 #pragma unroll
@@ -158,15 +150,14 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
       hv[part][p] = -INFINITY;
       hi[part][p] = 0;
     }
-    const float* kb = a.knorm + (static_cast<int64_t>(part) * a.H + h) * a.n_sub * HALF;
-    for (int s = 0; s < a.n_sub; ++s) {
+    const float* kb = kn + part * g.n_sub * HALF;
+    for (int s = 0; s < g.n_sub; ++s) {
       float acc = 0.f;
 #pragma unroll
       for (int d = 0; d < HALF; ++d) acc = fmaf(u[d], kb[s * HALF + d], acc);
-      top_insert<CAP>(hv[part], hi[part], acc, s, a.c1);
+      top_insert<CAP>(hv[part], hi[part], acc, s, g.c1);
     }
   }
-
   // Combine: (a, b) can be among the kk best only when fewer than kk pairs dominate it, i.e. (a+1)(b+1) <= kk
   // (a dominating pair has a score >= and a lower flat index a * c1 + b).
   float cv[CAP];
@@ -178,164 +169,606 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   }
 #pragma unroll
   for (int ra = 0; ra < CAP; ++ra) {
-    if (ra < a.c1) {
+    if (ra < g.c1) {
 #pragma unroll
       for (int rb = 0; rb < CAP; ++rb) {
-        if (rb < a.c1 && (ra + 1) * (rb + 1) <= a.kk) {
+        if (rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk) {
           const float s = (hv[0][ra] + hv[1][rb]) * 0.5f;
-          top_insert<CAP>(cv, ci, s, ra * a.c1 + rb, a.kk);
+          top_insert<CAP>(cv, ci, s, ra * g.c1 + rb, g.kk);
         }
       }
     }
   }
-
-  // softmax(exp(log_scale) * score) over the kk picks; the first pick holds the maximum
-  const float scale = expf(a.log_scale[h]);
+  // softmax over the kk picks; the first pick holds the maximum
+  const float scale = expf(g.log_scale[h]);
   float e[CAP];
   const float x0 = cv[0] * scale;
   float sum = 0.f;
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
-    e[p] = (p < a.kk) ? expf(cv[p] * scale - x0) : 0.f;
+    e[p] = (p < g.kk) ? expf(cv[p] * scale - x0) : 0.f;
     sum += e[p];
   }
-  float gate = 1.f;
-  if (set == 0 && a.g != nullptr) {
-    const InT* grow = static_cast<const InT*>(a.g) + n * a.g_stride;
-    const float logit = to_f32(grow[h]) + (a.gate_bias ? a.gate_bias[h] : 0.f);
-    gate = 1.f / (1.f + expf(-logit));
+#pragma unroll
+  for (int p = 0; p < CAP; ++p) {
+    const bool live = p < g.kk;
+    int sl = 0;
+    if (live) {
+      const int ra = ci[p] / g.c1;
+      const int rb = ci[p] - ra * g.c1;
+      int i1 = 0, i2 = 0;
+#pragma unroll
+      for (int q = 0; q < CAP; ++q) {
+        if (q == ra) i1 = hi[0][q];
+        if (q == rb) i2 = hi[1][q];
+      }
+      sl = i1 * g.n_sub + i2;
+    }
+    slot[p] = sl;
+    w[p] = live ? e[p] / sum * gate : 0.f;
+    score[p] = live ? cv[p] : 0.f;
   }
+}
 
+template <typename InT>
+__device__ __forceinline__ float gate_of(const InT* grow, int h, const float* gate_bias) {
+  const float logit = to_f32(grow[h]) + (gate_bias ? gate_bias[h] : 0.f);
+  return 1.f / (1.f + expf(-logit));
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// addressing of 64 addresses by one wave on the matrix cores (n_sub <= 32, half width HALF = 2 * S, S in {4, 8, 16})
+//
+// The scores of one half form the 32 x 64 product of the zero-padded unit sub-keys and the 64 unit address halves:
+// two 32 x 32 tiles of v_mfma_f32_32x32x2f32 accumulated over S steps.  Lane l feeds sub-key row l % 32 and address
+// column l % 32 of a tile, with dims (l / 32) * S + s at step s.  Lane l's output covers address l % 32 of the tile
+// and sub-keys 8 * (r / 4) + 4 * (l / 32) + r % 4 (r < 16); one permlane32 swap per output register leaves lane l
+// with all 32 sub-key scores of address l.  Selection then runs per lane on f64 keys with bitonic networks.
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// f64 selection key: plain double order = (score descending, then lower index first).  A float converted to double
+// has 29 zero low mantissa bits; the index goes there (index for negative scores, idx_max - index otherwise, so the
+// lower index is the larger key).  Zero scores map to (idx_max - index) * 2^-1000, between every negative and every
+// positive score, so no key is a denormal or -0.
+__device__ __forceinline__ double sel_key(float s, int idx, int idx_max) {
+  if (s == 0.f) return static_cast<double>(idx_max - idx) * 0x1p-1000;
+  const unsigned long long low =
+      s > 0.f ? static_cast<unsigned long long>(idx_max - idx) : static_cast<unsigned long long>(idx);
+  return __longlong_as_double(__double_as_longlong(static_cast<double>(s)) | low);
+}
+__device__ __forceinline__ void sel_decode(double k, int idx_max, float& s, int& idx) {
+  if (fabs(k) < 0x1p-900) {
+    s = 0.f;
+    idx = idx_max - static_cast<int>(k * 0x1p1000);
+    return;
+  }
+  const unsigned long long bits = __double_as_longlong(k);
+  const int low = static_cast<int>(bits & 0xffull);   // idx_max <= 255
+  idx = k > 0.0 ? idx_max - low : low;
+  s = static_cast<float>(__longlong_as_double(bits & ~0x1fffffffull));
+}
+
+// compare-exchange networks on f64 keys, descending
+template <int N>
+__device__ __forceinline__ void bitonic_sort_desc(double* v) {
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const double x = v[i], y = v[l];
+          if ((i & k) == 0) {
+            v[i] = fmax(x, y);
+            v[l] = fmin(x, y);
+          } else {
+            v[i] = fmin(x, y);
+            v[l] = fmax(x, y);
+          }
+        }
+      }
+    }
+  }
+}
+// a, b sorted descending -> a = the N largest of both, sorted descending
+template <int N>
+__device__ __forceinline__ void merge_top_desc(double* a, const double* b) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = fmax(a[i], b[N - 1 - i]);   // bitonic
+#pragma unroll
+  for (int j = N >> 1; j > 0; j >>= 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int l = i ^ j;
+      if (l > i) {
+        const double x = a[i], y = a[l];
+        a[i] = fmax(x, y);
+        a[l] = fmin(x, y);
+      }
+    }
+  }
+}
+// the K largest of c[0..N) (N a multiple of K) -> c[0..K), sorted descending
+template <int K, int N>
+__device__ __forceinline__ void top_k_desc(double (&c)[N]) {
+#pragma unroll
+  for (int g = 0; g < N / K; ++g) bitonic_sort_desc<K>(c + g * K);
+#pragma unroll
+  for (int g = 1; g < N / K; ++g) merge_top_desc<K>(c, c + g * K);
+}
+
+// n values of type InT from p into floats: 16-byte loads when p is 16-byte aligned, element loads otherwise
+template <int n, typename InT>
+__device__ __forceinline__ void load_vals(const InT* p, float (&out)[n]) {
+  constexpr int kBytes = n * static_cast<int>(sizeof(InT));
+  if constexpr (kBytes % 16 == 0) {
+    if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+#pragma unroll
+      for (int q = 0; q < kBytes / 16; ++q) {
+        const uint4 u = reinterpret_cast<const uint4*>(p)[q];
+        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (sizeof(InT) == 2) {
+            out[8 * q + 2 * e] = __uint_as_float(wd[e] << 16);
+            out[8 * q + 2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+          } else {
+            out[4 * q + e] = __uint_as_float(wd[e]);
+          }
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < n; ++s) out[s] = to_f32(p[s]);
+}
+
+// number of grid pairs (a, b), a, b < CAP, with (a+1)(b+1) <= CAP: the candidates of the top-CAP combine
+__host__ __device__ constexpr int n_pairs(int cap) {
+  int n = 0;
+  for (int a = 0; a < cap; ++a)
+    for (int b = 0; b < cap; ++b)
+      if ((a + 1) * (b + 1) <= cap) ++n;
+  return n;
+}
+
+// Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
+// clamped; their lanes' outputs are unspecified), same results as address_one up to float rounding of the scores.
+// All 64 lanes of the wave must call it.
+template <int S, int CAP, typename InT>
+__device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
+                                             float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
+  constexpr int HALF = 2 * S;
+  const int l = threadIdx.x & 63;
+  const int kb = l >> 5, jl = l & 31;
+  float hv[2][CAP];
+  int hx[2][CAP];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    float ka[S];
+    load_vals<S, float>(g.knorm + ((static_cast<int64_t>(hf) * g.H + h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S,
+                        ka);
+    if (jl >= g.n_sub) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) ka[s] = 0.f;
+    }
+    floatx16 acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = min(32 * t + jl, rows - 1);
+      float zb[S];
+      load_vals<S, InT>(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + hf * HALF + kb * S, zb);
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (g.addr_b) zb[s] += g.addr_b[h * 2 * HALF + hf * HALF + kb * S + s];
+        ss = fmaf(zb[s], zb[s], ss);
+      }
+      const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);   // dims of both lane halves, same order in both
+      const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+      acc[t] = floatx16{};
+#pragma unroll
+      for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[s] * inv, acc[t], 0, 0, 0);
+    }
+    double c[32];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]), false,
+                                                       false);
+      const int i0 = 8 * (r / 4) + (r % 4);
+      c[r] = i0 < g.n_sub ? sel_key(__uint_as_float(sw[0]), i0, 31) : -INFINITY;
+      c[16 + r] = i0 + 4 < g.n_sub ? sel_key(__uint_as_float(sw[1]), i0 + 4, 31) : -INFINITY;
+    }
+    top_k_desc<CAP, 32>(c);
+#pragma unroll
+    for (int r = 0; r < CAP; ++r) sel_decode(c[r], 31, hv[hf][r], hx[hf][r]);
+  }
+  // combine over the dominance-pruned grid (see address_one)
+  constexpr int NP = n_pairs(CAP);
+  constexpr int NPAD = (NP + CAP - 1) / CAP * CAP;
+  double pc[NPAD];
+  {
+    int n = 0;
+#pragma unroll
+    for (int ra = 0; ra < CAP; ++ra) {
+#pragma unroll
+      for (int rb = 0; rb < CAP; ++rb) {
+        if ((ra + 1) * (rb + 1) <= CAP) {
+          const bool ok = ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk;
+          pc[n++] = ok ? sel_key((hv[0][ra] + hv[1][rb]) * 0.5f, ra * g.c1 + rb, 255) : -INFINITY;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = NP; i < NPAD; ++i) pc[i] = -INFINITY;
+  }
+  top_k_desc<CAP, NPAD>(pc);
+  float cv[CAP];
+  int ci[CAP];
+#pragma unroll
+  for (int p = 0; p < CAP; ++p) sel_decode(pc[p], 255, cv[p], ci[p]);
+  const float scale = expf(g.log_scale[h]);
+  float e[CAP];
+  const float x0 = cv[0] * scale;
+  float sum = 0.f;
+#pragma unroll
+  for (int p = 0; p < CAP; ++p) {
+    e[p] = (p < g.kk) ? expf(cv[p] * scale - x0) : 0.f;
+    sum += e[p];
+  }
+#pragma unroll
+  for (int p = 0; p < CAP; ++p) {
+    const bool live = p < g.kk;
+    int sl = 0;
+    if (live) {
+      const int ra = ci[p] / g.c1;
+      const int rb = ci[p] - ra * g.c1;
+      int i1 = 0, i2 = 0;
+#pragma unroll
+      for (int q = 0; q < CAP; ++q) {
+        if (q == ra) i1 = hx[0][q];
+        if (q == rb) i2 = hx[1][q];
+      }
+      sl = i1 * g.n_sub + i2;
+    }
+    slot[p] = sl;
+    w[p] = live ? e[p] / sum * gate : 0.f;
+    score[p] = live ? cv[p] : 0.f;
+  }
+}
+
+struct AddrArgs {
+  AddrGeom g;
+  const void* z;              // address rows
+  int64_t z_stride;
+  const void* gl;             // gate logit rows or nullptr
+  int64_t g_stride;
+  int B, T, pitch;
+  int32_t* slot_out;          // [B][H][T][pitch]
+  float* w_out;
+  float* s_out;
+};
+
+// Copy head h's unit sub-keys of both halves ([2][n_sub][HALF] floats) into LDS.
+template <int HALF>
+__device__ __forceinline__ void stage_keys(const AddrGeom& g, int h, float* kn, int tid, int nthreads) {
+  const int per_half = g.n_sub * HALF;
+  for (int i = tid; i < 2 * per_half; i += nthreads) {
+    const int part = i >= per_half;
+    kn[i] = g.knorm[(static_cast<int64_t>(part) * g.H + h) * per_half + (i - part * per_half)];
+  }
+}
+
+// sdm_rt_address: one thread per (token, head).  Grid: x = token tiles of 64, y = head.  MF: the tile is addressed
+// by the wave on the matrix cores (address_wave), else per thread with the sub-keys staged in LDS (address_one).
+template <int HALF, int CAP, typename InT, bool MF>
+__global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
+  extern __shared__ float kn[];   // [2][n_sub][HALF] (per-thread path)
+  const int h = blockIdx.y;
+  const int64_t N = static_cast<int64_t>(a.B) * a.T;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t n = n0 + threadIdx.x;
+  const float gate =
+      (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
+  int slot[CAP];
+  float w[CAP], sc[CAP];
+  if constexpr (MF) {
+    address_wave<HALF / 2, CAP, InT>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
+                                     static_cast<int>(min<int64_t>(64, N - n0)), gate, slot, w, sc);
+    if (n >= N) return;
+  } else {
+    stage_keys<HALF>(a.g, h, kn, threadIdx.x, 64);
+    __syncthreads();
+    if (n >= N) return;
+    const InT* zrow = static_cast<const InT*>(a.z) + n * a.z_stride + static_cast<int64_t>(h) * 2 * HALF;
+    address_one<HALF, CAP, InT>(a.g, h, kn, zrow, gate, slot, w, sc);
+  }
   const int b = static_cast<int>(n / a.T);
   const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
-  const int64_t base = ((static_cast<int64_t>(b) * a.H + h) * a.T + t) * a.pitch;
+  const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
     if (p < a.pitch) {
-      const bool live = p < a.kk;
-      int slot = -1;
-      if (live) {
-        const int ra = ci[p] / a.c1;
-        const int rb = ci[p] - ra * a.c1;
-        int i1 = 0, i2 = 0;
-#pragma unroll
-        for (int q = 0; q < CAP; ++q) {
-          if (q == ra) i1 = hi[0][q];
-          if (q == rb) i2 = hi[1][q];
-        }
-        slot = i1 * a.n_sub + i2;
-      }
-      if (a.idx16[set]) a.idx16[set][base + p] = static_cast<uint16_t>(live ? slot : 0);
-      if (a.idx32[set]) a.idx32[set][base + p] = slot;
-      if (a.w_out[set]) a.w_out[set][base + p] = live ? e[p] / sum * gate : 0.f;
-      if (a.s_out[set]) a.s_out[set][base + p] = live ? cv[p] : 0.f;
+      const bool live = p < a.g.kk;
+      a.slot_out[base + p] = live ? slot[p] : -1;
+      if (a.w_out) a.w_out[base + p] = w[p];
+      if (a.s_out) a.s_out[base + p] = sc[p];
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// scan
-struct ScanArgs {
-  const uint16_t* idx_w;   // [B][H][T][KP]
-  const uint16_t* idx_r;
-  const float* w_w;
-  const float* w_r;
-  const void* v;           // value rows
-  int64_t v_stride;
+// the chunk plan
+//
+// One plan per (batch row, head, chunk) at a fixed stride in the workspace.  The scan reads its fixed-size part
+// straight into registers and stages its variable part into LDS (KP = pick pitch, PR = position record bytes):
+//   pos[64]          per position p: u16 slot[KP], f32 w[KP] (read picks and weights, pads 0), then u16 ri_begin,
+//                    u16 ri_end, f32 csum (the sum of p's in-chunk read coefficients), padding to PR bytes
+//   wrec[64][KP]     write records of 8 bytes; distinct written slot u of the chunk is wrec[u % 64][u / 64] =
+//                    {slot | q0 << 16 | xo << 22, c0 | more << 31}: q0 is the slot's first writer in the chunk and
+//                    c0 = lam^(L-1-q0) * ww its coefficient; when later positions write the slot too (more = 1)
+//                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last
+//   variable part    u32 {n_ri, n_wu, n_ext, bytes}; ext[n_ext] = {c = lam^(L-1-q) * ww, q | last << 31};
+//                    f32 ri_c[n_ri]; u8 ri_q[n_ri]
+// Read contribution e of position p (ri_begin <= e < ri_end): position q = ri_q[e] < p of the chunk wrote some of
+// p's read slots; ri_c[e] = the sum over those slots of wr * ww * lam^(p-1-q).  sizes[] holds the bytes of each
+// plan's variable part.
+struct PlanGeom {
+  int KP;
+  __host__ __device__ constexpr int pos_bytes() const { return (6 * KP + 16 + 15) / 16 * 16; }
+  __host__ __device__ constexpr int off_tail() const { return 6 * KP; }
+  __host__ __device__ constexpr int off_wrec() const { return kChunk * pos_bytes(); }
+  __host__ __device__ constexpr int off_var() const { return off_wrec() + 8 * kChunk * KP; }
+  __host__ __device__ constexpr int max_var() const {
+    return (16 + 8 * kChunk * KP + 5 * (kChunk * (kChunk - 1) / 2) + 15) / 16 * 16;
+  }
+  __host__ __device__ constexpr int stride() const { return (off_var() + max_var() + 255) / 256 * 256; }
+};
+
+struct PlanArgs {
+  AddrGeom g;
+  const void* kz;
+  int64_t kz_stride;
+  const void* qz;
+  int64_t qz_stride;
+  const void* gl;          // gate logit rows or nullptr
+  int64_t g_stride;
   const float* decay;      // [H]
+  unsigned char* plans;    // [B][H][n_chunks][stride]
+  int32_t* sizes;          // [B][H][n_chunks] bytes of each plan's variable part
+  int B, T, M, n_chunks;
+};
+
+// static LDS of plan_kernel (picks, fade powers, totals)
+__host__ __device__ constexpr size_t plan_static_lds(int KP) { return 2 * kChunk * KP * (2 + 4) + 4 * (kChunk + 4) + 16; }
+
+// inclusive prefix sum over the 64 lanes of a wave
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(v, off, 64);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// plan_kernel: block (chunk, head, batch row), 128 threads: wave 0 addresses the write keys of the chunk's positions,
+// wave 1 the read queries (MF: on the matrix cores, else per thread); then the writers of every slot are marked in
+// 64-bit masks, each position's read contributions and each written slot's writer list are found, counted,
+// prefix-summed within the wave and written out.
+template <int HALF, int KP, typename InT, bool MF>
+__global__ void __launch_bounds__(128) plan_kernel(PlanArgs a) {
+  constexpr PlanGeom pg{KP};
+  const int c = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int set = tid >> 6;     // 0: write keys, 1: read queries
+  const int p = tid & 63;
+  const int M = a.M;
+  const int kk = a.g.kk;
+  const int c0 = c * kChunk;
+  const int L = min(kChunk, a.T - c0);
+  const float lam = a.decay[h];
+
+  __shared__ uint16_t pk_slot[2][kChunk][KP];
+  __shared__ float pk_w[2][kChunk][KP];
+  __shared__ float pw[kChunk + 4];
+  __shared__ int tot[4];
+  extern __shared__ unsigned long long wmask[];   // [M], then (per-thread path) the head's sub-keys [2][n_sub][HALF]
+  float* kn = reinterpret_cast<float*>(wmask + M);
+
+  if constexpr (!MF) stage_keys<HALF>(a.g, h, kn, tid, 128);
+  for (int i = tid; i < M; i += 128) wmask[i] = 0ull;
+  if (tid <= kChunk) {
+    float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
+    for (int e = 0; e < tid; ++e) v *= lam;
+    pw[tid] = v;
+  }
+  if constexpr (!MF) __syncthreads();
+
+  // addressing
+  {
+    int slot[KP];
+    float w[KP], sc[KP];
+    const int64_t row0 = static_cast<int64_t>(b) * a.T + c0;
+    const float gate = (set == 0 && a.gl && p < L)
+                           ? gate_of(static_cast<const InT*>(a.gl) + (row0 + p) * a.g_stride, h, a.g.gate_bias)
+                           : 1.f;
+    const InT* zb = static_cast<const InT*>(set == 0 ? a.kz : a.qz);
+    const int64_t zs = set == 0 ? a.kz_stride : a.qz_stride;
+    if constexpr (MF) {
+      address_wave<HALF / 2, KP, InT>(a.g, h, zb + row0 * zs, zs, L, gate, slot, w, sc);
+    } else if (p < L) {
+      address_one<HALF, KP, InT>(a.g, h, kn, zb + (row0 + p) * zs + static_cast<int64_t>(h) * 2 * HALF, gate, slot, w,
+                                 sc);
+    }
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      pk_slot[set][p][j] = p < L ? static_cast<uint16_t>(slot[j]) : 0;
+      pk_w[set][p][j] = p < L ? w[j] : 0.f;
+    }
+  }
+  __syncthreads();
+  // mark the writers of every slot
+  if (set == 0 && p < L) {
+    for (int j = 0; j < kk; ++j) atomicOr(&wmask[pk_slot[0][p][j]], 1ull << p);
+  }
+  __syncthreads();
+  // weight with which position q wrote slot m (a position's picks are distinct locations)
+  auto wweight = [&](int q, int m) {
+    float r = 0.f;
+#pragma unroll
+    for (int j = 0; j < KP; ++j)
+      if (j < kk && pk_slot[0][q][j] == m) r = pk_w[0][q][j];
+    return r;
+  };
+  int ms[KP];
+  float ws[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    ms[j] = pk_slot[set][p][j];
+    ws[j] = pk_w[set][p][j];
+  }
+  unsigned long long mk[KP];           // read side: the earlier writers of each read slot
+  unsigned long long touched = 0ull;   // read side: every earlier position contributing to this one
+  int n_a = 0, n_b = 0;                // read side: contributions; write side: distinct slots owned, later writers
+  if (p < L) {
+    if (set == 1) {
+      const unsigned long long below = (1ull << p) - 1ull;
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {
+        mk[i] = i < kk ? wmask[ms[i]] & below : 0ull;
+        touched |= mk[i];
+      }
+      n_a = __builtin_popcountll(touched);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KP; ++j) {
+        if (j < kk) {
+          const unsigned long long mm = wmask[ms[j]];
+          if (__builtin_ctzll(mm) == p) {
+            ++n_a;
+            n_b += __builtin_popcountll(mm) - 1;
+          }
+        }
+      }
+    }
+  }
+  const int inc_a = wave_incl_scan(n_a, p);
+  const int inc_b = wave_incl_scan(n_b, p);
+  if (p == 63) {
+    if (set == 1) {
+      tot[0] = inc_a;
+    } else {
+      tot[1] = inc_a;
+      tot[2] = inc_b;
+    }
+  }
+  __syncthreads();
+  const int n_ri = tot[0], n_wu = tot[1], n_ext = tot[2];
+  const int64_t plan_id = (static_cast<int64_t>(b) * a.g.H + h) * a.n_chunks + c;
+  unsigned char* plan = a.plans + plan_id * pg.stride();
+  unsigned char* var = plan + pg.off_var();
+  uint2* ext = reinterpret_cast<uint2*>(var + 16);
+  float* ri_c = reinterpret_cast<float*>(var + 16 + 8 * n_ext);
+  unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
+  if (tid == 0) {
+    const int bytes = 16 + 8 * n_ext + 5 * n_ri;
+    *reinterpret_cast<uint4*>(var) = make_uint4(n_ri, n_wu, n_ext, bytes);
+    a.sizes[plan_id] = bytes;
+  }
+  if (set == 1) {
+    // in-chunk contributions in ascending q, and their coefficient sum
+    const int e0 = inc_a - n_a;
+    int k = e0;
+    float csum = 0.f;
+    while (touched) {
+      const int q = __builtin_ctzll(touched);
+      touched &= touched - 1ull;
+      float coef = 0.f;
+#pragma unroll
+      for (int i = 0; i < KP; ++i)
+        if ((mk[i] >> q) & 1ull) coef = fmaf(ws[i], wweight(q, ms[i]), coef);
+      coef *= pw[p - 1 - q];
+      ri_q[k] = static_cast<unsigned char>(q);
+      ri_c[k] = coef;
+      csum += coef;
+      ++k;
+    }
+    // position record: slots, weights, then ri_begin | ri_end << 16, csum
+    uint32_t rec[pg.pos_bytes() / 4];
+#pragma unroll
+    for (int i = 0; i < pg.pos_bytes() / 4; ++i) rec[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < KP; i += 2) rec[i / 2] = static_cast<uint32_t>(ms[i]) | (static_cast<uint32_t>(ms[i + 1]) << 16);
+#pragma unroll
+    for (int i = 0; i < KP; ++i) rec[KP / 2 + i] = __float_as_uint(ws[i]);
+    rec[pg.off_tail() / 4] = static_cast<uint32_t>(e0) | (static_cast<uint32_t>(inc_a) << 16);
+    rec[pg.off_tail() / 4 + 1] = __float_as_uint(csum);
+    uint4* dst = reinterpret_cast<uint4*>(plan + p * pg.pos_bytes());
+#pragma unroll
+    for (int i = 0; i < pg.pos_bytes() / 16; ++i) dst[i] = make_uint4(rec[4 * i], rec[4 * i + 1], rec[4 * i + 2], rec[4 * i + 3]);
+  } else if (p < L) {
+    uint2* wrec = reinterpret_cast<uint2*>(plan + pg.off_wrec());
+    int u = inc_a - n_a, e = inc_b - n_b;
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      if (j >= kk) break;
+      const int m = ms[j];
+      unsigned long long mm = wmask[m];
+      if (__builtin_ctzll(mm) != p) continue;   // p is the slot's first writer in the chunk
+      mm &= mm - 1ull;
+      const uint32_t cw = __float_as_uint(pw[L - 1 - p] * ws[j]) | (mm ? 0x80000000u : 0u);
+      wrec[(u & 63) * KP + (u >> 6)] =
+          make_uint2(static_cast<uint32_t>(m) | (static_cast<uint32_t>(p) << 16) | (static_cast<uint32_t>(e) << 22), cw);
+      ++u;
+      while (mm) {
+        const int q = __builtin_ctzll(mm);
+        mm &= mm - 1ull;
+        ext[e] = make_uint2(__float_as_uint(pw[L - 1 - q] * wweight(q, m)),
+                            static_cast<uint32_t>(q) | (mm ? 0u : 0x80000000u));
+        ++e;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// scan (executes the plans)
+struct ScanArgs {
+  const unsigned char* plans;  // [B][H][n_chunks][stride]
+  const int32_t* sizes;        // [B][H][n_chunks]
+  const void* v;               // value rows
+  int64_t v_stride;
+  const float* decay;          // [H]
   const float* state_in_mem;   // [B][H][M][dh] or nullptr
   const float* state_in_cnt;   // [B][H][M] or nullptr
   float* state_out_mem;
   float* state_out_cnt;
-  void* r_out;             // rows of H * dh; OutT
+  void* r_out;                 // rows of H * dh; OutT
   int64_t r_stride;
-  int B, T, H, dh, M, kk, read_mean;
+  int B, T, H, dh, M, n_chunks, read_mean;
   float read_eps;
 };
 
-constexpr int kChunk = 64;                 // positions per chunk (one bit each in the per-location writer masks)
-constexpr size_t kLdsBytes = 160 * 1024;   // LDS per workgroup on gfx950
-constexpr int kScanThreads = 512;          // 64 positions x 8 lanes
-constexpr int kNoQ = 0x7f;                 // "no in-chunk writer" in the packed read flags
+constexpr int kScanThreads = 512;   // 64 positions x 8 lanes
 
 __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 
-// LDS of one scan workgroup, in order: the slab A[M][CW] (CW value columns of every location), the write counts
-// cnt[M], the writer masks of the current chunk wmask[M] (bit q: position q of the chunk writes the location);
-// u16 [64][KP] arrays: picks s_iw / s_ir, packed read flags s_qf (first and second earlier in-chunk writer of the
-// read pick, and a bit for "three or more"), write ranks s_rk (earlier in-chunk writers of the write pick's slot);
-// f32 [64][KP]: weights s_ww / s_wr and the two in-chunk read coefficients s_c1 / s_c2; the staged values s_v[64][CW]
-// (VT: bfloat16 inputs are staged exactly as bfloat16), denominators s_den[64], fade powers pw[68], and the
-// largest write rank of the chunk.
+// LDS of one scan workgroup: the slab A[M][CW], the write counts cnt[M], the current chunk's variable plan part, its
+// values s_v[64][CW] (staged in the input type: bfloat16 exactly), and fade powers pw[68].
 __host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int v_bytes) {
-  return sizeof(float) * (static_cast<size_t>(M) * CW + pad4(M)) + sizeof(unsigned long long) * pad4(M) +
-         sizeof(uint16_t) * 4 * kChunk * KP + sizeof(float) * 4 * kChunk * KP +
-         static_cast<size_t>(v_bytes) * kChunk * CW + sizeof(float) * (kChunk + 68) + 16;
+  return sizeof(float) * (static_cast<size_t>(M) * CW + pad4(M)) + PlanGeom{KP}.max_var() +
+         static_cast<size_t>(v_bytes) * kChunk * CW + sizeof(float) * 68;
 }
 
-// The KP picks of one position: slot ids (16-bit) and weights, loaded with 128-bit LDS reads.
-template <int KP>
-__device__ __forceinline__ void load_picks(const uint16_t* sl, const float* wt, int (&m)[KP], float (&w)[KP]) {
-#pragma unroll
-  for (int g = 0; g < KP / 8; ++g) {
-    const uint4 v = *reinterpret_cast<const uint4*>(sl + 8 * g);
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      m[8 * g + 2 * e] = static_cast<int>(u[e] & 0xffffu);
-      m[8 * g + 2 * e + 1] = static_cast<int>(u[e] >> 16);
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < KP / 4; ++g) {
-    const float4 v = *reinterpret_cast<const float4*>(wt + 4 * g);
-    w[4 * g] = v.x;
-    w[4 * g + 1] = v.y;
-    w[4 * g + 2] = v.z;
-    w[4 * g + 3] = v.w;
-  }
-}
-
-template <int KP>
-__device__ __forceinline__ void load_u16(const uint16_t* sl, int (&m)[KP]) {
-#pragma unroll
-  for (int g = 0; g < KP / 8; ++g) {
-    const uint4 v = *reinterpret_cast<const uint4*>(sl + 8 * g);
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      m[8 * g + 2 * e] = static_cast<int>(u[e] & 0xffffu);
-      m[8 * g + 2 * e + 1] = static_cast<int>(u[e] >> 16);
-    }
-  }
-}
-
-template <int KP>
-__device__ __forceinline__ void load_f32(const float* wt, float (&w)[KP]) {
-#pragma unroll
-  for (int g = 0; g < KP / 4; ++g) {
-    const float4 v = *reinterpret_cast<const float4*>(wt + 4 * g);
-    w[4 * g] = v.x;
-    w[4 * g + 1] = v.y;
-    w[4 * g + 2] = v.z;
-    w[4 * g + 3] = v.w;
-  }
-}
-
-// Weight with which position q (its KP slot ids sl and weights wt, the first kk live) wrote slot m (a position
-// writes a slot at most once; 0 when it did not).
-template <int KP>
-__device__ __forceinline__ float writer_weight(const uint16_t* sl, const float* wt, int m, int kk) {
-  int mq[KP];
-  float wq[KP];
-  load_picks<KP>(sl, wt, mq, wq);
-  float r = 0.f;
-#pragma unroll
-  for (int j = 0; j < KP; ++j) r = (j < kk && mq[j] == m) ? wq[j] : r;
-  return r;
-}
-
-// CPL consecutive floats (CPL = 4, 2, 1) of LDS, one vector access; the bfloat16 variant converts.
+// CPL consecutive values (CPL = 4, 2, 1) from LDS in one access; bfloat16 values are converted.
 template <int CPL>
 struct Seg {
   float v[CPL];
@@ -386,7 +819,7 @@ __device__ __forceinline__ void store_seg(OutT* o, const float (&v)[CPL]) {
   for (int c = 0; c < CPL; ++c) o[c] = from_f32<OutT>(v[c]);
 }
 
-// Sum over the 8 consecutive lanes of a position (DPP: swap neighbours, swap pairs, mirror the halves of 8).
+// Sum over the 8 consecutive lanes of a group (DPP: swap neighbours, swap pairs, mirror the halves of 8).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
@@ -399,7 +832,7 @@ __device__ __forceinline__ float sum8(float v) {
 }
 
 // Workgroup barrier that orders LDS accesses only: the scan shares nothing else between its threads, so global loads
-// issued ahead (the next chunk's picks) and global stores (read-outs) need not complete at every barrier.
+// issued ahead (the next chunk's plan and values) and global stores (read-outs) need not complete at a barrier.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
@@ -407,61 +840,85 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Scan of one (batch row, head) slab over CW of its value columns, 512 threads = 64 positions x 8 lanes.
-// Per chunk of up to 64 positions, separated by barriers:
-//   P1 stage   lane (position, pick): the chunk's picks and weights (loaded one chunk ahead) and CW/8 value columns
-//              into LDS; first the previous chunk's writer marks made from the same entries are cleared
-//   P2 mark    each write (q, j) sets bit q of wmask[slot]
-//   P3 control lane (position, pick): the read pick's S_in count term, its first two earlier in-chunk writers and
-//              their coefficients (a flag for more), the position's denominator (summed over its 8 lanes), and the
-//              write pick's rank = number of earlier in-chunk writers of its slot
-//   P4 read    lane (position, segment of CW/8 columns): mu * lam^p * S_in rows of the picks plus the in-chunk
-//              writes, divided by the denominator
-//   P5 write   in rounds r = 0, 1, ...: the writes of rank r add their faded value to their slot's row with one
-//              128-bit read-modify-write per lane (no two writes of a round share a slot; no LDS float atomics)
-// All sums are over fixed orders, so results are deterministic.
+// registers holding the next chunk's plan records, variable-part pieces and values until they are used
+template <int KP, int NV, typename VT, int CPL>
+struct ChunkRegs {
+  uint4 pos[PlanGeom{KP}.pos_bytes() / 16];
+  uint4 wrec[KP / 2];
+  uint4 var[NV];
+  VT v[CPL];
+  int pieces;
+};
+
+// Loads are unconditional (indexes clamped into the plan), so the compiler keeps them in flight across a chunk.
+template <int KP, int NV, typename VT, int CPL>
+__device__ __forceinline__ ChunkRegs<KP, NV, VT, CPL> fetch_chunk(const ScanArgs& a, int64_t slab, int b, int h,
+                                                                  int col0, int c, int bytes, int tid, int p, int l8) {
+  constexpr PlanGeom pg{KP};
+  ChunkRegs<KP, NV, VT, CPL> r;
+  const unsigned char* base = a.plans + (slab * a.n_chunks + c) * pg.stride();
+  const uint4* ps = reinterpret_cast<const uint4*>(base + p * pg.pos_bytes());
+#pragma unroll
+  for (int k = 0; k < pg.pos_bytes() / 16; ++k) r.pos[k] = ps[k];
+  const uint4* ws = reinterpret_cast<const uint4*>(base + pg.off_wrec() + p * KP * 8);
+#pragma unroll
+  for (int k = 0; k < KP / 2; ++k) r.wrec[k] = ws[k];
+  const uint4* vs = reinterpret_cast<const uint4*>(base + pg.off_var());
+  r.pieces = (bytes + 15) >> 4;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) r.var[k] = vs[min(tid + k * kScanThreads, r.pieces - 1)];
+  const int row = min(c * kChunk + p, a.T - 1);
+  const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + row) * a.v_stride +
+                   static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) r.v[k] = vrow[k];
+  return r;
+}
+
+__device__ __forceinline__ uint32_t u4_word(const uint4& q, int i) {
+  return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+}
+
+// Scan of one (batch row, head) slab over CW of its value columns, 512 threads = 64 groups x 8 lanes of CW/8
+// columns.  Per chunk:
+//   S1 stage  the chunk's variable plan part and values (loaded into registers one chunk ahead) into LDS
+//   S2 read   group = position: mu * lam^p * S_in rows of the read picks, plus the plan's in-chunk contributions
+//             of earlier positions' values; the mean read divides by mu * lam^p * sum(w * cnt) + the plan's in-chunk
+//             coefficient sum
+//   S3 write  group g takes the written slots g, g + 64, ...: their writers' faded values, divided by mu after the
+//             fade, are added to the slot's row (one owner per row: no atomics)
+// All sums run in fixed orders, so results are deterministic.
 template <int CW, int KP, typename VT, typename OutT>
 __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
-  constexpr int CPL = CW / 8;   // value columns per data lane
-  constexpr int G = KP / 8;     // picks per control lane
+  constexpr int CPL = CW / 8;
+  constexpr PlanGeom pg{KP};
+  constexpr int NV = (pg.max_var() / 16 + kScanThreads - 1) / kScanThreads;   // variable-part pieces per thread
+  constexpr int NB = 8;                                                          // write records per batch
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int M = a.M;
   float* A = lds;
   float* cnt = A + static_cast<size_t>(M) * CW;
-  unsigned long long* wmask = reinterpret_cast<unsigned long long*>(cnt + pad4(M));
-  uint16_t* s_iw = reinterpret_cast<uint16_t*>(wmask + pad4(M));
-  uint16_t* s_ir = s_iw + kChunk * KP;
-  uint16_t* s_qf = s_ir + kChunk * KP;
-  uint16_t* s_rk = s_qf + kChunk * KP;
-  float* s_ww = reinterpret_cast<float*>(s_rk + kChunk * KP);
-  float* s_wr = s_ww + kChunk * KP;
-  float* s_c1 = s_wr + kChunk * KP;
-  float* s_c2 = s_c1 + kChunk * KP;
-  VT* s_v = reinterpret_cast<VT*>(s_c2 + kChunk * KP);
-  float* s_den = reinterpret_cast<float*>(s_v + kChunk * CW);
-  float* pw = s_den + kChunk;
-  int* s_maxrank = reinterpret_cast<int*>(pw + 68);
+  unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M));
+  VT* s_v = reinterpret_cast<VT*>(var + pg.max_var());
+  float* pw = reinterpret_cast<float*>(s_v + kChunk * CW);
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int p = tid >> 3;     // position in the chunk
-  const int l8 = tid & 7;     // pick (control) or column segment (data)
+  const int p = tid >> 3;    // position (read) or slot group (write)
+  const int l8 = tid & 7;    // column segment
   const int col0 = cg * CW;
   const int64_t slab = static_cast<int64_t>(b) * a.H + h;
   const float lam = a.decay[h];
-  const int kk = a.kk;
+  const int32_t* sizes = a.sizes + slab * a.n_chunks;
 
   for (int i = tid; i < M * CW; i += kScanThreads) {
     const int m = i / CW;
     const int c = i - m * CW;
     A[i] = a.state_in_mem ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
   }
-  for (int m = tid; m < M; m += kScanThreads) {
-    cnt[m] = a.state_in_cnt ? a.state_in_cnt[slab * M + m] : 0.f;
-    wmask[m] = 0ull;
-  }
+  for (int m = tid; m < M; m += kScanThreads) cnt[m] = a.state_in_cnt ? a.state_in_cnt[slab * M + m] : 0.f;
   if (tid <= kChunk) {
     float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
     for (int e = 0; e < tid; ++e) v *= lam;
@@ -469,230 +926,168 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   }
   float mu = 1.f;
 
-  // this lane's picks (control role) and value columns (data role) of the next chunk, loaded one chunk ahead
-  int n_iw[G], n_ir[G];
-  float n_ww[G], n_wr[G];
-  VT n_v[CPL];
-  auto fetch = [&](int c0) {
-    if (p < min(kChunk, a.T - c0)) {
-      const int64_t pb = (slab * a.T + c0 + p) * KP;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int j = l8 + 8 * g;
-        n_iw[g] = a.idx_w[pb + j];
-        n_ir[g] = a.idx_r[pb + j];
-        n_ww[g] = a.w_w[pb + j];
-        n_wr[g] = a.w_r[pb + j];
-      }
-      const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + c0 + p) * a.v_stride +
-                       static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) n_v[c] = vrow[c];
-    }
-  };
-  fetch(0);
+  ChunkRegs<KP, NV, VT, CPL> nx = fetch_chunk<KP, NV, VT, CPL>(a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
+  int next_bytes = a.n_chunks > 1 ? sizes[1] : 0;
   lds_barrier();
 
-  for (int c0 = 0; c0 < a.T; c0 += kChunk) {
+  for (int c = 0; c < a.n_chunks; ++c) {
+    const int c0 = c * kChunk;
     const int L = min(kChunk, a.T - c0);
-    const bool active = p < L;
-    const int64_t row = static_cast<int64_t>(b) * a.T + c0 + p;
-    int iw[G], ir[G];
-    float ww[G], wr[G];
-    float vreg[CPL];
-    // P1: clear the previous chunk's marks made from this lane's entries, then stage
-    if (c0 > 0) {
+    // S1: stage
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int j = l8 + 8 * g;
-        if (j < kk) wmask[s_iw[p * KP + j]] = 0ull;
-      }
+    for (int k = 0; k < NV; ++k) {
+      const int piece = tid + k * kScanThreads;
+      if (piece < nx.pieces) reinterpret_cast<uint4*>(var)[piece] = nx.var[k];
     }
-    if (tid == 0) *s_maxrank = 0;
-    if (active) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int j = l8 + 8 * g;
-        iw[g] = n_iw[g];
-        ir[g] = n_ir[g];
-        ww[g] = n_ww[g];
-        wr[g] = n_wr[g];
-        s_iw[p * KP + j] = static_cast<uint16_t>(iw[g]);
-        s_ir[p * KP + j] = static_cast<uint16_t>(ir[g]);
-        s_ww[p * KP + j] = ww[g];
-        s_wr[p * KP + j] = wr[g];
-      }
+    for (int k = 0; k < CPL; ++k) s_v[p * CW + CPL * l8 + k] = nx.v[k];
+    // this chunk's records
+    int m[KP];
+    float w[KP];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        vreg[c] = to_f32(n_v[c]);
-        s_v[p * CW + CPL * l8 + c] = n_v[c];
-      }
+    for (int i = 0; i < KP; ++i) {
+      const uint32_t word = u4_word(nx.pos[i / 8], (i % 8) / 2);
+      m[i] = static_cast<int>(i % 2 ? word >> 16 : word & 0xffffu);
+      w[i] = __uint_as_float(u4_word(nx.pos[(2 * KP + 4 * i) / 16], ((2 * KP + 4 * i) % 16) / 4));
     }
+    const uint32_t tail0 = u4_word(nx.pos[pg.off_tail() / 16], (pg.off_tail() % 16) / 4);
+    const float csum = __uint_as_float(u4_word(nx.pos[pg.off_tail() / 16], (pg.off_tail() % 16) / 4 + 1));
+    const int ri_b = tail0 & 0xffffu, ri_e = tail0 >> 16;
+    uint2 wr[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) wr[k] = make_uint2(u4_word(nx.wrec[k / 2], 2 * (k % 2)), u4_word(nx.wrec[k / 2], 2 * (k % 2) + 1));
     lds_barrier();
-    // P2: mark; then start loading the next chunk
-    if (active) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (l8 + 8 * g < kk) atomicOr(&wmask[iw[g]], 1ull << p);
+    if (c + 1 < a.n_chunks) {
+      nx = fetch_chunk<KP, NV, VT, CPL>(a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
+      next_bytes = c + 2 < a.n_chunks ? sizes[c + 2] : 0;
     }
-    if (c0 + kChunk < a.T) fetch(c0 + kChunk);
-    lds_barrier();
-    // P3: control
-    if (active) {
+    const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
+    const int n_ri = hdr[0], n_wu = hdr[1], n_ext = hdr[2];
+    const uint2* ext = reinterpret_cast<const uint2*>(var + 16);
+    const float* ri_c = reinterpret_cast<const float*>(var + 16 + 8 * n_ext);
+    const unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
+    // S2: read
+    if (p < L) {
       const float fin = mu * pw[p];
-      const unsigned long long below = (1ull << p) - 1ull;
-      float dpart = 0.f;
-      int myrank = 0;
+      // the group's lanes share the count sum: lane l8 takes picks l8, l8 + 8
+      float cpart = 0.f;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int i = l8 + 8 * g;
-        uint32_t qf = kNoQ | (kNoQ << 7);
-        uint16_t rk = 0;
-        float c1 = 0.f, c2 = 0.f;
-        if (i < kk) {
-          const int m = ir[g];
-          const float w = wr[g];
-          dpart = fmaf(w * fin, cnt[m], dpart);
-          unsigned long long mk = wmask[m] & below;
-          if (mk) {
-            const int q1 = __builtin_ctzll(mk);
-            mk &= mk - 1ull;
-            const int q2 = mk ? __builtin_ctzll(mk) : q1;
-            const float w1 = writer_weight<KP>(s_iw + q1 * KP, s_ww + q1 * KP, m, kk);
-            const float w2 = writer_weight<KP>(s_iw + q2 * KP, s_ww + q2 * KP, m, kk);
-            c1 = w * w1 * pw[p - 1 - q1];
-            dpart += c1;
-            qf = q1 | (kNoQ << 7);
-            if (mk) {
-              c2 = w * w2 * pw[p - 1 - q2];
-              dpart += c2;
-              qf = q1 | (q2 << 7);
-              mk &= mk - 1ull;
-              if (mk) qf |= 1u << 14;
-              while (mk) {   // three or more earlier writers: the rest only enters the denominator here
-                const int q = __builtin_ctzll(mk);
-                mk &= mk - 1ull;
-                dpart += w * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m, kk) * pw[p - 1 - q];
-              }
-            }
+      for (int i0 = 0; i0 < KP; i0 += 8) {
+        int ml = m[i0];
+        float wl = w[i0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) {
+          if (l8 == i) {
+            ml = m[i0 + i];
+            wl = w[i0 + i];
           }
-          const unsigned long long mm = wmask[iw[g]] & below;
-          rk = static_cast<uint16_t>(__builtin_popcountll(mm));
-          myrank = max(myrank, static_cast<int>(rk));
         }
-        s_qf[p * KP + i] = static_cast<uint16_t>(qf);
-        s_c1[p * KP + i] = c1;
-        s_c2[p * KP + i] = c2;
-        s_rk[p * KP + i] = rk;
+        cpart = fmaf(wl, cnt[ml], cpart);
       }
-      dpart = sum8(dpart);
-      if (l8 == 0) s_den[p] = dpart;
-      if (myrank > 0) atomicMax(s_maxrank, myrank);
-    }
-    lds_barrier();
-    // P4: read
-    if (active) {
-      const float fin = mu * pw[p];
-      int m[KP], qfl[KP];
-      float w[KP], c1[KP], c2[KP];
-      load_picks<KP>(s_ir + p * KP, s_wr + p * KP, m, w);
-      load_u16<KP>(s_qf + p * KP, qfl);
-      load_f32<KP>(s_c1 + p * KP, c1);
-      load_f32<KP>(s_c2 + p * KP, c2);
+      Seg<CPL> x[KP];
+#pragma unroll
+      for (int i = 0; i < KP; ++i) x[i] = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);   // pad picks carry weight 0
       float acc[CPL];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
-#pragma unroll
-      for (int i = 0; i < KP; ++i) {   // pad picks carry weight 0
-        const Seg<CPL> x = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] = fmaf(w[i], x.v[c], acc[c]);
-      }
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) acc[c] *= fin;
+      for (int k = 0; k < CPL; ++k) acc[k] = 0.f;
 #pragma unroll
       for (int i = 0; i < KP; ++i) {
-        const int q1 = qfl[i] & kNoQ;
-        const int q2 = (qfl[i] >> 7) & kNoQ;
-        if (q1 != kNoQ) {
-          const Seg<CPL> v1 = lds_seg<CPL>(&s_v[q1 * CW + CPL * l8]);
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c1[i], v1.v[c], acc[c]);
-        }
-        if (q2 != kNoQ) {
-          const Seg<CPL> v2 = lds_seg<CPL>(&s_v[q2 * CW + CPL * l8]);
-#pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(c2[i], v2.v[c], acc[c]);
-        }
+        for (int k = 0; k < CPL; ++k) acc[k] = fmaf(w[i], x[i].v[k], acc[k]);
       }
 #pragma unroll
-      for (int i = 0; i < KP; ++i) {
-        if (!(qfl[i] & (1 << 14))) continue;   // three or more earlier writers (rare)
-        unsigned long long mk = wmask[m[i]] & ((1ull << p) - 1ull);
-        mk &= mk - 1ull;
-        mk &= mk - 1ull;
-        while (mk) {
-          const int q = __builtin_ctzll(mk);
-          mk &= mk - 1ull;
-          const float coef = w[i] * writer_weight<KP>(s_iw + q * KP, s_ww + q * KP, m[i], kk) * pw[p - 1 - q];
-          const Seg<CPL> vq = lds_seg<CPL>(&s_v[q * CW + CPL * l8]);
+      for (int k = 0; k < CPL; ++k) acc[k] *= fin;
+      for (int e = ri_b; e < ri_e; e += 4) {   // in-chunk contributions, four at a time
+        float cf[4];
+        Seg<CPL> vq[4];
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = fmaf(coef, vq.v[c], acc[c]);
+        for (int j = 0; j < 4; ++j) {
+          const int ej = min(e + j, ri_e - 1);
+          cf[j] = e + j < ri_e ? ri_c[ej] : 0.f;
+          vq[j] = lds_seg<CPL>(&s_v[ri_q[ej] * CW + CPL * l8]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int k = 0; k < CPL; ++k) acc[k] = fmaf(cf[j], vq[j].v[k], acc[k]);
         }
       }
+      const float cn = sum8(cpart);
       if (a.read_mean) {
-        const float inv = 1.f / (s_den[p] + a.read_eps);
+        const float den = fmaf(fin, cn, csum);
+        const float inv = 1.f / (den + a.read_eps);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] *= inv;
+        for (int k = 0; k < CPL; ++k) acc[k] *= inv;
       }
-      store_seg<OutT, CPL>(static_cast<OutT*>(a.r_out) + row * a.r_stride + static_cast<int64_t>(h) * a.dh + col0 +
-                               CPL * l8, acc);
+      store_seg<OutT, CPL>(static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b) * a.T + c0 + p) * a.r_stride +
+                               static_cast<int64_t>(h) * a.dh + col0 + CPL * l8, acc);
     }
     lds_barrier();
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
     float mu_new = mu * pw[L];
     if (!(mu_new >= kMuFloor)) {
       for (int i = tid; i < M * CW; i += kScanThreads) A[i] *= mu_new;
-      for (int m = tid; m < M; m += kScanThreads) cnt[m] *= mu_new;
+      for (int i = tid; i < M; i += kScanThreads) cnt[i] *= mu_new;
       mu_new = 1.f;
       lds_barrier();
     }
-    // P5: write, in rounds of equal rank
-    const int maxrank = *s_maxrank;
+    // S3: write; group p takes the written slots p + 64 k, NB at a time (distinct slots: no conflicts)
     {
-      const float cpos = active ? pw[L - 1 - p] / mu_new : 0.f;
-      int m[KP], rk[KP];
-      float w[KP];
-      if (active) {
-        load_picks<KP>(s_iw + p * KP, s_ww + p * KP, m, w);
-        load_u16<KP>(s_rk + p * KP, rk);
-      }
-      for (int r = 0; r <= maxrank; ++r) {
-        if (active) {
-          Seg<CPL> x[KP];
-          float cc[KP];
+      const float inv_mu = 1.f / mu_new;
 #pragma unroll
-          for (int j = 0; j < KP; ++j) {
-            if (j < kk && rk[j] == r) {
-              x[j] = lds_seg<CPL>(&A[m[j] * CW + CPL * l8]);
-              if (l8 == 0) cc[j] = cnt[m[j]];
-            }
+      for (int k0 = 0; k0 < KP; k0 += NB) {
+        if (p + kChunk * k0 < n_wu) {
+          int ms[NB];
+          float dc[NB];
+          Seg<CPL> x[NB], vq[NB];
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            const bool ok = p + kChunk * (k0 + j) < n_wu;   // records past the chunk's last are not read
+            ms[j] = ok ? static_cast<int>(wr[k0 + j].x & 0xffffu) : 0;
+            const int q0 = ok ? static_cast<int>((wr[k0 + j].x >> 16) & 63u) : 0;
+            dc[j] = ok ? __uint_as_float(wr[k0 + j].y & 0x7fffffffu) * inv_mu : 0.f;
+            x[j] = lds_seg<CPL>(&A[ms[j] * CW + CPL * l8]);
+            vq[j] = lds_seg<CPL>(&s_v[q0 * CW + CPL * l8]);
           }
 #pragma unroll
-          for (int j = 0; j < KP; ++j) {
-            if (j < kk && rk[j] == r) {
-              const float cp = cpos * w[j];
+          for (int j = 0; j < NB; ++j) {
 #pragma unroll
-              for (int c = 0; c < CPL; ++c) x[j].v[c] = fmaf(cp, vreg[c], x[j].v[c]);
-              lds_seg_store<CPL>(&A[m[j] * CW + CPL * l8], x[j]);
-              if (l8 == 0) cnt[m[j]] = cc[j] + cp;
+            for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(dc[j], vq[j].v[k], x[j].v[k]);
+            if (p + kChunk * (k0 + j) < n_wu && (wr[k0 + j].y & 0x80000000u)) {   // later writers of the slot
+              int e = wr[k0 + j].x >> 22;
+              uint2 t;
+              do {
+                t = ext[e++];
+                const float cf = __uint_as_float(t.x) * inv_mu;
+                const Seg<CPL> vx = lds_seg<CPL>(&s_v[(t.y & 63u) * CW + CPL * l8]);
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(cf, vx.v[k], x[j].v[k]);
+                dc[j] += cf;
+              } while (!(t.y & 0x80000000u));
             }
           }
+          // lane l8 updates the count of record k0 + l8
+          int mc = ms[0];
+          float dcc = dc[0];
+#pragma unroll
+          for (int j = 1; j < NB; ++j) {
+            if (l8 == j) {
+              mc = ms[j];
+              dcc = dc[j];
+            }
+          }
+          const bool cnt_ok = p + kChunk * (k0 + l8) < n_wu;
+          const float cold = cnt[mc];
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            if (p + kChunk * (k0 + j) < n_wu) lds_seg_store<CPL>(&A[ms[j] * CW + CPL * l8], x[j]);
+          }
+          if (cnt_ok) cnt[mc] = cold + dcc;
         }
-        lds_barrier();
       }
     }
     mu = mu_new;
+    lds_barrier();
   }
 
   if (a.state_out_mem) {
@@ -732,9 +1127,9 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
 // ---------------------------------------------------------------------------------------------------------------
 // host side
 struct Plan {
-  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap;
+  int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, n_chunks;
   // workspace offsets
-  size_t off_knorm, off_iw, off_ir, off_ww, off_wr, off_rtmp, total;
+  size_t off_knorm, off_sizes, off_plans, off_rtmp, total;
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -766,32 +1161,39 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   p->pitch = (p->kk + 7) / 8 * 8;
   if (scan_lds_bytes(p->M, p->pitch, 8, sizeof(float)) > kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations do not fit a slab of 8 columns in LDS", p->M);
+  if (plan_static_lds(p->pitch) + 8 * static_cast<size_t>(p->M) + 8 * static_cast<size_t>(p->n_sub) * p->half + 256 >
+      kLdsBytes)
+    return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations: writer masks and sub-keys do not fit in LDS", p->M);
+  p->n_chunks = (p->T + kChunk - 1) / kChunk;
   const size_t tok = static_cast<size_t>(p->B) * p->T;
-  const size_t picks = tok * p->H * p->pitch;
+  const size_t n_plans = static_cast<size_t>(p->B) * p->H * p->n_chunks;
   size_t o = 0;
   p->off_knorm = o;
   o = align_up(o + sizeof(float) * 2 * p->H * p->n_sub * p->half, 256);
-  p->off_iw = o;
-  o = align_up(o + sizeof(uint16_t) * picks, 256);
-  p->off_ir = o;
-  o = align_up(o + sizeof(uint16_t) * picks, 256);
-  p->off_ww = o;
-  o = align_up(o + sizeof(float) * picks, 256);
-  p->off_wr = o;
-  o = align_up(o + sizeof(float) * picks, 256);
+  p->off_sizes = o;
+  o = align_up(o + sizeof(int32_t) * n_plans, 256);
+  p->off_plans = o;
+  o = align_up(o + static_cast<size_t>(PlanGeom{p->pitch}.stride()) * n_plans, 256);
   p->off_rtmp = o;
   o = align_up(o + (d->out_norm ? sizeof(float) * tok * p->H * p->dh : 0), 256);
   p->total = o;
   return SDM_RT_OK;
 }
 
-bool aligned(const void* ptr, size_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
-
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_err(SDM_RT_ELAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
   return SDM_RT_OK;
 }
+
+// lets a kernel use all the LDS its static arrays leave free for dynamic LDS (once per kernel and process)
+bool allow_lds(const void* fn) {
+  hipFuncAttributes fa;
+  if (hipFuncGetAttributes(&fa, fn) != hipSuccess || fa.sharedSizeBytes > kLdsBytes) return false;
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(kLdsBytes - fa.sharedSizeBytes)) == hipSuccess;
+}
+int lds_err(const char* what) { return set_err(SDM_RT_ELAUNCH, "%s: cannot enable %zu bytes of LDS", what, kLdsBytes); }
 
 int launch_keynorm(const Plan& p, const sdm_rt_params* prm, float* knorm, hipStream_t st) {
   const int rows = p.H * p.n_sub;
@@ -801,43 +1203,83 @@ int launch_keynorm(const Plan& p, const sdm_rt_params* prm, float* knorm, hipStr
   return check_launch("keynorm");
 }
 
-template <int HALF, int CAP, typename InT>
-void launch_address_t(const Plan& p, const AddrArgs& a, int sets, hipStream_t st) {
-  const int64_t N = static_cast<int64_t>(p.B) * p.T;
-  dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H, sets);
-  hipLaunchKernelGGL((address_kernel<HALF, CAP, InT>), grid, dim3(64), 0, st, a);
+AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm, const float* knorm) {
+  AddrGeom g;
+  g.knorm = knorm;
+  g.addr_b = prm->addr_b;
+  g.log_scale = prm->log_scale;
+  g.gate_bias = prm->gate_bias;
+  g.H = p.H;
+  g.n_sub = p.n_sub;
+  g.c1 = p.c1;
+  g.kk = p.kk;
+  return g;
 }
 
-template <int HALF, typename InT>
-int launch_address_h(const Plan& p, const AddrArgs& a, int sets, hipStream_t st) {
-  if (p.cap == 8)
-    launch_address_t<HALF, 8, InT>(p, a, sets, st);
-  else
-    launch_address_t<HALF, 16, InT>(p, a, sets, st);
-  return check_launch("address");
-}
-
-template <typename InT>
-int launch_address_d(const Plan& p, const AddrArgs& a, int sets, hipStream_t st) {
-  switch (p.half) {
-    case 1: return launch_address_h<1, InT>(p, a, sets, st);
-    case 2: return launch_address_h<2, InT>(p, a, sets, st);
-    case 3: return launch_address_h<3, InT>(p, a, sets, st);
-    case 4: return launch_address_h<4, InT>(p, a, sets, st);
-    case 6: return launch_address_h<6, InT>(p, a, sets, st);
-    case 8: return launch_address_h<8, InT>(p, a, sets, st);
-    case 12: return launch_address_h<12, InT>(p, a, sets, st);
-    case 16: return launch_address_h<16, InT>(p, a, sets, st);
-    case 24: return launch_address_h<24, InT>(p, a, sets, st);
-    case 32: return launch_address_h<32, InT>(p, a, sets, st);
+// dispatch on the half width of an address (compile-time unrolled addressing)
+template <template <int, typename> class F, typename InT, typename... Args>
+int by_half(int half, Args&&... args) {
+  switch (half) {
+    case 1: return F<1, InT>::run(args...);
+    case 2: return F<2, InT>::run(args...);
+    case 3: return F<3, InT>::run(args...);
+    case 4: return F<4, InT>::run(args...);
+    case 6: return F<6, InT>::run(args...);
+    case 8: return F<8, InT>::run(args...);
+    case 12: return F<12, InT>::run(args...);
+    case 16: return F<16, InT>::run(args...);
+    case 24: return F<24, InT>::run(args...);
+    case 32: return F<32, InT>::run(args...);
     default:
-      return set_err(SDM_RT_EUNSUPPORTED, "addr_dim %d: half width must be one of 1,2,3,4,6,8,12,16,24,32", p.d_a);
+      return set_err(SDM_RT_EUNSUPPORTED, "addr_dim %d: half width must be one of 1,2,3,4,6,8,12,16,24,32", 2 * half);
   }
 }
 
-int launch_address(const Plan& p, const AddrArgs& a, int sets, sdm_rt_dtype dt, hipStream_t st) {
-  return dt == SDM_RT_BF16 ? launch_address_d<bf16_t>(p, a, sets, st) : launch_address_d<float>(p, a, sets, st);
-}
+// the matrix-core addressing covers half widths 8, 16, 32 and up to 32 sub-keys per half
+constexpr bool mf_half(int half) { return half == 8 || half == 16 || half == 32; }
+bool use_mf(const Plan& p) { return mf_half(p.half) && p.n_sub <= 32; }
+
+template <int HALF, typename InT>
+struct AddressLaunch {
+  template <int CAP, bool MF>
+  static void go(const Plan& p, const AddrArgs& a, hipStream_t st) {
+    const int64_t N = static_cast<int64_t>(p.B) * p.T;
+    dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H);
+    const size_t lds = MF ? 0 : sizeof(float) * 2 * p.n_sub * HALF;
+    hipLaunchKernelGGL((address_kernel<HALF, CAP, InT, MF>), grid, dim3(64), lds, st, a);
+  }
+  static int run(const Plan& p, const AddrArgs& a, hipStream_t st) {
+    if constexpr (mf_half(HALF)) {
+      if (use_mf(p)) {
+        if (p.cap == 8) go<8, true>(p, a, st);
+        else go<16, true>(p, a, st);
+        return check_launch("address");
+      }
+    }
+    if (p.cap == 8) go<8, false>(p, a, st);
+    else go<16, false>(p, a, st);
+    return check_launch("address");
+  }
+};
+
+template <int HALF, typename InT>
+struct PlanLaunch {
+  template <int KP, bool MF>
+  static int go(const Plan& p, const PlanArgs& a, hipStream_t st) {
+    dim3 grid(p.n_chunks, p.H, p.B);
+    const size_t lds = sizeof(unsigned long long) * p.M + (MF ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
+    static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MF>));
+    if (!ok) return lds_err("plan");
+    hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MF>), grid, dim3(128), lds, st, a);
+    return check_launch("plan");
+  }
+  static int run(const Plan& p, const PlanArgs& a, hipStream_t st) {
+    if constexpr (mf_half(HALF)) {
+      if (use_mf(p)) return p.pitch == 8 ? go<8, true>(p, a, st) : go<16, true>(p, a, st);
+    }
+    return p.pitch == 8 ? go<8, false>(p, a, st) : go<16, false>(p, a, st);
+  }
+};
 
 template <int CW, int KP, typename VT, typename OutT>
 int launch_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
@@ -856,7 +1298,7 @@ int launch_scan_k(const Plan& p, const ScanArgs& a, hipStream_t st) {
   return p.pitch == 8 ? launch_scan_t<CW, 8, VT, OutT>(p, a, st) : launch_scan_t<CW, 16, VT, OutT>(p, a, st);
 }
 
-// widest column group per scan workgroup (32, 16 or 8 value columns) whose slab and staging fit in LDS
+// widest column group per scan workgroup (32, 16 or 8 value columns) whose slab, plan and values fit in LDS
 template <typename VT>
 int scan_columns(const Plan& p) {
   for (int cw : {32, 16, 8})
@@ -886,13 +1328,12 @@ int check_dtype(sdm_rt_dtype t, const char* what) {
   return SDM_RT_OK;
 }
 
-int check_params(const Plan& p, const sdm_rt_params* prm, bool need_onorm) {
+int check_params(const sdm_rt_params* prm, bool need_onorm) {
   if (!prm) return set_err(SDM_RT_EINVAL, "params is NULL");
   if (!prm->keys1 || !prm->keys2) return set_err(SDM_RT_EINVAL, "keys1/keys2 must not be NULL");
   if (!prm->log_scale) return set_err(SDM_RT_EINVAL, "log_scale must not be NULL");
   if (!prm->decay) return set_err(SDM_RT_EINVAL, "decay must not be NULL");
   if (need_onorm && !prm->onorm_w) return set_err(SDM_RT_EINVAL, "onorm_w must not be NULL when out_norm is set");
-  (void)p;
   return SDM_RT_OK;
 }
 
@@ -923,7 +1364,7 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   Plan p;
   int rc = make_plan(dims, &p);
   if (rc) return rc;
-  if ((rc = check_params(p, params, false))) return rc;
+  if ((rc = check_params(params, false))) return rc;
   if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
   if (p.B == 0 || p.T == 0) return SDM_RT_OK;
   if (!z || !slot_out) return set_err(SDM_RT_EINVAL, "z and slot_out must not be NULL");
@@ -934,30 +1375,22 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   if (!workspace || workspace_bytes < p.total)
     return set_err(SDM_RT_ENOSPACE, "workspace %zu bytes < required %zu", workspace_bytes, p.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  float* knorm = reinterpret_cast<float*>(ws + p.off_knorm);
+  float* knorm = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.off_knorm);
   if ((rc = launch_keynorm(p, params, knorm, st))) return rc;
   AddrArgs a{};
-  a.z[0] = z;
-  a.z[1] = nullptr;
-  a.z_stride[0] = z_row_stride;
-  a.g = gate_logits;
+  a.g = addr_geom(p, params, knorm);
+  a.z = z;
+  a.z_stride = z_row_stride;
+  a.gl = gate_logits;
   a.g_stride = gate_row_stride;
-  a.gate_bias = params->gate_bias;
-  a.knorm = knorm;
-  a.addr_b = params->addr_b;
-  a.log_scale = params->log_scale;
   a.B = p.B;
   a.T = p.T;
-  a.H = p.H;
-  a.n_sub = p.n_sub;
-  a.c1 = p.c1;
-  a.kk = p.kk;
   a.pitch = p.pitch;
-  a.idx32[0] = slot_out;
-  a.w_out[0] = weight_out;
-  a.s_out[0] = score_out;
-  return launch_address(p, a, 1, in_dtype, st);
+  a.slot_out = slot_out;
+  a.w_out = weight_out;
+  a.s_out = score_out;
+  return in_dtype == SDM_RT_BF16 ? by_half<AddressLaunch, bf16_t>(p.half, p, a, st)
+                                 : by_half<AddressLaunch, float>(p.half, p, a, st);
 }
 
 int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* kz, int64_t kz_row_stride,
@@ -970,7 +1403,7 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   Plan p;
   int rc = make_plan(dims, &p);
   if (rc) return rc;
-  if ((rc = check_params(p, params, dims->out_norm != 0))) return rc;
+  if ((rc = check_params(params, dims->out_norm != 0))) return rc;
   if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
   if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
   const bool empty = p.B == 0 || p.T == 0;
@@ -986,7 +1419,7 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   if (v_row_stride < wv) return set_err(SDM_RT_EINVAL, "v_row_stride %lld < heads * head_dim", (long long)v_row_stride);
   if (gate_logits && gate_row_stride < p.H)
     return set_err(SDM_RT_EINVAL, "gate_row_stride %lld < heads", (long long)gate_row_stride);
-  if (out_row_stride < static_cast<int64_t>(p.H) * p.dh)
+  if (out_row_stride < wv)
     return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
   if ((state_in_mem == nullptr) != (state_in_cnt == nullptr))
     return set_err(SDM_RT_EINVAL, "state_in_mem and state_in_cnt must both be given or both be NULL");
@@ -1010,42 +1443,33 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   }
   char* ws = static_cast<char*>(workspace);
   float* knorm = reinterpret_cast<float*>(ws + p.off_knorm);
-  uint16_t* iw = reinterpret_cast<uint16_t*>(ws + p.off_iw);
-  uint16_t* ir = reinterpret_cast<uint16_t*>(ws + p.off_ir);
-  float* w_w = reinterpret_cast<float*>(ws + p.off_ww);
-  float* w_r = reinterpret_cast<float*>(ws + p.off_wr);
+  int32_t* sizes = reinterpret_cast<int32_t*>(ws + p.off_sizes);
+  unsigned char* plans = reinterpret_cast<unsigned char*>(ws + p.off_plans);
   float* rtmp = reinterpret_cast<float*>(ws + p.off_rtmp);
 
   if ((rc = launch_keynorm(p, params, knorm, st))) return rc;
-  AddrArgs a{};
-  a.z[0] = kz;
-  a.z[1] = qz;
-  a.z_stride[0] = kz_row_stride;
-  a.z_stride[1] = qz_row_stride;
-  a.g = dims->write_gate ? gate_logits : nullptr;
-  a.g_stride = gate_row_stride;
-  a.gate_bias = params->gate_bias;
-  a.knorm = knorm;
-  a.addr_b = params->addr_b;
-  a.log_scale = params->log_scale;
-  a.B = p.B;
-  a.T = p.T;
-  a.H = p.H;
-  a.n_sub = p.n_sub;
-  a.c1 = p.c1;
-  a.kk = p.kk;
-  a.pitch = p.pitch;
-  a.idx16[0] = iw;
-  a.idx16[1] = ir;
-  a.w_out[0] = w_w;
-  a.w_out[1] = w_r;
-  if ((rc = launch_address(p, a, 2, in_dtype, st))) return rc;
+  PlanArgs pa{};
+  pa.g = addr_geom(p, params, knorm);
+  pa.kz = kz;
+  pa.kz_stride = kz_row_stride;
+  pa.qz = qz;
+  pa.qz_stride = qz_row_stride;
+  pa.gl = dims->write_gate ? gate_logits : nullptr;
+  pa.g_stride = gate_row_stride;
+  pa.decay = params->decay;
+  pa.plans = plans;
+  pa.sizes = sizes;
+  pa.B = p.B;
+  pa.T = p.T;
+  pa.M = p.M;
+  pa.n_chunks = p.n_chunks;
+  rc = in_dtype == SDM_RT_BF16 ? by_half<PlanLaunch, bf16_t>(p.half, p, pa, st)
+                               : by_half<PlanLaunch, float>(p.half, p, pa, st);
+  if (rc) return rc;
 
   ScanArgs s{};
-  s.idx_w = iw;
-  s.idx_r = ir;
-  s.w_w = w_w;
-  s.w_r = w_r;
+  s.plans = plans;
+  s.sizes = sizes;
   s.v = v;
   s.v_stride = v_row_stride;
   s.decay = params->decay;
@@ -1058,7 +1482,7 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   s.H = p.H;
   s.dh = p.dh;
   s.M = p.M;
-  s.kk = p.kk;
+  s.n_chunks = p.n_chunks;
   s.read_mean = dims->read_mean;
   s.read_eps = dims->read_eps;
   if (dims->out_norm) {
