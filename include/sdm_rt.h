@@ -112,6 +112,16 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    float* state_out_mem, float* state_out_cnt,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* The input norm of RunTimeSdm (RMSNorm, experiments/track4/sdmllm/track4_sdmllm_models.py:63-71) with the
+ * reference's rounding: out = cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), the mean and product in float32,
+ * cast_in rounding to the input dtype and cast_out to out_dtype.
+ *   x    [rows] of d values, dtype in_dtype, row stride x_row_stride (elements)
+ *   w    [d] float32
+ *   out  [rows] of d values, dtype out_dtype, row stride out_row_stride */
+int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, int64_t rows, int32_t d,
+                    const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                    void* stream);
+
 /* Description of the last failure on the calling thread ("" if none). */
 const char* sdm_rt_last_error(void);
 

@@ -154,3 +154,28 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
     if want_state:
         return out, (mem_out, cnt_out)
     return out
+
+
+def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
+    """RMSNorm of the last dimension with the reference's rounding (track4_sdmllm_models.py:63-71):
+    cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), float32 math; out_dtype defaults to x.dtype."""
+    if x.device.type != "cuda":
+        raise RuntimeError("rms_norm needs a ROCm device tensor")
+    if x.dtype not in _DT:
+        raise ValueError(f"rms_norm: dtype {x.dtype} is not float32 or bfloat16")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d)
+    if x2.numel() and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    out_dtype = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    o2 = out.view(-1, d)
+    wf = w.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.sdm_rt_rms_norm(_ptr(x2), x2.stride(0) if x2.numel() else d, _DT[x.dtype], x2.shape[0], d, _ptr(wf),
+                             float(eps), _ptr(o2), o2.stride(0) if o2.numel() else d, _DT[out_dtype],
+                             ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return out

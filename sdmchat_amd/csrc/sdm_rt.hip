@@ -1,7 +1,6 @@
 // sdm_rt.hip -- HIP kernels for gfx950 and the C ABI declared in include/sdm_rt.h.
 //
 // One forward is four launches:
-//   keynorm_kernel  unit-normalise every sub-key once per call (F.normalize of keys, track4_onesdm_models.py:137-140)
 //   plan_kernel     per (chunk of 64 positions, head, batch row): product-key addressing of the chunk's write keys
 //                   and read queries (pk_address :134-148; softmax weights and gate, prepare :203-207), then the
 //                   chunk's plan: which earlier positions of the chunk each read sees (with their faded
@@ -74,20 +73,6 @@ constexpr int kChunk = 64;                          // positions per chunk (one 
 constexpr size_t kLdsBytes = 160 * 1024;            // LDS per workgroup on gfx950
 
 // ---------------------------------------------------------------------------------------------------------------
-// keynorm: out[s][:] = keys[s][:] / max(||keys[s]||, 1e-12) for the 2 * H * n_sub sub-keys
-__global__ void keynorm_kernel(const float* __restrict__ keys1, const float* __restrict__ keys2,
-                               float* __restrict__ out, int rows_per_set, int half) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= 2 * rows_per_set) return;
-  const float* src = (r < rows_per_set ? keys1 + static_cast<int64_t>(r) * half
-                                       : keys2 + static_cast<int64_t>(r - rows_per_set) * half);
-  float ss = 0.f;
-  for (int d = 0; d < half; ++d) ss = fmaf(src[d], src[d], ss);
-  const float n = fmaxf(sqrtf(ss), 1e-12f);
-  for (int d = 0; d < half; ++d) out[static_cast<int64_t>(r) * half + d] = src[d] / n;
-}
-
-// ---------------------------------------------------------------------------------------------------------------
 // addressing of one (token, head, address set)
 
 // sorted top list in registers: v[0] >= v[1] >= ...; an incoming value moves ahead of an entry only when strictly
@@ -112,7 +97,8 @@ __device__ __forceinline__ void top_insert(float (&v)[CAP], int (&ix)[CAP], floa
 }
 
 struct AddrGeom {
-  const float* knorm;      // [2][H][n_sub][half] unit sub-keys
+  const float* keys[2];    // [H][n_sub][half] sub-keys of each half (unit-normalised where they are used,
+                           // F.normalize of keys, track4_onesdm_models.py:137-140)
   const float* addr_b;     // [H][d_a] or nullptr
   const float* log_scale;  // [H]
   const float* gate_bias;  // [H] or nullptr
@@ -349,12 +335,16 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
   int hx[2][CAP];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    float ka[S];
-    load_vals<S, float>(g.knorm + ((static_cast<int64_t>(hf) * g.H + h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S,
-                        ka);
-    if (jl >= g.n_sub) {
+    float ka[S];   // sub-key row jl, dims kb * S .. kb * S + S - 1, unit-normalised over the row
+    {
+      load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
+      float ks = 0.f;
 #pragma unroll
-      for (int s = 0; s < S; ++s) ka[s] = 0.f;
+      for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
+      const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
+      const float kn = fmaxf(sqrtf(__uint_as_float(kp[0]) + __uint_as_float(kp[1])), 1e-12f);
+#pragma unroll
+      for (int s = 0; s < S; ++s) ka[s] = jl < g.n_sub ? ka[s] / kn : 0.f;
     }
     floatx16 acc[2];
 #pragma unroll
@@ -454,13 +444,16 @@ struct AddrArgs {
   float* s_out;
 };
 
-// Copy head h's unit sub-keys of both halves ([2][n_sub][HALF] floats) into LDS.
+// Head h's sub-keys of both halves, unit-normalised ([2][n_sub][HALF] floats), into LDS: one row per thread.
 template <int HALF>
 __device__ __forceinline__ void stage_keys(const AddrGeom& g, int h, float* kn, int tid, int nthreads) {
-  const int per_half = g.n_sub * HALF;
-  for (int i = tid; i < 2 * per_half; i += nthreads) {
-    const int part = i >= per_half;
-    kn[i] = g.knorm[(static_cast<int64_t>(part) * g.H + h) * per_half + (i - part * per_half)];
+  for (int r = tid; r < 2 * g.n_sub; r += nthreads) {
+    const int part = r >= g.n_sub;
+    const float* src = g.keys[part] + (static_cast<int64_t>(h) * g.n_sub + (r - part * g.n_sub)) * HALF;
+    float ss = 0.f;
+    for (int d = 0; d < HALF; ++d) ss = fmaf(src[d], src[d], ss);
+    const float n = fmaxf(sqrtf(ss), 1e-12f);
+    for (int d = 0; d < HALF; ++d) kn[r * HALF + d] = src[d] / n;
   }
 }
 
@@ -1103,25 +1096,107 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// finish: one wave per (token, head) row of dh float32 read-outs
+// finish: 8 lanes per (token, head) row of dh float32 read-outs, 8 columns per lane and step
 template <typename OutT>
 __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r, int64_t r_stride,
                                                      OutT* __restrict__ out, int64_t out_stride,
                                                      const float* __restrict__ onorm_w, int64_t rows, int H,
                                                      int dh, float eps) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const int64_t n = row / H;
-  const int h = static_cast<int>(row - n * H);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 32 + (threadIdx.x >> 3);
+  const int l8 = threadIdx.x & 7;
+  const bool live = row < rows;   // every lane runs the cross-lane sum
+  const int64_t n = live ? row / H : 0;
+  const int h = live ? static_cast<int>(row - n * H) : 0;
   const float* src = r + n * r_stride + static_cast<int64_t>(h) * dh;
+  constexpr int kMaxSteps = 8;    // dh <= 512
+  float v[kMaxSteps][8];
   float ss = 0.f;
-  for (int d = lane; d < dh; d += 64) ss = fmaf(src[d], src[d], ss);
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  for (int k = 0; k < kMaxSteps; ++k) {
+    const int c = 8 * l8 + 64 * k;
+    if (live && c < dh) {
+      const float4 x0 = *reinterpret_cast<const float4*>(src + c);
+      const float4 x1 = *reinterpret_cast<const float4*>(src + c + 4);
+      v[k][0] = x0.x; v[k][1] = x0.y; v[k][2] = x0.z; v[k][3] = x0.w;
+      v[k][4] = x1.x; v[k][5] = x1.y; v[k][6] = x1.z; v[k][7] = x1.w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+    }
+  }
+  ss = sum8(ss);
+  if (!live) return;
   const float inv = 1.f / sqrtf(ss / static_cast<float>(dh) + eps);
   OutT* dst = out + n * out_stride + static_cast<int64_t>(h) * dh;
-  for (int d = lane; d < dh; d += 64) dst[d] = from_f32<OutT>(src[d] * inv * onorm_w[h * dh + d]);
+  const float* wr = onorm_w + h * dh;
+#pragma unroll
+  for (int k = 0; k < kMaxSteps; ++k) {
+    const int c = 8 * l8 + 64 * k;
+    if (c < dh) {
+      const float4 w0 = *reinterpret_cast<const float4*>(wr + c);
+      const float4 w1 = *reinterpret_cast<const float4*>(wr + c + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      OutT o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = from_f32<OutT>(v[k][e] * inv * wv[e]);
+      if ((reinterpret_cast<uintptr_t>(dst + c) & 15u) == 0) {
+        if constexpr (sizeof(OutT) == 2) {
+          uint32_t q[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            q[e] = static_cast<uint32_t>(reinterpret_cast<const uint16_t&>(o[2 * e])) |
+                   (static_cast<uint32_t>(reinterpret_cast<const uint16_t&>(o[2 * e + 1])) << 16);
+          *reinterpret_cast<uint4*>(dst + c) = make_uint4(q[0], q[1], q[2], q[3]);
+        } else {
+          *reinterpret_cast<float4*>(dst + c) = make_float4(v[k][0] * inv * wv[0], v[k][1] * inv * wv[1],
+                                                            v[k][2] * inv * wv[2], v[k][3] * inv * wv[3]);
+          *reinterpret_cast<float4*>(dst + c + 4) = make_float4(v[k][4] * inv * wv[4], v[k][5] * inv * wv[5],
+                                                                v[k][6] * inv * wv[6], v[k][7] * inv * wv[7]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[c + e] = o[e];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// rms_norm: one wave per row; lanes take 8 consecutive values at a time
+template <typename InT, typename OutT>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x, int64_t x_stride,
+                                                       OutT* __restrict__ out, int64_t out_stride,
+                                                       const float* __restrict__ w, int64_t rows, int d, float eps) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;   // whole waves
+  const InT* src = x + row * x_stride;
+  constexpr int kMax = 4;    // 8 * 64 * 4 = 2048 values per row in registers
+  float v[kMax][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMax; ++k) {
+    const int c = 8 * (lane + 64 * k);
+    if (c < d) {
+      load_vals<8, InT>(src + c, v[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  OutT* dst = out + row * out_stride;
+#pragma unroll
+  for (int k = 0; k < kMax; ++k) {
+    const int c = 8 * (lane + 64 * k);
+    if (c < d) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = to_f32(from_f32<InT>(v[k][e] * r));   // .to(x.dtype)
+        dst[c + e] = from_f32<OutT>(t * w[c + e]);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1129,7 +1204,7 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
 struct Plan {
   int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, n_chunks;
   // workspace offsets
-  size_t off_knorm, off_sizes, off_plans, off_rtmp, total;
+  size_t off_sizes, off_plans, off_rtmp, total;
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -1140,6 +1215,7 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   if (d->heads < 1) return set_err(SDM_RT_EINVAL, "heads must be >= 1");
   if (d->head_dim < 8 || d->head_dim % 8 != 0)
     return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d must be a positive multiple of 8", d->head_dim);
+  if (d->head_dim > 512) return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d exceeds 512", d->head_dim);
   if (d->addr_dim < 2 || d->addr_dim % 2 != 0) return set_err(SDM_RT_EINVAL, "addr_dim %d must be even", d->addr_dim);
   if (d->n_sub < 1) return set_err(SDM_RT_EINVAL, "n_sub must be >= 1");
   if (d->top_k < 1) return set_err(SDM_RT_EINVAL, "top_k must be >= 1");
@@ -1168,8 +1244,6 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   const size_t tok = static_cast<size_t>(p->B) * p->T;
   const size_t n_plans = static_cast<size_t>(p->B) * p->H * p->n_chunks;
   size_t o = 0;
-  p->off_knorm = o;
-  o = align_up(o + sizeof(float) * 2 * p->H * p->n_sub * p->half, 256);
   p->off_sizes = o;
   o = align_up(o + sizeof(int32_t) * n_plans, 256);
   p->off_plans = o;
@@ -1195,17 +1269,10 @@ bool allow_lds(const void* fn) {
 }
 int lds_err(const char* what) { return set_err(SDM_RT_ELAUNCH, "%s: cannot enable %zu bytes of LDS", what, kLdsBytes); }
 
-int launch_keynorm(const Plan& p, const sdm_rt_params* prm, float* knorm, hipStream_t st) {
-  const int rows = p.H * p.n_sub;
-  const int threads = 128;
-  const int blocks = (2 * rows + threads - 1) / threads;
-  hipLaunchKernelGGL(keynorm_kernel, dim3(blocks), dim3(threads), 0, st, prm->keys1, prm->keys2, knorm, rows, p.half);
-  return check_launch("keynorm");
-}
-
-AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm, const float* knorm) {
+AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm) {
   AddrGeom g;
-  g.knorm = knorm;
+  g.keys[0] = prm->keys1;
+  g.keys[1] = prm->keys2;
   g.addr_b = prm->addr_b;
   g.log_scale = prm->log_scale;
   g.gate_bias = prm->gate_bias;
@@ -1357,6 +1424,34 @@ int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims) {
 
 const char* sdm_rt_last_error(void) { return g_err; }
 
+int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, int64_t rows, int32_t d,
+                    const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                    void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (rows < 0 || d < 1) return set_err(SDM_RT_EINVAL, "rows must be >= 0 and d >= 1");
+  if (d % 8 != 0 || d > 2048) return set_err(SDM_RT_EUNSUPPORTED, "d = %d must be a multiple of 8 up to 2048", d);
+  if (rows == 0) return SDM_RT_OK;
+  if (!x || !w || !out) return set_err(SDM_RT_EINVAL, "x, w and out must not be NULL");
+  if (x_row_stride < d || out_row_stride < d) return set_err(SDM_RT_EINVAL, "row strides must be >= d");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+#define SDM_RT_NORM(IT, OT)                                                                                     \
+  hipLaunchKernelGGL((rms_norm_kernel<IT, OT>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x),      \
+                     x_row_stride, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  if (in_dtype == SDM_RT_BF16) {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(bf16_t, bf16_t);
+    else SDM_RT_NORM(bf16_t, float);
+  } else {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(float, bf16_t);
+    else SDM_RT_NORM(float, float);
+  }
+#undef SDM_RT_NORM
+  return check_launch("rms_norm");
+}
+
 int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* z, int64_t z_row_stride,
                    const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype, int32_t* slot_out,
                    float* score_out, float* weight_out, void* workspace, size_t workspace_bytes, void* stream) {
@@ -1372,13 +1467,11 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
     return set_err(SDM_RT_EINVAL, "z_row_stride %lld < heads * addr_dim", (long long)z_row_stride);
   if (gate_logits && gate_row_stride < p.H)
     return set_err(SDM_RT_EINVAL, "gate_row_stride %lld < heads", (long long)gate_row_stride);
-  if (!workspace || workspace_bytes < p.total)
-    return set_err(SDM_RT_ENOSPACE, "workspace %zu bytes < required %zu", workspace_bytes, p.total);
+  (void)workspace;   // the addressing alone needs no workspace
+  (void)workspace_bytes;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  float* knorm = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.off_knorm);
-  if ((rc = launch_keynorm(p, params, knorm, st))) return rc;
   AddrArgs a{};
-  a.g = addr_geom(p, params, knorm);
+  a.g = addr_geom(p, params);
   a.z = z;
   a.z_stride = z_row_stride;
   a.gl = gate_logits;
@@ -1406,6 +1499,8 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   if ((rc = check_params(params, dims->out_norm != 0))) return rc;
   if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
   if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (dims->out_norm && (reinterpret_cast<uintptr_t>(params->onorm_w) & 15u) != 0)
+    return set_err(SDM_RT_EINVAL, "onorm_w must be 16-byte aligned");
   const bool empty = p.B == 0 || p.T == 0;
   if (!empty && (!kz || !qz || !v || !r_out))
     return set_err(SDM_RT_EINVAL, "kz, qz, v and r_out must not be NULL");
@@ -1442,14 +1537,12 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
     return SDM_RT_OK;
   }
   char* ws = static_cast<char*>(workspace);
-  float* knorm = reinterpret_cast<float*>(ws + p.off_knorm);
   int32_t* sizes = reinterpret_cast<int32_t*>(ws + p.off_sizes);
   unsigned char* plans = reinterpret_cast<unsigned char*>(ws + p.off_plans);
   float* rtmp = reinterpret_cast<float*>(ws + p.off_rtmp);
 
-  if ((rc = launch_keynorm(p, params, knorm, st))) return rc;
   PlanArgs pa{};
-  pa.g = addr_geom(p, params, knorm);
+  pa.g = addr_geom(p, params);
   pa.kz = kz;
   pa.kz_stride = kz_row_stride;
   pa.qz = qz;
@@ -1490,7 +1583,7 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
     s.r_stride = static_cast<int64_t>(p.H) * p.dh;
     if ((rc = launch_scan(p, s, in_dtype, SDM_RT_F32, st))) return rc;
     const int64_t rows = static_cast<int64_t>(p.B) * p.T * p.H;
-    const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+    const unsigned blocks = static_cast<unsigned>((rows + 31) / 32);
     if (out_dtype == SDM_RT_BF16) {
       hipLaunchKernelGGL((finish_kernel<bf16_t>), dim3(blocks), dim3(256), 0, st, rtmp, s.r_stride,
                          static_cast<bf16_t*>(r_out), out_row_stride, params->onorm_w, rows, p.H, p.dh,

@@ -71,6 +71,7 @@ class RunTimeSdm(nn.Module):
         if out_norm:
             self.onorm_w = nn.Parameter(torch.ones(heads, self.dh))
         self.gate_bias0 = gate_bias
+        self._gate_src = None
         self.last_gate = None
         self.last_state = None
         self._fused = None
@@ -88,13 +89,14 @@ class RunTimeSdm(nn.Module):
 
     # -- fused input projection ----------------------------------------------------------------------------------
     def _fused_weight(self, dtype):
-        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 64), cached until a weight changes."""
+        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 256, a shape hipBLASLt runs well), cached until a
+        weight changes."""
         ws = (self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight)
         key = (dtype, ws[0].device) + tuple((w.data_ptr(), w._version) for w in ws)
         if self._fused is not None and self._fused[0] == key:
             return self._fused[1], self._fused[2]
         rows = sum(w.shape[0] for w in ws)
-        padded = (rows + 63) // 64 * 64
+        padded = (rows + 255) // 256 * 256
         W = torch.zeros(padded, self.d, dtype=dtype, device=ws[0].device)
         W[:rows].copy_(torch.cat([w.detach() for w in ws], 0))
         wo = self.wo.weight.detach().to(dtype)
@@ -126,9 +128,9 @@ class RunTimeSdm(nn.Module):
         kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer;
         addr_b and the gate bias are added inside the core."""
         H, d_a, d = self.h, self.d_a, self.d
-        hx = self.norm(x).float()
+        hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
         W = self._fused_weight(dt)[0]
-        proj = torch.matmul(hx.to(dt), W.t())                          # [B, T, padded rows]
+        proj = torch.matmul(hx, W.t())                                 # [B, T, padded rows]
         o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
         g = proj[..., o_g:o_g + H] if self.write_gate else None
         return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
@@ -153,12 +155,26 @@ class RunTimeSdm(nn.Module):
                 want_state=self.keep_state, workspace=self._ws)
             r, state = (res if self.keep_state else (res, None))
             y = torch.matmul(r, wo.t()).to(x.dtype)
-        if self.write_gate:
-            self.last_gate = torch.sigmoid(g.float() + self.wg.bias.detach().float())
-        else:
-            self.last_gate = torch.ones(B, T, H, device=x.device)
+        self._gate_src = (g, self.wg.bias.detach() if self.write_gate else None, (B, T, H), x.device)
+        self._last_gate = None
         self.last_state = state
         return y
+
+    @property
+    def last_gate(self):
+        """The write gate of the last forward, [B, T, H] float32 (prepare, track4_onesdm_models.py:205, 212);
+        computed from the kept gate logits when first read."""
+        if self._last_gate is None and self._gate_src is not None:
+            g, bias, shape, dev = self._gate_src
+            self._last_gate = (torch.sigmoid(g.float() + bias.float()) if g is not None
+                               else torch.ones(shape, device=dev))
+            self._gate_src = None
+        return self._last_gate
+
+    @last_gate.setter
+    def last_gate(self, value):
+        self._last_gate = value
+        self._gate_src = None
 
     def forward_sequential(self, x, reset=None):
         """The token recurrence of the reference (track4_onesdm_models.py:276-300).  It is the same function as

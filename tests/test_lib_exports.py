@@ -86,3 +86,13 @@ def test_missing_pointers_and_small_workspace_are_rejected():
     rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 7, one, 4096, 0,
                             None, None, None, None, one, 1 << 30, None)
     assert rc == -1 and "dtype" in lib.sdm_rt_last_error().decode()
+
+
+def test_rms_norm_validation():
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)
+    assert lib.sdm_rt_rms_norm(one, 12, 1, 4, 12, one, 1e-6, one, 12, 1, None) == -3   # d not a multiple of 8
+    assert "multiple of 8" in lib.sdm_rt_last_error().decode()
+    assert lib.sdm_rt_rms_norm(one, 8, 1, 4, 16, one, 1e-6, one, 16, 1, None) == -1    # row stride < d
+    assert lib.sdm_rt_rms_norm(one, 16, 5, 4, 16, one, 1e-6, one, 16, 1, None) == -1   # unknown dtype
+    assert lib.sdm_rt_rms_norm(None, 16, 1, 0, 16, None, 1e-6, None, 16, 1, None) == 0  # no rows: nothing to do
