@@ -1,20 +1,27 @@
 """Throughput of the run-time SDM mixer forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--core-only] [--copy-probe]
 
 Workload: one RunTimeSdm layer forward at B=8, T=2048, d=768, 12 heads of width 64, 1,024 product-key locations
 per head, k=8, bf16 activations and weights, float32 memory state, synthetic seeded inputs and Xavier weights.  A
-step is one module forward (RMSNorm, fused input projection, SDM core, output map) over the 16,384 tokens, with
-inputs already resident in HBM.  Prints one JSON line.
+step is one module forward (fused RMSNorm, fused input projection GEMM, SDM core, output map) over the 16,384
+tokens, with inputs already resident in HBM; value = 16,384 * K / the wall time of K steps.  Prints one JSON line.
 
-roofline: the SDM core (sdm_rt_forward: addressing, scan, finish) is HBM-bound.  Its algorithmic traffic is
-6,168 B per token (kz, qz, V in bf16 = 3 x 1,536 B, gate logits 24 B, read-out 1,536 B) plus 104,544 B of
-parameters per call: 101,161,056 B at this shape.  achieved = that / the core's mean call time, timed with HIP events
-on the stream the kernels run on.  traffic = HBM bytes per call from rocprofv3 FETCH_SIZE / WRITE_SIZE counters,
-read from profiles/traffic_core_bench.txt when present (null otherwise).
+roofline: the SDM core (sdm_rt_forward: plan_kernel, scan_kernel, finish_kernel, from the projection outputs to
+the read-out before wo) is HBM-bound.  Its algorithmic traffic is 6,168 B per token (kz, qz, V in bf16 =
+3 x 1,536 B, gate logits 24 B, read-out 1,536 B) plus 104,544 B of parameters per call: 101,161,056 B at this
+shape.  achieved = that / the core's median call time (5 warm calls, then the median of 50, each bracketed by HIP
+events on the stream the kernels run on).  traffic = measured HBM bytes per call (rocprofv3 FETCH_SIZE +
+WRITE_SIZE summed over the three kernels, scaled by the same counters' reading for a device copy of known size),
+read from profiles/sdm_core_traffic_b8_t2048.txt when present (null otherwise).
+
+module: the whole layer is MFMA-bound (79.6 GFLOP per call against 55.2 MB): module.frac = max(bytes / 8 TB/s,
+FLOPs / 2.5 PFLOP/s) / module time.  copy_gbs: a 1 GiB device-to-device copy, for context.
 
 cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle/sdm_torch32.py, the reference's
 dense chunk algorithm) on the same workload, all host cores, one warm call then best of three.
+
+--copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
 """
 import argparse
 import json
@@ -31,6 +38,11 @@ B, T, D, H, N_SUB, D_A, K = 8, 2048, 768, 12, 32, 64, 8
 HBM_PEAK_GBS = 8000.0
 CORE_BYTES_PER_TOKEN = 3 * H * 64 * 2 + H * 2 + H * 64 * 2          # 6,168
 CORE_PARAM_BYTES = 2 * H * N_SUB * (D_A // 2) * 4 + H * D_A * 4 + 2 * H * 4 + H * 64 * 4   # keys, addr_b, scale, fade, onorm
+BF16_PEAK_FLOPS = 2.5e15
+# whole layer: x in and y out (bf16), the four projections and wo (bf16), wg bias and norm weight, core parameters
+MODULE_BYTES = B * T * D * 2 * 2 + 4 * D * D * 2 + (D * H * 2 + H * 2) + D * 2 + CORE_PARAM_BYTES
+# projections, wo, key scores (2 address sets x 2 halves x 32 sub-keys x 32 dims x 2), sparse write and read
+MODULE_FLOPS = B * T * (2 * D * (3 * D + H) + 2 * D * D + 98_304 + 24_960)
 
 
 def log(*a):
@@ -38,7 +50,7 @@ def log(*a):
 
 
 def read_traffic():
-    path = os.path.join(ROOT, "profiles", "traffic_core_bench.txt")
+    path = os.path.join(ROOT, "profiles", "sdm_core_traffic_b8_t2048.txt")
     if not os.path.exists(path):
         return None
     m = re.search(r"^traffic_bytes_per_call:\s*([0-9.eE+]+)", open(path).read(), re.M)
@@ -77,6 +89,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
+    ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
@@ -105,27 +118,47 @@ def main():
             core.core_forward(kz, qz, V, g, keys1=m.keys1, keys2=m.keys2, log_scale=m.log_scale, decay=m.decay(),
                               k=K, out=r_out, workspace=ws, params=prm)
 
+        if a.copy_probe:
+            src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+
+        def median_call_ms(fn, n=50, warm=5):
+            for _ in range(warm):
+                fn()
+            torch.cuda.synchronize()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+            for e0, e1 in evs:
+                e0.record()
+                fn()
+                e1.record()
+            torch.cuda.synchronize()
+            ts = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+            return ts[n // 2]
+
         def timed(fn, steps, warmup):
             for _ in range(warmup):
                 fn()
             torch.cuda.synchronize()
-            ev0 = torch.cuda.Event(enable_timing=True)
-            ev1 = torch.cuda.Event(enable_timing=True)
             t0 = time.perf_counter()
-            ev0.record()
             for _ in range(steps):
                 fn()
-            ev1.record()
             torch.cuda.synchronize()
-            wall = time.perf_counter() - t0
-            return ev0.elapsed_time(ev1) / steps, wall
+            return time.perf_counter() - t0
 
-        core_ms, _ = timed(core_call, max(a.steps, 20), a.warmup)
-        log(f"core: {core_ms * 1e3:.1f} us per call")
+        core_ms = median_call_ms(core_call)
+        log(f"core: {core_ms * 1e3:.1f} us per call (median of 50)")
         if a.core_only:
             print(json.dumps({"core_ms": core_ms}))
             return
-        mod_ev_ms, wall = timed(lambda: m(x), a.steps, a.warmup)
+        mod_ms = median_call_ms(lambda: m(x))
+        wall = timed(lambda: m(x), a.steps, a.warmup)
+        big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        big2 = torch.empty_like(big)
+        copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
+        del big, big2
 
     ms_per_step = wall * 1e3 / a.steps
     tokens = B * T
@@ -152,7 +185,10 @@ def main():
                      "kernel": "SDM core (sdm_rt_forward)", "algorithmic_bytes": core_bytes,
                      "ms_per_call": round(core_ms, 5)},
         "core": {"ms": round(core_ms, 5), "tokens_per_s": round(tokens / (core_ms * 1e-3), 1)},
-        "module_event_ms": round(mod_ev_ms, 5),
+        "module": {"ms": round(mod_ms, 5), "bound": "mfma", "bytes": MODULE_BYTES, "flops": MODULE_FLOPS,
+                   "frac": round(max(MODULE_BYTES / (HBM_PEAK_GBS * 1e9), MODULE_FLOPS / BF16_PEAK_FLOPS)
+                                 / (mod_ms * 1e-3), 4)},
+        "copy_gbs": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
     }
     if not a.no_cpu:
         log("cpu baseline ...")

@@ -313,6 +313,33 @@ __device__ __forceinline__ void load_vals(const InT* p, float (&out)[n]) {
   for (int s = 0; s < n; ++s) out[s] = to_f32(p[s]);
 }
 
+// n floats to n values of type OutT at p: 16-byte stores when p is 16-byte aligned, element stores otherwise
+template <int n, typename OutT>
+__device__ __forceinline__ void store_vals(OutT* p, const float (&v)[n]) {
+  constexpr int kBytes = n * static_cast<int>(sizeof(OutT));
+  if constexpr (kBytes % 16 == 0) {
+    if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+#pragma unroll
+      for (int q = 0; q < kBytes / 16; ++q) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (sizeof(OutT) == 2) {
+            wd[e] = static_cast<uint32_t>(from_f32<bf16_t>(v[8 * q + 2 * e]).bits) |
+                    (static_cast<uint32_t>(from_f32<bf16_t>(v[8 * q + 2 * e + 1]).bits) << 16);
+          } else {
+            wd[e] = __float_as_uint(v[4 * q + e]);
+          }
+        }
+        reinterpret_cast<uint4*>(p)[q] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < n; ++s) p[s] = from_f32<OutT>(v[s]);
+}
+
 // number of grid pairs (a, b), a, b < CAP, with (a+1)(b+1) <= CAP: the candidates of the top-CAP combine
 __host__ __device__ constexpr int n_pairs(int cap) {
   int n = 0;
@@ -1132,30 +1159,11 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
   for (int k = 0; k < kMaxSteps; ++k) {
     const int c = 8 * l8 + 64 * k;
     if (c < dh) {
-      const float4 w0 = *reinterpret_cast<const float4*>(wr + c);
-      const float4 w1 = *reinterpret_cast<const float4*>(wr + c + 4);
-      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      OutT o[8];
+      float wv[8], o[8];
+      load_vals<8, float>(wr + c, wv);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = from_f32<OutT>(v[k][e] * inv * wv[e]);
-      if ((reinterpret_cast<uintptr_t>(dst + c) & 15u) == 0) {
-        if constexpr (sizeof(OutT) == 2) {
-          uint32_t q[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            q[e] = static_cast<uint32_t>(reinterpret_cast<const uint16_t&>(o[2 * e])) |
-                   (static_cast<uint32_t>(reinterpret_cast<const uint16_t&>(o[2 * e + 1])) << 16);
-          *reinterpret_cast<uint4*>(dst + c) = make_uint4(q[0], q[1], q[2], q[3]);
-        } else {
-          *reinterpret_cast<float4*>(dst + c) = make_float4(v[k][0] * inv * wv[0], v[k][1] * inv * wv[1],
-                                                            v[k][2] * inv * wv[2], v[k][3] * inv * wv[3]);
-          *reinterpret_cast<float4*>(dst + c + 4) = make_float4(v[k][4] * inv * wv[4], v[k][5] * inv * wv[5],
-                                                                v[k][6] * inv * wv[6], v[k][7] * inv * wv[7]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dst[c + e] = o[e];
-      }
+      for (int e = 0; e < 8; ++e) o[e] = v[k][e] * inv * wv[e];
+      store_vals<8, OutT>(dst + c, o);
     }
   }
 }
@@ -1190,11 +1198,12 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x
   for (int k = 0; k < kMax; ++k) {
     const int c = 8 * (lane + 64 * k);
     if (c < d) {
+      float wv[8];
+      load_vals<8, float>(w + c, wv);
+      float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float t = to_f32(from_f32<InT>(v[k][e] * r));   // .to(x.dtype)
-        dst[c + e] = from_f32<OutT>(t * w[c + e]);
-      }
+      for (int e = 0; e < 8; ++e) o[e] = to_f32(from_f32<InT>(v[k][e] * r)) * wv[e];   // .to(x.dtype) * w
+      store_vals<8, OutT>(dst + c, o);
     }
   }
 }
@@ -1499,8 +1508,6 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   if ((rc = check_params(params, dims->out_norm != 0))) return rc;
   if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
   if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
-  if (dims->out_norm && (reinterpret_cast<uintptr_t>(params->onorm_w) & 15u) != 0)
-    return set_err(SDM_RT_EINVAL, "onorm_w must be 16-byte aligned");
   const bool empty = p.B == 0 || p.T == 0;
   if (!empty && (!kz || !qz || !v || !r_out))
     return set_err(SDM_RT_EINVAL, "kz, qz, v and r_out must not be NULL");
