@@ -70,7 +70,8 @@ typedef struct {
   const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
 } sdm_rt_params;
 
-/* Bytes of workspace sdm_rt_forward / sdm_rt_address need for these dimensions (0 on invalid dims). */
+/* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (about
+ * 22.5 KB per 64 positions of one head at k <= 8) and, with out_norm, a float32 copy of the read-out. */
 size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
 
 /* Row pitch (entries per token and head) of the pick arrays sdm_rt_address writes: kk rounded up to 8. */
@@ -83,7 +84,8 @@ int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims);
  *   slot_out     [B][H][T][pitch] int32 slot ids, the kk picks in descending score order, ties to the lower
  *                index (pad entries -1)
  *   score_out    same layout, float32 scores (v1 + v2) / 2; may be NULL
- *   weight_out   same layout, float32 softmax(exp(log_scale) * score) (times the gate); may be NULL */
+ *   weight_out   same layout, float32 softmax(exp(log_scale) * score) (times the gate); may be NULL
+ *   workspace    not used by the addressing alone (may be NULL) */
 int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    const void* z, int64_t z_row_stride,
                    const void* gate_logits, int64_t gate_row_stride,

@@ -81,11 +81,9 @@ def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_b
     slots = torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev)
     scores = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
     weights = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
-    nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = lib.sdm_rt_address(ctypes.byref(dims), ctypes.byref(prm), _ptr(z), zs, _ptr(gate_logits), gs, _DT[z.dtype],
-                            _ptr(slots), _ptr(scores), _ptr(weights), _ptr(ws), nbytes, ctypes.c_void_p(stream))
+                            _ptr(slots), _ptr(scores), _ptr(weights), None, 0, ctypes.c_void_p(stream))
     _lib.check(rc, lib)
     del held
     return slots[..., :kk], scores[..., :kk], weights[..., :kk]

@@ -41,8 +41,9 @@ def test_workspace_and_pitch():
     lib = _lib.load()
     dims = _dims()
     ws = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))
-    picks = 8 * 2048 * 12 * 8
-    assert ws >= picks * (2 + 2 + 4 + 4) + 8 * 2048 * 12 * 64 * 4
+    plans = 8 * 12 * (2048 // 64)               # one plan per 64 positions of one head of one batch row
+    assert ws >= plans * 64 * (8 * 6 + 8 * 8) + 8 * 2048 * 12 * 64 * 4   # picks and write records, fp32 read-out
+    assert ws < plans * 32768 + 8 * 2048 * 12 * 64 * 4 + (1 << 20)
     assert lib.sdm_rt_pick_pitch(ctypes.byref(dims)) == 8
     assert lib.sdm_rt_pick_pitch(ctypes.byref(_dims(k=16, addr_dim=32))) == 16
     assert lib.sdm_rt_pick_pitch(ctypes.byref(_dims(k=5, n_sub=6))) == 8

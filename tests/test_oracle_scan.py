@@ -139,3 +139,31 @@ def test_finish_closed_form():
     r = O.finish(num, den, "mean", 0.0, True, np.array([[2.0, 2.0]]), 0.0)
     np.testing.assert_allclose(r[0, 0, 0], np.array([3.0, 4.0]) / np.sqrt(12.5) * 2, rtol=1e-15)
     np.testing.assert_allclose(O.finish(num, den, "sum", 1.0, False), num)
+
+
+def _closed_variant(siw, ww, sir, wr, V, lam, lag, include_self):
+    """The closed-form double sum with a fade exponent of t - lag - s, over s < t (or s <= t)."""
+    B, H, T, _ = siw.shape
+    num = np.zeros(V.shape)
+    for b, h, t in np.ndindex(B, H, T):
+        for s in range(t + 1 if include_self else t):
+            m = (sir[b, h, t][:, None] == siw[b, h, s][None, :]).astype(np.float64)
+            c = float(wr[b, h, t] @ m @ ww[b, h, s]) * lam[h] ** (t - lag - s)
+            num[b, h, t] += c * V[b, h, s]
+    return num
+
+
+def test_planted_scan_mistakes_fail_the_closed_form():
+    """The recurrence agrees with the closed form, and the closed form tells apart the plausible mistakes: a fade
+    exponent off by one, and a read that already sees the current position's write."""
+    rng = np.random.Generator(np.random.PCG64(23))
+    B, H, T, k, M, dh = 1, 2, 12, 3, 5, 3
+    siw = _distinct_ids(rng, (B, H, T), k, M)
+    sir = _distinct_ids(rng, (B, H, T), k, M)
+    ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
+    V = rng.standard_normal((B, H, T, dh))
+    lam = np.array([0.6, 0.9])
+    num, _, _, _ = O.scan_recurrence(siw, ww, sir, wr, V, lam, state=(np.zeros((B, H, M, dh)), np.zeros((B, H, M))))
+    np.testing.assert_allclose(_closed_variant(siw, ww, sir, wr, V, lam, 1, False), num, atol=1e-12)
+    assert np.abs(_closed_variant(siw, ww, sir, wr, V, lam, 0, False) - num).max() > 1e-3
+    assert np.abs(_closed_variant(siw, ww, sir, wr, V, lam, 1, True) - num).max() > 1e-3
