@@ -213,29 +213,55 @@ __device__ __forceinline__ float gate_of(const InT* grow, int h, const float* ga
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-// f64 selection key: plain double order = (score descending, then lower index first).  A float converted to double
-// has 29 zero low mantissa bits; the index goes there (index for negative scores, idx_max - index otherwise, so the
-// lower index is the larger key).  Zero scores map to (idx_max - index) * 2^-1000, between every negative and every
-// positive score, so no key is a denormal or -0.
-__device__ __forceinline__ double sel_key(float s, int idx, int idx_max) {
-  if (s == 0.f) return static_cast<double>(idx_max - idx) * 0x1p-1000;
-  const unsigned long long low =
-      s > 0.f ? static_cast<unsigned long long>(idx_max - idx) : static_cast<unsigned long long>(idx);
+// f64 selection key: plain double order = (score descending, then lower tie index first).  A float converted to
+// double has 29 zero low mantissa bits; they hold a TB-bit tie field above a PB-bit payload field.  The tie field
+// is the tie index for negative scores and (2^TB - 1) - tie index otherwise, so the lower index gives the larger key;
+// the payload (a function of the candidate, below the tie field) never decides an order.  A zero score's key is
+// built the same way and then given the smallest normal exponent (fix_zero_key): it sorts between every negative
+// and every positive score, in tie order, and no key is a denormal.
+template <int TB, int PB>
+__device__ __forceinline__ double sel_key(float s, int tie, int payload) {
+  static_assert(TB + PB <= 29, "key fields exceed the free mantissa bits");
+  // (2^TB - 1) - tie == tie ^ (2^TB - 1): flip the tie field unless the sign bit is set
+  const uint32_t flip = ~static_cast<uint32_t>(static_cast<int32_t>(__float_as_uint(s)) >> 31) &
+                        (((1u << TB) - 1u) << PB);
+  const uint32_t low = ((static_cast<uint32_t>(tie) << PB) | static_cast<uint32_t>(payload)) ^ flip;
   return __longlong_as_double(__double_as_longlong(static_cast<double>(s)) | low);
 }
-__device__ __forceinline__ void sel_decode(double k, int idx_max, float& s, int& idx) {
-  if (fabs(k) < 0x1p-900) {
-    s = 0.f;
-    idx = idx_max - static_cast<int>(k * 0x1p1000);
-    return;
-  }
+// A +0 score's key has a zero high word (exponent field 0); every other key's high word is at least 0x36A00000
+// (positive) or has the sign bit set, so an unsigned max with 0x00100000 moves exactly the zero keys to exponent 1.
+__device__ __forceinline__ double fix_zero_key(double k) {
+  const unsigned long long b = __double_as_longlong(k);
+  const uint32_t hi = max(static_cast<uint32_t>(b >> 32), 0x00100000u);
+  return __longlong_as_double((static_cast<unsigned long long>(hi) << 32) | (b & 0xffffffffull));
+}
+// the most negative finite double: below every real key, and no NaN whatever the low word
+__device__ __forceinline__ double lowest_key(double k) {
+  return __longlong_as_double((0xffefffffull << 32) | (__double_as_longlong(k) & 0xffffffffull));
+}
+// the score and the payload of a key
+template <int PB>
+__device__ __forceinline__ void sel_decode(double k, float& s, int& payload) {
   const unsigned long long bits = __double_as_longlong(k);
-  const int low = static_cast<int>(bits & 0xffull);   // idx_max <= 255
-  idx = k > 0.0 ? idx_max - low : low;
-  s = static_cast<float>(__longlong_as_double(bits & ~0x1fffffffull));
+  s = ((bits >> 52) & 0x7ffu) <= 1u ? 0.f : static_cast<float>(__longlong_as_double(bits & ~0x1fffffffull));
+  payload = static_cast<int>(bits & ((1ull << PB) - 1));
 }
 
 // compare-exchange networks on f64 keys, descending
+__device__ __forceinline__ void ce_desc(double& a, double& b) {
+  const double x = a, y = b;
+  a = fmax(x, y);
+  b = fmin(x, y);
+}
+// 8 keys with the 19-comparator network of depth 6
+__device__ __forceinline__ void sort8_desc(double* v) {
+  ce_desc(v[0], v[2]); ce_desc(v[1], v[3]); ce_desc(v[4], v[6]); ce_desc(v[5], v[7]);
+  ce_desc(v[0], v[4]); ce_desc(v[1], v[5]); ce_desc(v[2], v[6]); ce_desc(v[3], v[7]);
+  ce_desc(v[0], v[1]); ce_desc(v[2], v[3]); ce_desc(v[4], v[5]); ce_desc(v[6], v[7]);
+  ce_desc(v[2], v[4]); ce_desc(v[3], v[5]);
+  ce_desc(v[1], v[4]); ce_desc(v[3], v[6]);
+  ce_desc(v[1], v[2]); ce_desc(v[3], v[4]); ce_desc(v[5], v[6]);
+}
 template <int N>
 __device__ __forceinline__ void bitonic_sort_desc(double* v) {
 #pragma unroll
@@ -281,7 +307,10 @@ __device__ __forceinline__ void merge_top_desc(double* a, const double* b) {
 template <int K, int N>
 __device__ __forceinline__ void top_k_desc(double (&c)[N]) {
 #pragma unroll
-  for (int g = 0; g < N / K; ++g) bitonic_sort_desc<K>(c + g * K);
+  for (int g = 0; g < N / K; ++g) {
+    if constexpr (K == 8) sort8_desc(c + g * K);
+    else bitonic_sort_desc<K>(c + g * K);
+  }
 #pragma unroll
   for (int g = 1; g < N / K; ++g) merge_top_desc<K>(c, c + g * K);
 }
@@ -362,35 +391,45 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
   int hx[2][CAP];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    float ka[S];   // sub-key row jl, dims kb * S .. kb * S + S - 1, unit-normalised over the row
-    {
-      load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
+    // this half's loads first: the sub-key row, the address rows of both tiles, the address bias
+    float ka[S], zb[2][S], ab[S];
+    load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = min(32 * t + jl, rows - 1);
+      load_vals<S, InT>(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + hf * HALF + kb * S, zb[t]);
+    }
+    if (g.addr_b) {
+      load_vals<S, float>(g.addr_b + h * 2 * HALF + hf * HALF + kb * S, ab);
+    } else {
+#pragma unroll
+      for (int s = 0; s < S; ++s) ab[s] = 0.f;
+    }
+    {   // sub-key row jl, dims kb * S .. kb * S + S - 1, unit-normalised over the row
       float ks = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
       const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-      const float kn = fmaxf(sqrtf(__uint_as_float(kp[0]) + __uint_as_float(kp[1])), 1e-12f);
+      const float kinv = jl < g.n_sub ? 1.f / fmaxf(sqrtf(__uint_as_float(kp[0]) + __uint_as_float(kp[1])), 1e-12f)
+                                      : 0.f;
 #pragma unroll
-      for (int s = 0; s < S; ++s) ka[s] = jl < g.n_sub ? ka[s] / kn : 0.f;
+      for (int s = 0; s < S; ++s) ka[s] *= kinv;
     }
     floatx16 acc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int row = min(32 * t + jl, rows - 1);
-      float zb[S];
-      load_vals<S, InT>(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + hf * HALF + kb * S, zb);
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        if (g.addr_b) zb[s] += g.addr_b[h * 2 * HALF + hf * HALF + kb * S + s];
-        ss = fmaf(zb[s], zb[s], ss);
+        zb[t][s] += ab[s];
+        ss = fmaf(zb[t][s], zb[t][s], ss);
       }
       const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
       ss = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);   // dims of both lane halves, same order in both
       const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
       acc[t] = floatx16{};
 #pragma unroll
-      for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[s] * inv, acc[t], 0, 0, 0);
+      for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[t][s] * inv, acc[t], 0, 0, 0);
     }
     double c[32];
 #pragma unroll
@@ -398,14 +437,17 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]), false,
                                                        false);
       const int i0 = 8 * (r / 4) + (r % 4);
-      c[r] = i0 < g.n_sub ? sel_key(__uint_as_float(sw[0]), i0, 31) : -INFINITY;
-      c[16 + r] = i0 + 4 < g.n_sub ? sel_key(__uint_as_float(sw[1]), i0 + 4, 31) : -INFINITY;
+      c[r] = fix_zero_key(sel_key<5, 5>(__uint_as_float(sw[0]), i0, i0));
+      c[16 + r] = fix_zero_key(sel_key<5, 5>(__uint_as_float(sw[1]), i0 + 4, i0 + 4));
+      if (i0 >= g.n_sub) c[r] = lowest_key(c[r]);   // sub-keys past n_sub are never picked
+      if (i0 + 4 >= g.n_sub) c[16 + r] = lowest_key(c[16 + r]);
     }
     top_k_desc<CAP, 32>(c);
 #pragma unroll
-    for (int r = 0; r < CAP; ++r) sel_decode(c[r], 31, hv[hf][r], hx[hf][r]);
+    for (int r = 0; r < CAP; ++r) sel_decode<5>(c[r], hv[hf][r], hx[hf][r]);
   }
-  // combine over the dominance-pruned grid (see address_one)
+  // combine over the dominance-pruned grid (see address_one); tie index ra * 16 + rb orders like the flat grid index
+  // ra * c1 + rb, and the payload carries the slot's two sub-key ids
   constexpr int NP = n_pairs(CAP);
   constexpr int NPAD = (NP + CAP - 1) / CAP * CAP;
   double pc[NPAD];
@@ -417,7 +459,9 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
       for (int rb = 0; rb < CAP; ++rb) {
         if ((ra + 1) * (rb + 1) <= CAP) {
           const bool ok = ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk;
-          pc[n++] = ok ? sel_key((hv[0][ra] + hv[1][rb]) * 0.5f, ra * g.c1 + rb, 255) : -INFINITY;
+          const double k = fix_zero_key(sel_key<8, 10>((hv[0][ra] + hv[1][rb]) * 0.5f, ra * 16 + rb,
+                                                       hx[0][ra] * 32 + hx[1][rb]));
+          pc[n++] = ok ? k : lowest_key(k);
         }
       }
     }
@@ -428,7 +472,7 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
   float cv[CAP];
   int ci[CAP];
 #pragma unroll
-  for (int p = 0; p < CAP; ++p) sel_decode(pc[p], 255, cv[p], ci[p]);
+  for (int p = 0; p < CAP; ++p) sel_decode<10>(pc[p], cv[p], ci[p]);
   const float scale = expf(g.log_scale[h]);
   float e[CAP];
   const float x0 = cv[0] * scale;
@@ -438,23 +482,12 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
     e[p] = (p < g.kk) ? expf(cv[p] * scale - x0) : 0.f;
     sum += e[p];
   }
+  const float wscale = gate / sum;
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
     const bool live = p < g.kk;
-    int sl = 0;
-    if (live) {
-      const int ra = ci[p] / g.c1;
-      const int rb = ci[p] - ra * g.c1;
-      int i1 = 0, i2 = 0;
-#pragma unroll
-      for (int q = 0; q < CAP; ++q) {
-        if (q == ra) i1 = hx[0][q];
-        if (q == rb) i2 = hx[1][q];
-      }
-      sl = i1 * g.n_sub + i2;
-    }
-    slot[p] = sl;
-    w[p] = live ? e[p] / sum * gate : 0.f;
+    slot[p] = live ? (ci[p] >> 5) * g.n_sub + (ci[p] & 31) : 0;
+    w[p] = live ? e[p] * wscale : 0.f;
     score[p] = live ? cv[p] : 0.f;
   }
 }
@@ -582,7 +615,7 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // 64-bit masks, each position's read contributions and each written slot's writer list are found, counted,
 // prefix-summed within the wave and written out.
 template <int HALF, int KP, typename InT, bool MF>
-__global__ void __launch_bounds__(128) plan_kernel(PlanArgs a) {
+__global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   constexpr PlanGeom pg{KP};
   const int c = blockIdx.x;
   const int h = blockIdx.y;
@@ -596,8 +629,8 @@ __global__ void __launch_bounds__(128) plan_kernel(PlanArgs a) {
   const int L = min(kChunk, a.T - c0);
   const float lam = a.decay[h];
 
-  __shared__ uint16_t pk_slot[2][kChunk][KP];
-  __shared__ float pk_w[2][kChunk][KP];
+  __shared__ __attribute__((aligned(16))) uint16_t pk_slot[2][kChunk][KP];
+  __shared__ __attribute__((aligned(16))) float pk_w[2][kChunk][KP];
   __shared__ float pw[kChunk + 4];
   __shared__ int tot[4];
   extern __shared__ unsigned long long wmask[];   // [M], then (per-thread path) the head's sub-keys [2][n_sub][HALF]
@@ -644,8 +677,18 @@ __global__ void __launch_bounds__(128) plan_kernel(PlanArgs a) {
   auto wweight = [&](int q, int m) {
     float r = 0.f;
 #pragma unroll
-    for (int j = 0; j < KP; ++j)
-      if (j < kk && pk_slot[0][q][j] == m) r = pk_w[0][q][j];
+    for (int g8 = 0; g8 < KP / 8; ++g8) {   // the row's picks and weights in 16-byte reads
+      const uint4 sv = *reinterpret_cast<const uint4*>(&pk_slot[0][q][8 * g8]);
+      const float4 wa = *reinterpret_cast<const float4*>(&pk_w[0][q][8 * g8]);
+      const float4 wb = *reinterpret_cast<const float4*>(&pk_w[0][q][8 * g8 + 4]);
+      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+      const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sj = static_cast<int>((sw[j / 2] >> (16 * (j % 2))) & 0xffffu);
+        if (8 * g8 + j < kk && sj == m) r = wv[j];
+      }
+    }
     return r;
   };
   int ms[KP];
