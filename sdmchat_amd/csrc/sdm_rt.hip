@@ -365,6 +365,14 @@ __device__ __forceinline__ void store_vals(OutT* p, const float (&v)[n]) {
       return;
     }
   }
+  if constexpr (kBytes == 8 && sizeof(OutT) == 2) {
+    if ((reinterpret_cast<uintptr_t>(p) & 7u) == 0) {
+      *reinterpret_cast<uint2*>(p) =
+          make_uint2(static_cast<uint32_t>(from_f32<bf16_t>(v[0]).bits) | (static_cast<uint32_t>(from_f32<bf16_t>(v[1]).bits) << 16),
+                     static_cast<uint32_t>(from_f32<bf16_t>(v[2]).bits) | (static_cast<uint32_t>(from_f32<bf16_t>(v[3]).bits) << 16));
+      return;
+    }
+  }
 #pragma unroll
   for (int s = 0; s < n; ++s) p[s] = from_f32<OutT>(v[s]);
 }
@@ -560,20 +568,24 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
 //
 // One plan per (batch row, head, chunk) at a fixed stride in the workspace.  The scan reads its fixed-size part
 // straight into registers and stages its variable part into LDS (KP = pick pitch, PR = position record bytes):
-//   pos[64]          per position p: u16 slot[KP], f32 w[KP] (read picks and weights, pads 0), then u16 ri_begin,
-//                    u16 ri_end, f32 csum (the sum of p's in-chunk read coefficients), padding to PR bytes
+//   pos[64]          per position p: u16 slot[KP], f32 w[KP] (read picks and weights, pads 0), then the tail:
+//                    u16 ri_begin | u16 ri_end (its in-chunk contributions past the first kInline, in the variable
+//                    part), f32 csum (the sum of all its in-chunk read coefficients), u8 q[kInline] and u8 n_inline
+//                    (bytes 8..15), f32 c[kInline] (the first kInline contributions), padding to PR bytes
 //   wrec[64][KP]     write records of 8 bytes; distinct written slot u of the chunk is wrec[u % 64][u / 64] =
 //                    {slot | q0 << 16 | xo << 22, c0 | more << 31}: q0 is the slot's first writer in the chunk and
 //                    c0 = lam^(L-1-q0) * ww its coefficient; when later positions write the slot too (more = 1)
-//                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last
+//                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last.  Entries past the
+//                    chunk's n_wu slots are null records {M, 0}: the scratch row M with coefficient 0
 //   variable part    u32 {n_ri, n_wu, n_ext, bytes}; ext[n_ext] = {c = lam^(L-1-q) * ww, q | last << 31};
 //                    f32 ri_c[n_ri]; u8 ri_q[n_ri]
-// Read contribution e of position p (ri_begin <= e < ri_end): position q = ri_q[e] < p of the chunk wrote some of
-// p's read slots; ri_c[e] = the sum over those slots of wr * ww * lam^(p-1-q).  sizes[] holds the bytes of each
-// plan's variable part.
+// An in-chunk read contribution (q, c) of position p: position q < p of the chunk wrote some of p's read slots;
+// c = the sum over those slots of wr * ww * lam^(p-1-q).  Contributions run in ascending q.  sizes[] holds the
+// bytes of each plan's variable part.
+constexpr int kInline = 6;   // in-chunk contributions kept in the position record
 struct PlanGeom {
   int KP;
-  __host__ __device__ constexpr int pos_bytes() const { return (6 * KP + 16 + 15) / 16 * 16; }
+  __host__ __device__ constexpr int pos_bytes() const { return (6 * KP + 16 + 4 * kInline + 15) / 16 * 16; }
   __host__ __device__ constexpr int off_tail() const { return 6 * KP; }
   __host__ __device__ constexpr int off_wrec() const { return kChunk * pos_bytes(); }
   __host__ __device__ constexpr int off_var() const { return off_wrec() + 8 * kChunk * KP; }
@@ -709,7 +721,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
         mk[i] = i < kk ? wmask[ms[i]] & below : 0ull;
         touched |= mk[i];
       }
-      n_a = __builtin_popcountll(touched);
+      n_a = max(__builtin_popcountll(touched) - kInline, 0);   // contributions past the inline ones
     } else {
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
@@ -747,10 +759,19 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     a.sizes[plan_id] = bytes;
   }
   if (set == 1) {
-    // in-chunk contributions in ascending q, and their coefficient sum
+    // position record: slots, weights, then the tail
+    uint32_t rec[pg.pos_bytes() / 4];
+#pragma unroll
+    for (int i = 0; i < pg.pos_bytes() / 4; ++i) rec[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < KP; i += 2) rec[i / 2] = static_cast<uint32_t>(ms[i]) | (static_cast<uint32_t>(ms[i + 1]) << 16);
+#pragma unroll
+    for (int i = 0; i < KP; ++i) rec[KP / 2 + i] = __float_as_uint(ws[i]);
+    // in-chunk contributions in ascending q, and their coefficient sum: the first kInline into the record
     const int e0 = inc_a - n_a;
-    int k = e0;
+    int k = e0, j = 0;
     float csum = 0.f;
+    uint32_t qb[2] = {0u, 0u};
     while (touched) {
       const int q = __builtin_ctzll(touched);
       touched &= touched - 1ull;
@@ -759,26 +780,33 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
       for (int i = 0; i < KP; ++i)
         if ((mk[i] >> q) & 1ull) coef = fmaf(ws[i], wweight(q, ms[i]), coef);
       coef *= pw[p - 1 - q];
-      ri_q[k] = static_cast<unsigned char>(q);
-      ri_c[k] = coef;
+      if (j < kInline) {
+        qb[j / 4] |= static_cast<uint32_t>(q) << (8 * (j % 4));
+#pragma unroll
+        for (int t = 0; t < kInline; ++t)
+          if (t == j) rec[pg.off_tail() / 4 + 4 + t] = __float_as_uint(coef);
+        ++j;
+      } else {
+        ri_q[k] = static_cast<unsigned char>(q);
+        ri_c[k] = coef;
+        ++k;
+      }
       csum += coef;
-      ++k;
     }
-    // position record: slots, weights, then ri_begin | ri_end << 16, csum
-    uint32_t rec[pg.pos_bytes() / 4];
-#pragma unroll
-    for (int i = 0; i < pg.pos_bytes() / 4; ++i) rec[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < KP; i += 2) rec[i / 2] = static_cast<uint32_t>(ms[i]) | (static_cast<uint32_t>(ms[i + 1]) << 16);
-#pragma unroll
-    for (int i = 0; i < KP; ++i) rec[KP / 2 + i] = __float_as_uint(ws[i]);
     rec[pg.off_tail() / 4] = static_cast<uint32_t>(e0) | (static_cast<uint32_t>(inc_a) << 16);
     rec[pg.off_tail() / 4 + 1] = __float_as_uint(csum);
+    rec[pg.off_tail() / 4 + 2] = qb[0];
+    rec[pg.off_tail() / 4 + 3] = qb[1] | (static_cast<uint32_t>(j) << 24);
     uint4* dst = reinterpret_cast<uint4*>(plan + p * pg.pos_bytes());
 #pragma unroll
     for (int i = 0; i < pg.pos_bytes() / 16; ++i) dst[i] = make_uint4(rec[4 * i], rec[4 * i + 1], rec[4 * i + 2], rec[4 * i + 3]);
-  } else if (p < L) {
+  } else {
     uint2* wrec = reinterpret_cast<uint2*>(plan + pg.off_wrec());
+    // null records for group p's unused entries: the scratch row M, coefficient 0
+#pragma unroll
+    for (int k = 0; k < KP; ++k)
+      if (p + kChunk * k >= n_wu) wrec[p * KP + k] = make_uint2(static_cast<uint32_t>(M), 0u);
+    if (p >= L) return;
     int u = inc_a - n_a, e = inc_b - n_b;
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
@@ -824,11 +852,12 @@ constexpr int kScanThreads = 512;   // 64 positions x 8 lanes
 
 __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 
-// LDS of one scan workgroup: the slab A[M][CW], the write counts cnt[M], the current chunk's variable plan part, its
-// values s_v[64][CW] (staged in the input type: bfloat16 exactly), and fade powers pw[68].
-__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int v_bytes) {
-  return sizeof(float) * (static_cast<size_t>(M) * CW + pad4(M)) + PlanGeom{KP}.max_var() +
-         static_cast<size_t>(v_bytes) * kChunk * CW + sizeof(float) * 68;
+// LDS of one scan workgroup: the slab A[M + 1][CW] and the write counts cnt[M + 1] (row M is a scratch row that the
+// plan's null write records update), the current chunk's variable plan part, its values s_v[64][CW] in float32, and
+// fade powers pw[68].
+__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW) {
+  return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + PlanGeom{KP}.max_var() +
+         sizeof(float) * kChunk * CW + sizeof(float) * 68;
 }
 
 // CPL consecutive values (CPL = 4, 2, 1) from LDS in one access; bfloat16 values are converted.
@@ -876,11 +905,6 @@ __device__ __forceinline__ void lds_seg_store(float* p, const Seg<CPL>& r) {
   }
 }
 
-template <typename OutT, int CPL>
-__device__ __forceinline__ void store_seg(OutT* o, const float (&v)[CPL]) {
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) o[c] = from_f32<OutT>(v[c]);
-}
 
 // Sum over the 8 consecutive lanes of a group (DPP: swap neighbours, swap pairs, mirror the halves of 8).
 template <int CTRL>
@@ -906,8 +930,11 @@ __device__ __forceinline__ void lds_barrier() {
 // registers holding the next chunk's plan records, variable-part pieces and values until they are used
 template <int KP, int NV, typename VT, int CPL>
 struct ChunkRegs {
-  uint4 pos[PlanGeom{KP}.pos_bytes() / 16];
-  uint4 wrec[KP / 2];
+  uint4 pos[PlanGeom{KP}.pos_bytes() / 16];   // the group's position record
+  uint4 wrec[KP / 2];                         // the group's write records
+  uint2 own_w[KP / 8];                        // write records k = l8 + 8 b (the lane's count updates)
+  uint32_t own_slot[KP / 8];                  // read picks l8 + 8 b and their weights (the lane's count reads)
+  float own_wt[KP / 8];
   uint4 var[NV];
   VT v[CPL];
   int pieces;
@@ -920,12 +947,20 @@ __device__ __forceinline__ ChunkRegs<KP, NV, VT, CPL> fetch_chunk(const ScanArgs
   constexpr PlanGeom pg{KP};
   ChunkRegs<KP, NV, VT, CPL> r;
   const unsigned char* base = a.plans + (slab * a.n_chunks + c) * pg.stride();
-  const uint4* ps = reinterpret_cast<const uint4*>(base + p * pg.pos_bytes());
+  const unsigned char* prec = base + p * pg.pos_bytes();
+  const uint4* ps = reinterpret_cast<const uint4*>(prec);
 #pragma unroll
   for (int k = 0; k < pg.pos_bytes() / 16; ++k) r.pos[k] = ps[k];
-  const uint4* ws = reinterpret_cast<const uint4*>(base + pg.off_wrec() + p * KP * 8);
+  const uint2* wrow = reinterpret_cast<const uint2*>(base + pg.off_wrec()) + p * KP;
+  const uint4* ws = reinterpret_cast<const uint4*>(wrow);
 #pragma unroll
   for (int k = 0; k < KP / 2; ++k) r.wrec[k] = ws[k];
+#pragma unroll
+  for (int k = 0; k < KP / 8; ++k) {
+    r.own_w[k] = wrow[l8 + 8 * k];
+    r.own_slot[k] = reinterpret_cast<const uint16_t*>(prec)[l8 + 8 * k];
+    r.own_wt[k] = reinterpret_cast<const float*>(prec + 2 * KP)[l8 + 8 * k];
+  }
   const uint4* vs = reinterpret_cast<const uint4*>(base + pg.off_var());
   r.pieces = (bytes + 15) >> 4;
 #pragma unroll
@@ -948,8 +983,9 @@ __device__ __forceinline__ uint32_t u4_word(const uint4& q, int i) {
 //   S2 read   group = position: mu * lam^p * S_in rows of the read picks, plus the plan's in-chunk contributions
 //             of earlier positions' values; the mean read divides by mu * lam^p * sum(w * cnt) + the plan's in-chunk
 //             coefficient sum
-//   S3 write  group g takes the written slots g, g + 64, ...: their writers' faded values, divided by mu after the
-//             fade, are added to the slot's row (one owner per row: no atomics)
+//   S3 write  group g applies its KP write records (distinct slots, or the scratch row for null records): the
+//             writers' faded values, divided by mu after the fade, are added to the slot's row, and lane l8 adds
+//             record l8's coefficients to the slot's count (one owner per row: no atomics)
 // All sums run in fixed orders, so results are deterministic.
 template <int CW, int KP, typename VT, typename OutT>
 __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
@@ -959,29 +995,29 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   constexpr int NB = 8;                                                          // write records per batch
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int M = a.M;
-  float* A = lds;
-  float* cnt = A + static_cast<size_t>(M) * CW;
-  unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M));
-  VT* s_v = reinterpret_cast<VT*>(var + pg.max_var());
-  float* pw = reinterpret_cast<float*>(s_v + kChunk * CW);
+  float* A = lds;                                       // [M + 1][CW]
+  float* cnt = A + static_cast<size_t>(M + 1) * CW;     // [M + 1]
+  unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M + 1));
+  float* s_v = reinterpret_cast<float*>(var + pg.max_var());
+  float* pw = s_v + kChunk * CW;
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int p = tid >> 3;    // position (read) or slot group (write)
+  const int p = tid >> 3;    // position (read) or record group (write)
   const int l8 = tid & 7;    // column segment
   const int col0 = cg * CW;
   const int64_t slab = static_cast<int64_t>(b) * a.H + h;
   const float lam = a.decay[h];
   const int32_t* sizes = a.sizes + slab * a.n_chunks;
 
-  for (int i = tid; i < M * CW; i += kScanThreads) {
+  for (int i = tid; i < (M + 1) * CW; i += kScanThreads) {
     const int m = i / CW;
     const int c = i - m * CW;
-    A[i] = a.state_in_mem ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
+    A[i] = (a.state_in_mem && m < M) ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
   }
-  for (int m = tid; m < M; m += kScanThreads) cnt[m] = a.state_in_cnt ? a.state_in_cnt[slab * M + m] : 0.f;
+  for (int m = tid; m <= M; m += kScanThreads) cnt[m] = (a.state_in_cnt && m < M) ? a.state_in_cnt[slab * M + m] : 0.f;
   if (tid <= kChunk) {
     float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
     for (int e = 0; e < tid; ++e) v *= lam;
@@ -1002,8 +1038,12 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       const int piece = tid + k * kScanThreads;
       if (piece < nx.pieces) reinterpret_cast<uint4*>(var)[piece] = nx.var[k];
     }
+    {
+      float vv[CPL];
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) s_v[p * CW + CPL * l8 + k] = nx.v[k];
+      for (int k = 0; k < CPL; ++k) vv[k] = to_f32(nx.v[k]);
+      lds_seg_store<CPL>(&s_v[p * CW + CPL * l8], *reinterpret_cast<const Seg<CPL>*>(vv));
+    }
     // this chunk's records
     int m[KP];
     float w[KP];
@@ -1013,43 +1053,55 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       m[i] = static_cast<int>(i % 2 ? word >> 16 : word & 0xffffu);
       w[i] = __uint_as_float(u4_word(nx.pos[(2 * KP + 4 * i) / 16], ((2 * KP + 4 * i) % 16) / 4));
     }
-    const uint32_t tail0 = u4_word(nx.pos[pg.off_tail() / 16], (pg.off_tail() % 16) / 4);
-    const float csum = __uint_as_float(u4_word(nx.pos[pg.off_tail() / 16], (pg.off_tail() % 16) / 4 + 1));
+    auto tail = [&](int wd) { return u4_word(nx.pos[(pg.off_tail() + 4 * wd) / 16], ((pg.off_tail() + 4 * wd) % 16) / 4); };
+    const uint32_t tail0 = tail(0);
+    const float csum = __uint_as_float(tail(1));
     const int ri_b = tail0 & 0xffffu, ri_e = tail0 >> 16;
+    const uint32_t qw0 = tail(2), qw1 = tail(3);
+    const int n_in = qw1 >> 24;
+    int iq[kInline];
+    float ic[kInline];
+#pragma unroll
+    for (int t = 0; t < kInline; ++t) {
+      iq[t] = static_cast<int>(((t < 4 ? qw0 : qw1) >> (8 * (t % 4))) & 0xffu);
+      ic[t] = __uint_as_float(tail(4 + t));
+    }
     uint2 wr[KP];
 #pragma unroll
-    for (int k = 0; k < KP; ++k) wr[k] = make_uint2(u4_word(nx.wrec[k / 2], 2 * (k % 2)), u4_word(nx.wrec[k / 2], 2 * (k % 2) + 1));
+    for (int k = 0; k < KP; ++k)
+      wr[k] = make_uint2(u4_word(nx.wrec[k / 2], 2 * (k % 2)), u4_word(nx.wrec[k / 2], 2 * (k % 2) + 1));
+    uint2 own_w[KP / 8];
+    int own_slot[KP / 8];
+    float own_wt[KP / 8];
+#pragma unroll
+    for (int k = 0; k < KP / 8; ++k) {
+      own_w[k] = nx.own_w[k];
+      own_slot[k] = static_cast<int>(nx.own_slot[k]);
+      own_wt[k] = nx.own_wt[k];
+    }
     lds_barrier();
     if (c + 1 < a.n_chunks) {
       nx = fetch_chunk<KP, NV, VT, CPL>(a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
       next_bytes = c + 2 < a.n_chunks ? sizes[c + 2] : 0;
     }
     const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
-    const int n_ri = hdr[0], n_wu = hdr[1], n_ext = hdr[2];
+    const int n_ri = hdr[0], n_ext = hdr[2];
     const uint2* ext = reinterpret_cast<const uint2*>(var + 16);
     const float* ri_c = reinterpret_cast<const float*>(var + 16 + 8 * n_ext);
     const unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
     // S2: read
     if (p < L) {
       const float fin = mu * pw[p];
-      // the group's lanes share the count sum: lane l8 takes picks l8, l8 + 8
-      float cpart = 0.f;
+      float cpart = 0.f;   // the group's lanes share the count sum: lane l8 takes picks l8, l8 + 8
 #pragma unroll
-      for (int i0 = 0; i0 < KP; i0 += 8) {
-        int ml = m[i0];
-        float wl = w[i0];
+      for (int k = 0; k < KP / 8; ++k) cpart = fmaf(own_wt[k], cnt[own_slot[k]], cpart);
+      // one batch of reads: the rows of the read picks (pad picks carry weight 0) and the values of the in-chunk
+      // contributions kept in the record (unused entries read row 0 with coefficient 0)
+      Seg<CPL> x[KP], vi[kInline];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) {
-          if (l8 == i) {
-            ml = m[i0 + i];
-            wl = w[i0 + i];
-          }
-        }
-        cpart = fmaf(wl, cnt[ml], cpart);
-      }
-      Seg<CPL> x[KP];
+      for (int i = 0; i < KP; ++i) x[i] = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);
 #pragma unroll
-      for (int i = 0; i < KP; ++i) x[i] = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);   // pad picks carry weight 0
+      for (int t = 0; t < kInline; ++t) vi[t] = lds_seg<CPL>(&s_v[(t < n_in ? iq[t] : 0) * CW + CPL * l8]);
       float acc[CPL];
 #pragma unroll
       for (int k = 0; k < CPL; ++k) acc[k] = 0.f;
@@ -1060,7 +1112,13 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < CPL; ++k) acc[k] *= fin;
-      for (int e = ri_b; e < ri_e; e += 4) {   // in-chunk contributions, four at a time
+#pragma unroll
+      for (int t = 0; t < kInline; ++t) {
+        const float cf = t < n_in ? ic[t] : 0.f;
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) acc[k] = fmaf(cf, vi[t].v[k], acc[k]);
+      }
+      for (int e = ri_b; e < ri_e; e += 4) {   // the rest, from the variable part, four at a time
         float cf[4];
         Seg<CPL> vq[4];
 #pragma unroll
@@ -1082,71 +1140,64 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 #pragma unroll
         for (int k = 0; k < CPL; ++k) acc[k] *= inv;
       }
-      store_seg<OutT, CPL>(static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b) * a.T + c0 + p) * a.r_stride +
+      store_vals<CPL, OutT>(static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b) * a.T + c0 + p) * a.r_stride +
                                static_cast<int64_t>(h) * a.dh + col0 + CPL * l8, acc);
     }
     lds_barrier();
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
     float mu_new = mu * pw[L];
     if (!(mu_new >= kMuFloor)) {
-      for (int i = tid; i < M * CW; i += kScanThreads) A[i] *= mu_new;
-      for (int i = tid; i < M; i += kScanThreads) cnt[i] *= mu_new;
+      for (int i = tid; i < (M + 1) * CW; i += kScanThreads) A[i] *= mu_new;
+      for (int i = tid; i <= M; i += kScanThreads) cnt[i] *= mu_new;
       mu_new = 1.f;
       lds_barrier();
     }
-    // S3: write; group p takes the written slots p + 64 k, NB at a time (distinct slots: no conflicts)
+    // S3: write; group p applies records p + 64 k, NB at a time (distinct slots; null records hit the scratch row)
     {
       const float inv_mu = 1.f / mu_new;
 #pragma unroll
       for (int k0 = 0; k0 < KP; k0 += NB) {
-        if (p + kChunk * k0 < n_wu) {
-          int ms[NB];
-          float dc[NB];
-          Seg<CPL> x[NB], vq[NB];
+        Seg<CPL> x[NB], vq[NB];
+        float dc[NB];
 #pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            const bool ok = p + kChunk * (k0 + j) < n_wu;   // records past the chunk's last are not read
-            ms[j] = ok ? static_cast<int>(wr[k0 + j].x & 0xffffu) : 0;
-            const int q0 = ok ? static_cast<int>((wr[k0 + j].x >> 16) & 63u) : 0;
-            dc[j] = ok ? __uint_as_float(wr[k0 + j].y & 0x7fffffffu) * inv_mu : 0.f;
-            x[j] = lds_seg<CPL>(&A[ms[j] * CW + CPL * l8]);
-            vq[j] = lds_seg<CPL>(&s_v[q0 * CW + CPL * l8]);
-          }
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-#pragma unroll
-            for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(dc[j], vq[j].v[k], x[j].v[k]);
-            if (p + kChunk * (k0 + j) < n_wu && (wr[k0 + j].y & 0x80000000u)) {   // later writers of the slot
-              int e = wr[k0 + j].x >> 22;
-              uint2 t;
-              do {
-                t = ext[e++];
-                const float cf = __uint_as_float(t.x) * inv_mu;
-                const Seg<CPL> vx = lds_seg<CPL>(&s_v[(t.y & 63u) * CW + CPL * l8]);
-#pragma unroll
-                for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(cf, vx.v[k], x[j].v[k]);
-                dc[j] += cf;
-              } while (!(t.y & 0x80000000u));
-            }
-          }
-          // lane l8 updates the count of record k0 + l8
-          int mc = ms[0];
-          float dcc = dc[0];
-#pragma unroll
-          for (int j = 1; j < NB; ++j) {
-            if (l8 == j) {
-              mc = ms[j];
-              dcc = dc[j];
-            }
-          }
-          const bool cnt_ok = p + kChunk * (k0 + l8) < n_wu;
-          const float cold = cnt[mc];
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            if (p + kChunk * (k0 + j) < n_wu) lds_seg_store<CPL>(&A[ms[j] * CW + CPL * l8], x[j]);
-          }
-          if (cnt_ok) cnt[mc] = cold + dcc;
+        for (int j = 0; j < NB; ++j) {
+          const uint32_t rx = wr[k0 + j].x;
+          dc[j] = __uint_as_float(wr[k0 + j].y & 0x7fffffffu) * inv_mu;
+          x[j] = lds_seg<CPL>(&A[(rx & 0xffffu) * CW + CPL * l8]);
+          vq[j] = lds_seg<CPL>(&s_v[((rx >> 16) & 63u) * CW + CPL * l8]);
         }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+#pragma unroll
+          for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(dc[j], vq[j].v[k], x[j].v[k]);
+          if (wr[k0 + j].y & 0x80000000u) {   // later writers of the slot in this chunk
+            int e = wr[k0 + j].x >> 22;
+            uint2 t;
+            do {
+              t = ext[e++];
+              const float cf = __uint_as_float(t.x) * inv_mu;
+              const Seg<CPL> vx = lds_seg<CPL>(&s_v[(t.y & 63u) * CW + CPL * l8]);
+#pragma unroll
+              for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(cf, vx.v[k], x[j].v[k]);
+            } while (!(t.y & 0x80000000u));
+          }
+        }
+        // lane l8's count update for record k0 + l8
+        const uint2 ow = own_w[k0 / NB];
+        const int mc = static_cast<int>(ow.x & 0xffffu);
+        float dcc = __uint_as_float(ow.y & 0x7fffffffu) * inv_mu;
+        if (ow.y & 0x80000000u) {
+          int e = ow.x >> 22;
+          uint2 t;
+          do {
+            t = ext[e++];
+            dcc += __uint_as_float(t.x) * inv_mu;
+          } while (!(t.y & 0x80000000u));
+        }
+        const float cold = cnt[mc];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) lds_seg_store<CPL>(&A[(wr[k0 + j].x & 0xffffu) * CW + CPL * l8], x[j]);
+        cnt[mc] = cold + dcc;
       }
     }
     mu = mu_new;
@@ -1287,7 +1338,7 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   if (p->M > 65535) return set_err(SDM_RT_EUNSUPPORTED, "n_sub^2 = %d locations exceed 65535", p->M);
   p->cap = p->c1 <= 8 && p->kk <= 8 ? 8 : 16;
   p->pitch = (p->kk + 7) / 8 * 8;
-  if (scan_lds_bytes(p->M, p->pitch, 8, sizeof(float)) > kLdsBytes)
+  if (scan_lds_bytes(p->M, p->pitch, 8) > kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations do not fit a slab of 8 columns in LDS", p->M);
   if (plan_static_lds(p->pitch) + 8 * static_cast<size_t>(p->M) + 8 * static_cast<size_t>(p->n_sub) * p->half + 256 >
       kLdsBytes)
@@ -1402,7 +1453,7 @@ struct PlanLaunch {
 
 template <int CW, int KP, typename VT, typename OutT>
 int launch_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  const size_t lds = scan_lds_bytes(p.M, KP, CW, sizeof(VT));
+  const size_t lds = scan_lds_bytes(p.M, KP, CW);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<CW, KP, VT, OutT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(kLdsBytes));
@@ -1421,7 +1472,7 @@ int launch_scan_k(const Plan& p, const ScanArgs& a, hipStream_t st) {
 template <typename VT>
 int scan_columns(const Plan& p) {
   for (int cw : {32, 16, 8})
-    if (p.dh % cw == 0 && scan_lds_bytes(p.M, p.pitch, cw, sizeof(VT)) <= kLdsBytes) return cw;
+    if (p.dh % cw == 0 && scan_lds_bytes(p.M, p.pitch, cw) <= kLdsBytes) return cw;
   return 0;
 }
 
