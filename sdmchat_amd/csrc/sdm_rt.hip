@@ -386,17 +386,95 @@ __host__ __device__ constexpr int n_pairs(int cap) {
   return n;
 }
 
+// Offset selection keys of the matrix-core addressing (address_wave).  A cosine score s (|s| < 2) is keyed by the
+// double s + 6: one binade [4, 8) with a grid of 2^-50.  The low 19 mantissa bits are cleared (scores closer than
+// 2^-31 then tie) and hold fields that order equal values (larger field first) and name the candidate:
+//   half key        bits FS..FS+4: 31 - i (sub-key i); FS = 6 for the first half, 1 for the second
+//   ranked half key plus bits 15..18 (first half) or 11..14 (second): 15 - rank within the half
+// Every field bit is even, so the sum of a ranked first-half key and a ranked second-half key is exact (a multiple
+// of 2^-49 in [8, 16)): its value part is the sum of the two truncated scores + 12, and its low 18 bits are
+//   14..17: 15 - ra, 10..13: 15 - rb, 5..9: 31 - i1, 0..4: 31 - i2
+// so plain double order is (mean score descending, then (ra, rb) ascending), and the field names the slot.  Keys
+// of invalid candidates get the high word 0x00100000: a normal double below every real key.
+template <int FS>
+__device__ __forceinline__ double half_key(float s, int i) {
+  const unsigned long long b = __double_as_longlong(static_cast<double>(s) + 6.0);
+  const uint32_t lo = (static_cast<uint32_t>(b) & 0xfff80000u) | (static_cast<uint32_t>(31 - i) << FS);
+  return __longlong_as_double((b & 0xffffffff00000000ull) | lo);
+}
+__device__ __forceinline__ double key_or(double k, uint32_t bits) {
+  return __longlong_as_double(__double_as_longlong(k) | bits);
+}
+__device__ __forceinline__ double key_invalid(double k) {
+  return __longlong_as_double((0x00100000ull << 32) | (__double_as_longlong(k) & 0xffffffffull));
+}
+// the mean score of a grid key, to within 2^-32
+__device__ __forceinline__ float grid_score(double k) {
+  const double v = __longlong_as_double(__double_as_longlong(k) & ~0x3ffffull);
+  return static_cast<float>(fma(v, 0.5, -6.0));
+}
+
+// merges of sorted (descending) key lists: Batcher's odd-even merge of 2 + 2 and 4 + 4
+__device__ __forceinline__ void oe_merge22(double a0, double a1, double b0, double b1, double (&c)[4]) {
+  ce_desc(a0, b0);
+  ce_desc(a1, b1);
+  ce_desc(a1, b0);
+  c[0] = a0;
+  c[1] = a1;
+  c[2] = b0;
+  c[3] = b1;
+}
+__device__ __forceinline__ void oe_merge44(const double (&a)[4], const double (&b)[4], double (&c)[8]) {
+  double v[4], w[4];
+  oe_merge22(a[0], a[2], b[0], b[2], v);
+  oe_merge22(a[1], a[3], b[1], b[3], w);
+  c[0] = v[0];
+  c[7] = w[3];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    c[2 * i - 1] = fmax(w[i - 1], v[i]);
+    c[2 * i] = fmin(w[i - 1], v[i]);
+  }
+}
+// the 8 largest grid keys, sorted, of the pruned 8 x 8 grid ((ra + 1)(rb + 1) <= 8): its rows and its first column
+// are already sorted runs, merged as row 0 | (row 1 | column ra >= 4) | (row 2 | row 3)
+__device__ __forceinline__ void grid_top8(const double (&g0)[8], const double (&g1)[4], const double (&g2)[2],
+                                          const double (&g3)[2], const double (&gc)[4], double (&out)[8]) {
+  double m4[4], m8[8];
+  oe_merge22(g2[0], g2[1], g3[0], g3[1], m4);
+  oe_merge44(g1, gc, m8);
+#pragma unroll
+  for (int i = 4; i < 8; ++i) m8[i] = fmax(m8[i], m4[7 - i]);   // top 8 of m8 | m4, bitonic
+#pragma unroll
+  for (int j = 4; j > 0; j >>= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((i ^ j) > i) ce_desc(m8[i], m8[i ^ j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = g0[i];
+  merge_top_desc<8>(out, m8);
+}
+
+// 1 / max(sqrt(ss), 1e-12): hardware reciprocal square root and one Newton step
+__device__ __forceinline__ float inv_norm(float ss) {
+  const float x = fmaxf(ss, 1e-24f);
+  const float y = __builtin_amdgcn_rsqf(x);
+  return y * fmaf(-0.5f * x * y, y, 1.5f);
+}
+
 // Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
-// clamped; their lanes' outputs are unspecified), same results as address_one up to float rounding of the scores.
-// All 64 lanes of the wave must call it.
-template <int S, int CAP, typename InT>
+// clamped; their lanes' outputs are unspecified): the selection of address_one on offset keys, scores within 2^-31
+// of float rounding.  FULL: n_sub = 32 and c1 = kk = CAP (no candidate is masked).  All 64 lanes of the wave must
+// call it.
+template <int S, int CAP, typename InT, bool FULL>
 __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
                                              float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
   constexpr int HALF = 2 * S;
   const int l = threadIdx.x & 63;
   const int kb = l >> 5, jl = l & 31;
-  float hv[2][CAP];
-  int hx[2][CAP];
+  double hk[2][CAP];   // ranked half keys
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     // this half's loads first: the sub-key row, the address rows of both tiles, the address bias
@@ -418,8 +496,7 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
 #pragma unroll
       for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
       const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-      const float kinv = jl < g.n_sub ? 1.f / fmaxf(sqrtf(__uint_as_float(kp[0]) + __uint_as_float(kp[1])), 1e-12f)
-                                      : 0.f;
+      const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s) ka[s] *= kinv;
     }
@@ -433,8 +510,7 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
         ss = fmaf(zb[t][s], zb[t][s], ss);
       }
       const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-      ss = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);   // dims of both lane halves, same order in both
-      const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+      const float inv = inv_norm(__uint_as_float(pr[0]) + __uint_as_float(pr[1]));   // same order in both halves
       acc[t] = floatx16{};
 #pragma unroll
       for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[t][s] * inv, acc[t], 0, 0, 0);
@@ -445,56 +521,88 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]), false,
                                                        false);
       const int i0 = 8 * (r / 4) + (r % 4);
-      c[r] = fix_zero_key(sel_key<5, 5>(__uint_as_float(sw[0]), i0, i0));
-      c[16 + r] = fix_zero_key(sel_key<5, 5>(__uint_as_float(sw[1]), i0 + 4, i0 + 4));
-      if (i0 >= g.n_sub) c[r] = lowest_key(c[r]);   // sub-keys past n_sub are never picked
-      if (i0 + 4 >= g.n_sub) c[16 + r] = lowest_key(c[16 + r]);
+      if (hf == 0) {
+        c[r] = half_key<6>(__uint_as_float(sw[0]), i0);
+        c[16 + r] = half_key<6>(__uint_as_float(sw[1]), i0 + 4);
+      } else {
+        c[r] = half_key<1>(__uint_as_float(sw[0]), i0);
+        c[16 + r] = half_key<1>(__uint_as_float(sw[1]), i0 + 4);
+      }
+      if (!FULL) {   // sub-keys past n_sub are never picked
+        if (i0 >= g.n_sub) c[r] = key_invalid(c[r]);
+        if (i0 + 4 >= g.n_sub) c[16 + r] = key_invalid(c[16 + r]);
+      }
     }
     top_k_desc<CAP, 32>(c);
 #pragma unroll
-    for (int r = 0; r < CAP; ++r) sel_decode<5>(c[r], hv[hf][r], hx[hf][r]);
+    for (int r = 0; r < CAP; ++r) hk[hf][r] = key_or(c[r], static_cast<uint32_t>(15 - r) << (hf == 0 ? 15 : 11));
   }
-  // combine over the dominance-pruned grid (see address_one); tie index ra * 16 + rb orders like the flat grid index
-  // ra * c1 + rb, and the payload carries the slot's two sub-key ids
-  constexpr int NP = n_pairs(CAP);
-  constexpr int NPAD = (NP + CAP - 1) / CAP * CAP;
-  double pc[NPAD];
-  {
+  // combine over the dominance-pruned grid (see address_one)
+  auto cell = [&](int ra, int rb) {
+    const double k = hk[0][ra] + hk[1][rb];
+    if (FULL) return k;
+    return (ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk) ? k : key_invalid(k);
+  };
+  double pc[CAP];
+  if constexpr (CAP == 8) {
+    double g0[8], g1[4], g2[2], g3[2], gc[4];
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) g0[rb] = cell(0, rb);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) g1[rb] = cell(1, rb);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      g2[rb] = cell(2, rb);
+      g3[rb] = cell(3, rb);
+    }
+#pragma unroll
+    for (int ra = 4; ra < 8; ++ra) gc[ra - 4] = cell(ra, 0);
+    grid_top8(g0, g1, g2, g3, gc, pc);
+  } else {
+    constexpr int NP = n_pairs(CAP);
+    constexpr int NPAD = (NP + CAP - 1) / CAP * CAP;
+    double all[NPAD];
     int n = 0;
 #pragma unroll
     for (int ra = 0; ra < CAP; ++ra) {
 #pragma unroll
       for (int rb = 0; rb < CAP; ++rb) {
-        if ((ra + 1) * (rb + 1) <= CAP) {
-          const bool ok = ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk;
-          const double k = fix_zero_key(sel_key<8, 10>((hv[0][ra] + hv[1][rb]) * 0.5f, ra * 16 + rb,
-                                                       hx[0][ra] * 32 + hx[1][rb]));
-          pc[n++] = ok ? k : lowest_key(k);
-        }
+        if ((ra + 1) * (rb + 1) <= CAP) all[n++] = cell(ra, rb);
       }
     }
 #pragma unroll
-    for (int i = NP; i < NPAD; ++i) pc[i] = -INFINITY;
-  }
-  top_k_desc<CAP, NPAD>(pc);
-  float cv[CAP];
-  int ci[CAP];
+    for (int i = NP; i < NPAD; ++i) all[i] = -INFINITY;
+    top_k_desc<CAP, NPAD>(all);
 #pragma unroll
-  for (int p = 0; p < CAP; ++p) sel_decode<10>(pc[p], cv[p], ci[p]);
+    for (int p = 0; p < CAP; ++p) pc[p] = all[p];
+  }
+  float cv[CAP];
+  int si[CAP];
+#pragma unroll
+  for (int p = 0; p < CAP; ++p) {
+    cv[p] = grid_score(pc[p]);
+    const uint32_t f = static_cast<uint32_t>(__double_as_longlong(pc[p]));
+    if (FULL) {
+      si[p] = 1023 - static_cast<int>(f & 1023u);   // (31 - i1) * 32 + (31 - i2) = 1023 - slot
+    } else {
+      const int i1 = 31 - static_cast<int>((f >> 5) & 31u), i2 = 31 - static_cast<int>(f & 31u);
+      si[p] = min(i1 * g.n_sub + i2, g.n_sub * g.n_sub - 1);
+    }
+  }
   const float scale = expf(g.log_scale[h]);
   float e[CAP];
   const float x0 = cv[0] * scale;
   float sum = 0.f;
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
-    e[p] = (p < g.kk) ? expf(cv[p] * scale - x0) : 0.f;
+    e[p] = (FULL || p < g.kk) ? expf(cv[p] * scale - x0) : 0.f;
     sum += e[p];
   }
   const float wscale = gate / sum;
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
-    const bool live = p < g.kk;
-    slot[p] = live ? (ci[p] >> 5) * g.n_sub + (ci[p] & 31) : 0;
+    const bool live = FULL || p < g.kk;
+    slot[p] = live ? si[p] : 0;
     w[p] = live ? e[p] * wscale : 0.f;
     score[p] = live ? cv[p] : 0.f;
   }
@@ -525,9 +633,10 @@ __device__ __forceinline__ void stage_keys(const AddrGeom& g, int h, float* kn, 
   }
 }
 
-// sdm_rt_address: one thread per (token, head).  Grid: x = token tiles of 64, y = head.  MF: the tile is addressed
-// by the wave on the matrix cores (address_wave), else per thread with the sub-keys staged in LDS (address_one).
-template <int HALF, int CAP, typename InT, bool MF>
+// sdm_rt_address: one thread per (token, head).  Grid: x = token tiles of 64, y = head.  MODE 1 and 2: the tile is
+// addressed by the wave on the matrix cores (address_wave; 2 = no masked candidate), MODE 0: per thread with the
+// sub-keys staged in LDS (address_one).
+template <int HALF, int CAP, typename InT, int MODE>
 __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   extern __shared__ float kn[];   // [2][n_sub][HALF] (per-thread path)
   const int h = blockIdx.y;
@@ -538,8 +647,8 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
       (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
   int slot[CAP];
   float w[CAP], sc[CAP];
-  if constexpr (MF) {
-    address_wave<HALF / 2, CAP, InT>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
+  if constexpr (MODE > 0) {
+    address_wave<HALF / 2, CAP, InT, MODE == 2>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
                                      static_cast<int>(min<int64_t>(64, N - n0)), gate, slot, w, sc);
     if (n >= N) return;
   } else {
@@ -623,10 +732,10 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 }
 
 // plan_kernel: block (chunk, head, batch row), 128 threads: wave 0 addresses the write keys of the chunk's positions,
-// wave 1 the read queries (MF: on the matrix cores, else per thread); then the writers of every slot are marked in
+// wave 1 the read queries (MODE 1, 2: on the matrix cores, MODE 0: per thread); then the writers of every slot are marked in
 // 64-bit masks, each position's read contributions and each written slot's writer list are found, counted,
 // prefix-summed within the wave and written out.
-template <int HALF, int KP, typename InT, bool MF>
+template <int HALF, int KP, typename InT, int MODE>
 __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   constexpr PlanGeom pg{KP};
   const int c = blockIdx.x;
@@ -648,14 +757,14 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   extern __shared__ unsigned long long wmask[];   // [M], then (per-thread path) the head's sub-keys [2][n_sub][HALF]
   float* kn = reinterpret_cast<float*>(wmask + M);
 
-  if constexpr (!MF) stage_keys<HALF>(a.g, h, kn, tid, 128);
+  if constexpr (MODE == 0) stage_keys<HALF>(a.g, h, kn, tid, 128);
   for (int i = tid; i < M; i += 128) wmask[i] = 0ull;
   if (tid <= kChunk) {
     float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
     for (int e = 0; e < tid; ++e) v *= lam;
     pw[tid] = v;
   }
-  if constexpr (!MF) __syncthreads();
+  if constexpr (MODE == 0) __syncthreads();
 
   // addressing
   {
@@ -667,8 +776,8 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
                            : 1.f;
     const InT* zb = static_cast<const InT*>(set == 0 ? a.kz : a.qz);
     const int64_t zs = set == 0 ? a.kz_stride : a.qz_stride;
-    if constexpr (MF) {
-      address_wave<HALF / 2, KP, InT>(a.g, h, zb + row0 * zs, zs, L, gate, slot, w, sc);
+    if constexpr (MODE > 0) {
+      address_wave<HALF / 2, KP, InT, MODE == 2>(a.g, h, zb + row0 * zs, zs, L, gate, slot, w, sc);
     } else if (p < L) {
       address_one<HALF, KP, InT>(a.g, h, kn, zb + (row0 + p) * zs + static_cast<int64_t>(h) * 2 * HALF, gate, slot, w,
                                  sc);
@@ -1408,46 +1517,49 @@ int by_half(int half, Args&&... args) {
 // the matrix-core addressing covers half widths 8, 16, 32 and up to 32 sub-keys per half
 constexpr bool mf_half(int half) { return half == 8 || half == 16 || half == 32; }
 bool use_mf(const Plan& p) { return mf_half(p.half) && p.n_sub <= 32; }
+// no masked candidate: 32 sub-keys per half and 8 picks from the top 8 of each half
+bool full_grid(const Plan& p) { return use_mf(p) && p.n_sub == 32 && p.c1 == 8 && p.kk == 8; }
 
 template <int HALF, typename InT>
 struct AddressLaunch {
-  template <int CAP, bool MF>
+  template <int CAP, int MODE>
   static void go(const Plan& p, const AddrArgs& a, hipStream_t st) {
     const int64_t N = static_cast<int64_t>(p.B) * p.T;
     dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H);
-    const size_t lds = MF ? 0 : sizeof(float) * 2 * p.n_sub * HALF;
-    hipLaunchKernelGGL((address_kernel<HALF, CAP, InT, MF>), grid, dim3(64), lds, st, a);
+    const size_t lds = MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF;
+    hipLaunchKernelGGL((address_kernel<HALF, CAP, InT, MODE>), grid, dim3(64), lds, st, a);
   }
   static int run(const Plan& p, const AddrArgs& a, hipStream_t st) {
     if constexpr (mf_half(HALF)) {
       if (use_mf(p)) {
-        if (p.cap == 8) go<8, true>(p, a, st);
-        else go<16, true>(p, a, st);
+        if (full_grid(p)) go<8, 2>(p, a, st);
+        else if (p.cap == 8) go<8, 1>(p, a, st);
+        else go<16, 1>(p, a, st);
         return check_launch("address");
       }
     }
-    if (p.cap == 8) go<8, false>(p, a, st);
-    else go<16, false>(p, a, st);
+    if (p.cap == 8) go<8, 0>(p, a, st);
+    else go<16, 0>(p, a, st);
     return check_launch("address");
   }
 };
 
 template <int HALF, typename InT>
 struct PlanLaunch {
-  template <int KP, bool MF>
+  template <int KP, int MODE>
   static int go(const Plan& p, const PlanArgs& a, hipStream_t st) {
     dim3 grid(p.n_chunks, p.H, p.B);
-    const size_t lds = sizeof(unsigned long long) * p.M + (MF ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
-    static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MF>));
+    const size_t lds = sizeof(unsigned long long) * p.M + (MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
+    static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MODE>));
     if (!ok) return lds_err("plan");
-    hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MF>), grid, dim3(128), lds, st, a);
+    hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MODE>), grid, dim3(128), lds, st, a);
     return check_launch("plan");
   }
   static int run(const Plan& p, const PlanArgs& a, hipStream_t st) {
     if constexpr (mf_half(HALF)) {
-      if (use_mf(p)) return p.pitch == 8 ? go<8, true>(p, a, st) : go<16, true>(p, a, st);
+      if (use_mf(p)) return full_grid(p) ? go<8, 2>(p, a, st) : p.pitch == 8 ? go<8, 1>(p, a, st) : go<16, 1>(p, a, st);
     }
-    return p.pitch == 8 ? go<8, false>(p, a, st) : go<16, false>(p, a, st);
+    return p.pitch == 8 ? go<8, 0>(p, a, st) : go<16, 0>(p, a, st);
   }
 };
 
