@@ -397,8 +397,8 @@ __host__ __device__ constexpr int n_pairs(int cap) {
 // so plain double order is (mean score descending, then (ra, rb) ascending), and the field names the slot.  Keys
 // of invalid candidates get the high word 0x00100000: a normal double below every real key.
 template <int FS>
-__device__ __forceinline__ double half_key(float s, int i) {
-  const unsigned long long b = __double_as_longlong(static_cast<double>(s) + 6.0);
+__device__ __forceinline__ double half_key(float a, double inv, int i) {   // s = a * inv
+  const unsigned long long b = __double_as_longlong(fma(static_cast<double>(a), inv, 6.0));
   const uint32_t lo = (static_cast<uint32_t>(b) & 0xfff80000u) | (static_cast<uint32_t>(31 - i) << FS);
   return __longlong_as_double((b & 0xffffffff00000000ull) | lo);
 }
@@ -464,57 +464,198 @@ __device__ __forceinline__ float inv_norm(float ss) {
   return y * fmaf(-0.5f * x * y, y, 1.5f);
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// 8 consecutive bfloat16 values at p as raw bits: one 16-byte load when p is 16-byte aligned
+__device__ __forceinline__ uint4 load_raw8(const bf16_t* p) {
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) return *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = p[2 * e].bits | (static_cast<uint32_t>(p[2 * e + 1].bits) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// a and b rounded to bfloat16 (nearest even), packed a | b << 16
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Cosine scores of one half (hf) of the wave's 64 addresses against the head's sub-keys of that half, up to one
+// factor per address: lane l, tile t: acc[t][r] * inv[t] = cos(sub-key 8(r/4) + 4(l/32) + r%4, address row
+// 32t + l%32), inv[t] = 1 / max(|z + addr_b|, 1e-12) of that row.  Sub-key rows past n_sub score 0.  Rows past
+// `rows` are clamped.
+
+// float32 matrix cores: lane l feeds dims (l/32) * HALF/2 ... (l/32) * HALF/2 + HALF/2 - 1 of sub-key row l%32 and
+// of both address rows
+template <int HALF, typename InT, bool FULL>
+__device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf, const InT* z0, int64_t zstride,
+                                                int rows, floatx16 (&acc)[2], float (&inv)[2]) {
+  constexpr int S = HALF / 2;
+  const int l = threadIdx.x & 63;
+  const int kb = l >> 5, jl = l & 31;
+  float ka[S], zb[2][S], ab[S];
+  load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = min(32 * t + jl, rows - 1);
+    load_vals<S, InT>(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + hf * HALF + kb * S, zb[t]);
+  }
+  if (g.addr_b) {
+    load_vals<S, float>(g.addr_b + h * 2 * HALF + hf * HALF + kb * S, ab);
+  } else {
+#pragma unroll
+    for (int s = 0; s < S; ++s) ab[s] = 0.f;
+  }
+  {   // unit-normalised sub-key row
+    float ks = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
+    const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
+    const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) ka[s] *= kinv;
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      zb[t][s] += ab[s];
+      ss = fmaf(zb[t][s], zb[t][s], ss);
+    }
+    const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    inv[t] = inv_norm(__uint_as_float(pr[0]) + __uint_as_float(pr[1]));   // same order in both lane halves
+    acc[t] = floatx16{};
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[t][s], acc[t], 0, 0, 0);
+  }
+}
+
+// bfloat16 matrix cores (bfloat16 addresses, HALF a multiple of 8): each unit sub-key is split into three bfloat16
+// terms k = k0 + k1 + k2 + r (k0 the nearest bfloat16 to k, k1 to k - k0, k2 to k - k0 - k1; |r| <= 2^-27 |k|), the
+// address values are bfloat16 already, so every product is exact in the float32 accumulation.  The address bias
+// enters through the accumulator's start value c_i = k_i . addr_b (one float32 matrix step: c_i x 1) and through
+// inv.  Lane l feeds dims 16q + 8(l/32) + e (e < 8) of sub-key row l%32 and of both address rows (HALF = 8: lanes
+// 32..63 feed zeros).
+template <int HALF, bool FULL>
+__device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
+                                                 int rows, floatx16 (&acc)[2], float (&inv)[2]) {
+  static_assert(HALF % 8 == 0, "bfloat16 scoring feeds 8 dims per lane");
+  constexpr int Q = (HALF + 15) / 16;
+  const int l = threadIdx.x & 63;
+  const int kb = l >> 5, jl = l & 31;
+  const bool has = HALF >= 16 || kb == 0;
+  const int d0 = hf * HALF + 8 * kb;   // first dim of the address this lane feeds
+  float ka[Q][8], ab[Q][8];
+  uint4 zr[2][Q];
+  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + 8 * kb;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = min(32 * t + jl, rows - 1);
+      zr[t][q] = has ? load_raw8(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + d0 + 16 * q)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (has) {
+      load_vals<8, float>(krow + 16 * q, ka[q]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ka[q][e] = 0.f;
+    }
+    if (g.addr_b && has) {
+      load_vals<8, float>(g.addr_b + h * 2 * HALF + d0 + 16 * q, ab[q]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ab[q][e] = 0.f;
+    }
+  }
+  {   // unit-normalised sub-key row
+    float ks = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ks = fmaf(ka[q][e], ka[q][e], ks);
+    const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
+    const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ka[q][e] *= kinv;
+  }
+  floatx16 init = {};
+  if (g.addr_b) {
+    float cp = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cp = fmaf(ka[q][e], ab[q][e], cp);
+    const auto cw = __builtin_amdgcn_permlane32_swap(__float_as_uint(cp), __float_as_uint(cp), false, false);
+    const float c = __uint_as_float(cw[0]) + __uint_as_float(cw[1]);
+    init = __builtin_amdgcn_mfma_f32_32x32x2f32(kb == 0 ? c : 0.f, kb == 0 ? 1.f : 0.f, init, 0, 0, 0);
+  }
+  uint32_t kt[3][Q][4];   // the three bfloat16 terms, packed in pairs
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float x0 = ka[q][2 * e2], x1 = ka[q][2 * e2 + 1];
+#pragma unroll
+      for (int term = 0; term < 3; ++term) {
+        const uint32_t p = pack_bf16(x0, x1);
+        kt[term][q][e2] = p;
+        x0 -= __uint_as_float(p << 16);   // exact
+        x1 -= __uint_as_float(p & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const uint32_t wd[4] = {zr[t][q].x, zr[t][q].y, zr[t][q].z, zr[t][q].w};
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const float v0 = __uint_as_float(wd[e2] << 16) + ab[q][2 * e2];
+        const float v1 = __uint_as_float(wd[e2] & 0xffff0000u) + ab[q][2 * e2 + 1];
+        ss = fmaf(v0, v0, ss);
+        ss = fmaf(v1, v1, ss);
+      }
+    }
+    const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    inv[t] = inv_norm(__uint_as_float(pr[0]) + __uint_as_float(pr[1]));
+    acc[t] = init;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+#pragma unroll
+      for (int term = 2; term >= 0; --term) {
+        const uint4 kq = make_uint4(kt[term][q][0], kt[term][q][1], kt[term][q][2], kt[term][q][3]);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kq),
+                                                         __builtin_bit_cast(bf16x8, zr[t][q]), acc[t], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
 // clamped; their lanes' outputs are unspecified): the selection of address_one on offset keys, scores within 2^-31
 // of float rounding.  FULL: n_sub = 32 and c1 = kk = CAP (no candidate is masked).  All 64 lanes of the wave must
 // call it.
-template <int S, int CAP, typename InT, bool FULL>
+template <int HALF, int CAP, typename InT, bool FULL>
 __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
                                              float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
-  constexpr int HALF = 2 * S;
-  const int l = threadIdx.x & 63;
-  const int kb = l >> 5, jl = l & 31;
+  const int kb = (threadIdx.x & 63) >> 5;
   double hk[2][CAP];   // ranked half keys
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    // this half's loads first: the sub-key row, the address rows of both tiles, the address bias
-    float ka[S], zb[2][S], ab[S];
-    load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int row = min(32 * t + jl, rows - 1);
-      load_vals<S, InT>(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + hf * HALF + kb * S, zb[t]);
-    }
-    if (g.addr_b) {
-      load_vals<S, float>(g.addr_b + h * 2 * HALF + hf * HALF + kb * S, ab);
-    } else {
-#pragma unroll
-      for (int s = 0; s < S; ++s) ab[s] = 0.f;
-    }
-    {   // sub-key row jl, dims kb * S .. kb * S + S - 1, unit-normalised over the row
-      float ks = 0.f;
-#pragma unroll
-      for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
-      const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-      const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
-#pragma unroll
-      for (int s = 0; s < S; ++s) ka[s] *= kinv;
-    }
     floatx16 acc[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float ss = 0.f;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        zb[t][s] += ab[s];
-        ss = fmaf(zb[t][s], zb[t][s], ss);
-      }
-      const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-      const float inv = inv_norm(__uint_as_float(pr[0]) + __uint_as_float(pr[1]));   // same order in both halves
-      acc[t] = floatx16{};
-#pragma unroll
-      for (int s = 0; s < S; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[s], zb[t][s] * inv, acc[t], 0, 0, 0);
-    }
+    float inv[2];
+    if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv);
+    else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv);
+    // after the swap below lane l holds every score of address row l
+    const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
     double c[32];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -522,11 +663,11 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
                                                        false);
       const int i0 = 8 * (r / 4) + (r % 4);
       if (hf == 0) {
-        c[r] = half_key<6>(__uint_as_float(sw[0]), i0);
-        c[16 + r] = half_key<6>(__uint_as_float(sw[1]), i0 + 4);
+        c[r] = half_key<6>(__uint_as_float(sw[0]), dinv, i0);
+        c[16 + r] = half_key<6>(__uint_as_float(sw[1]), dinv, i0 + 4);
       } else {
-        c[r] = half_key<1>(__uint_as_float(sw[0]), i0);
-        c[16 + r] = half_key<1>(__uint_as_float(sw[1]), i0 + 4);
+        c[r] = half_key<1>(__uint_as_float(sw[0]), dinv, i0);
+        c[16 + r] = half_key<1>(__uint_as_float(sw[1]), dinv, i0 + 4);
       }
       if (!FULL) {   // sub-keys past n_sub are never picked
         if (i0 >= g.n_sub) c[r] = key_invalid(c[r]);
@@ -648,7 +789,7 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   int slot[CAP];
   float w[CAP], sc[CAP];
   if constexpr (MODE > 0) {
-    address_wave<HALF / 2, CAP, InT, MODE == 2>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
+    address_wave<HALF, CAP, InT, MODE == 2>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
                                      static_cast<int>(min<int64_t>(64, N - n0)), gate, slot, w, sc);
     if (n >= N) return;
   } else {
@@ -777,7 +918,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     const InT* zb = static_cast<const InT*>(set == 0 ? a.kz : a.qz);
     const int64_t zs = set == 0 ? a.kz_stride : a.qz_stride;
     if constexpr (MODE > 0) {
-      address_wave<HALF / 2, KP, InT, MODE == 2>(a.g, h, zb + row0 * zs, zs, L, gate, slot, w, sc);
+      address_wave<HALF, KP, InT, MODE == 2>(a.g, h, zb + row0 * zs, zs, L, gate, slot, w, sc);
     } else if (p < L) {
       address_one<HALF, KP, InT>(a.g, h, kn, zb + (row0 + p) * zs + static_cast<int64_t>(h) * 2 * HALF, gate, slot, w,
                                  sc);
