@@ -825,8 +825,9 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
 //   wrec[64][KP]     write records of 8 bytes; distinct written slot u of the chunk is wrec[u % 64][u / 64] =
 //                    {slot | q0 << 16 | xo << 22, c0 | more << 31}: q0 is the slot's first writer in the chunk and
 //                    c0 = lam^(L-1-q0) * ww its coefficient; when later positions write the slot too (more = 1)
-//                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last.  Entries past the
-//                    chunk's n_wu slots are null records {M, 0}: the scratch row M with coefficient 0
+//                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last.  Slots with later
+//                    writers come first.  Entries past the chunk's n_wu slots are null records {M, 0}: they read
+//                    row M (always zero) and write nothing
 //   variable part    u32 {n_ri, n_wu, n_ext, bytes}; ext[n_ext] = {c = lam^(L-1-q) * ww, q | last << 31};
 //                    f32 ri_c[n_ri]; u8 ri_q[n_ri]
 // An in-chunk read contribution (q, c) of position p: position q < p of the chunk wrote some of p's read slots;
@@ -963,6 +964,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   unsigned long long mk[KP];           // read side: the earlier writers of each read slot
   unsigned long long touched = 0ull;   // read side: every earlier position contributing to this one
   int n_a = 0, n_b = 0;                // read side: contributions; write side: distinct slots owned, later writers
+  int n_m = 0;                         // write side: owned slots with later writers
   if (p < L) {
     if (set == 1) {
       const unsigned long long below = (1ull << p) - 1ull;
@@ -978,8 +980,10 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
         if (j < kk) {
           const unsigned long long mm = wmask[ms[j]];
           if (__builtin_ctzll(mm) == p) {
+            const int later = __builtin_popcountll(mm) - 1;
             ++n_a;
-            n_b += __builtin_popcountll(mm) - 1;
+            n_b += later;
+            n_m += later > 0;
           }
         }
       }
@@ -987,12 +991,14 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   }
   const int inc_a = wave_incl_scan(n_a, p);
   const int inc_b = wave_incl_scan(n_b, p);
+  const int inc_m = wave_incl_scan(n_m, p);
   if (p == 63) {
     if (set == 1) {
       tot[0] = inc_a;
     } else {
       tot[1] = inc_a;
       tot[2] = inc_b;
+      tot[3] = inc_m;
     }
   }
   __syncthreads();
@@ -1052,12 +1058,14 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     for (int i = 0; i < pg.pos_bytes() / 16; ++i) dst[i] = make_uint4(rec[4 * i], rec[4 * i + 1], rec[4 * i + 2], rec[4 * i + 3]);
   } else {
     uint2* wrec = reinterpret_cast<uint2*>(plan + pg.off_wrec());
-    // null records for group p's unused entries: the scratch row M, coefficient 0
+    // null records for group p's unused entries: row M, coefficient 0
 #pragma unroll
     for (int k = 0; k < KP; ++k)
       if (p + kChunk * k >= n_wu) wrec[p * KP + k] = make_uint2(static_cast<uint32_t>(M), 0u);
     if (p >= L) return;
-    int u = inc_a - n_a, e = inc_b - n_b;
+    // slots with later writers take the lowest indexes (records k = 0, 1, ...), so the scan's walks of the later
+    // writers gather in the first record batches
+    int u_m = inc_m - n_m, u_s = tot[3] + (inc_a - inc_m) - (n_a - n_m), e = inc_b - n_b;
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
       if (j >= kk) break;
@@ -1066,9 +1074,9 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
       if (__builtin_ctzll(mm) != p) continue;   // p is the slot's first writer in the chunk
       mm &= mm - 1ull;
       const uint32_t cw = __float_as_uint(pw[L - 1 - p] * ws[j]) | (mm ? 0x80000000u : 0u);
+      const int u = mm ? u_m++ : u_s++;
       wrec[(u & 63) * KP + (u >> 6)] =
           make_uint2(static_cast<uint32_t>(m) | (static_cast<uint32_t>(p) << 16) | (static_cast<uint32_t>(e) << 22), cw);
-      ++u;
       while (mm) {
         const int q = __builtin_ctzll(mm);
         mm &= mm - 1ull;
@@ -1102,12 +1110,12 @@ constexpr int kScanThreads = 512;   // 64 positions x 8 lanes
 
 __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 
-// LDS of one scan workgroup: the slab A[M + 1][CW] and the write counts cnt[M + 1] (row M is a scratch row that the
-// plan's null write records update), the current chunk's variable plan part, its values s_v[64][CW] in float32, and
-// fade powers pw[68].
-__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW) {
+// LDS of one scan workgroup: the slab A[M + 1][CW] and the write counts cnt[M + 1] (row M, which the plan's null
+// write records read, stays zero), the current chunk's variable plan part, its values s_v[64][CW] in float32, fade
+// powers pw[68] and the variable-part sizes of all n_chunks plans.
+__host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int n_chunks) {
   return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + PlanGeom{KP}.max_var() +
-         sizeof(float) * kChunk * CW + sizeof(float) * 68;
+         sizeof(float) * kChunk * CW + sizeof(float) * 68 + sizeof(int32_t) * pad4(n_chunks);
 }
 
 // CPL consecutive values (CPL = 4, 2, 1) from LDS in one access; bfloat16 values are converted.
@@ -1168,6 +1176,12 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// 1 / x for normal positive x: hardware reciprocal and one Newton step (within an ulp or so)
+__device__ __forceinline__ float fast_rcp(float x) {
+  const float y = __builtin_amdgcn_rcpf(x);
+  return fmaf(y, fmaf(-x, y, 1.f), y);
+}
+
 // Workgroup barrier that orders LDS accesses only: the scan shares nothing else between its threads, so global loads
 // issued ahead (the next chunk's plan and values) and global stores (read-outs) need not complete at a barrier.
 __device__ __forceinline__ void lds_barrier() {
@@ -1190,37 +1204,46 @@ struct ChunkRegs {
   int pieces;
 };
 
-// Loads are unconditional (indexes clamped into the plan), so the compiler keeps them in flight across a chunk.
-template <int KP, int NV, typename VT, int CPL>
-__device__ __forceinline__ ChunkRegs<KP, NV, VT, CPL> fetch_chunk(const ScanArgs& a, int64_t slab, int b, int h,
-                                                                  int col0, int c, int bytes, int tid, int p, int l8) {
+// The next chunk's loads, in three parts (PART 0: the group's position record; 1: its write records and the lane's
+// count records; 2: the variable-part pieces and the values), issued in two phases of the current chunk so the vector
+// memory path streams them while the current chunk works on LDS.  Record and value loads are
+// unconditional (indexes clamped into the plan), so the compiler keeps them in flight; variable-part pieces past the
+// plan's size are not loaded.
+template <int PART, int KP, int NV, typename VT, int CPL>
+__device__ __forceinline__ void fetch_chunk(ChunkRegs<KP, NV, VT, CPL>& r, const ScanArgs& a, int64_t slab, int b,
+                                            int h, int col0, int c, int bytes, int tid, int p, int l8) {
   constexpr PlanGeom pg{KP};
-  ChunkRegs<KP, NV, VT, CPL> r;
   const unsigned char* base = a.plans + (slab * a.n_chunks + c) * pg.stride();
   const unsigned char* prec = base + p * pg.pos_bytes();
-  const uint4* ps = reinterpret_cast<const uint4*>(prec);
+  if constexpr (PART == 0) {
+    const uint4* ps = reinterpret_cast<const uint4*>(prec);
 #pragma unroll
-  for (int k = 0; k < pg.pos_bytes() / 16; ++k) r.pos[k] = ps[k];
-  const uint2* wrow = reinterpret_cast<const uint2*>(base + pg.off_wrec()) + p * KP;
-  const uint4* ws = reinterpret_cast<const uint4*>(wrow);
+    for (int k = 0; k < pg.pos_bytes() / 16; ++k) r.pos[k] = ps[k];
+  } else if constexpr (PART == 1) {
+    const uint2* wrow = reinterpret_cast<const uint2*>(base + pg.off_wrec()) + p * KP;
+    const uint4* ws = reinterpret_cast<const uint4*>(wrow);
 #pragma unroll
-  for (int k = 0; k < KP / 2; ++k) r.wrec[k] = ws[k];
+    for (int k = 0; k < KP / 2; ++k) r.wrec[k] = ws[k];
 #pragma unroll
-  for (int k = 0; k < KP / 8; ++k) {
-    r.own_w[k] = wrow[l8 + 8 * k];
-    r.own_slot[k] = reinterpret_cast<const uint16_t*>(prec)[l8 + 8 * k];
-    r.own_wt[k] = reinterpret_cast<const float*>(prec + 2 * KP)[l8 + 8 * k];
+    for (int k = 0; k < KP / 8; ++k) {
+      r.own_w[k] = wrow[l8 + 8 * k];
+      r.own_slot[k] = reinterpret_cast<const uint16_t*>(prec)[l8 + 8 * k];
+      r.own_wt[k] = reinterpret_cast<const float*>(prec + 2 * KP)[l8 + 8 * k];
+    }
+  } else {
+    const uint4* vs = reinterpret_cast<const uint4*>(base + pg.off_var());
+    r.pieces = (bytes + 15) >> 4;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int piece = tid + k * kScanThreads;
+      r.var[k] = piece < r.pieces ? vs[piece] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const int row = min(c * kChunk + p, a.T - 1);
+    const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + row) * a.v_stride +
+                     static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) r.v[k] = vrow[k];
   }
-  const uint4* vs = reinterpret_cast<const uint4*>(base + pg.off_var());
-  r.pieces = (bytes + 15) >> 4;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) r.var[k] = vs[min(tid + k * kScanThreads, r.pieces - 1)];
-  const int row = min(c * kChunk + p, a.T - 1);
-  const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + row) * a.v_stride +
-                   static_cast<int64_t>(h) * a.dh + col0 + CPL * l8;
-#pragma unroll
-  for (int k = 0; k < CPL; ++k) r.v[k] = vrow[k];
-  return r;
 }
 
 __device__ __forceinline__ uint32_t u4_word(const uint4& q, int i) {
@@ -1233,7 +1256,7 @@ __device__ __forceinline__ uint32_t u4_word(const uint4& q, int i) {
 //   S2 read   group = position: mu * lam^p * S_in rows of the read picks, plus the plan's in-chunk contributions
 //             of earlier positions' values; the mean read divides by mu * lam^p * sum(w * cnt) + the plan's in-chunk
 //             coefficient sum
-//   S3 write  group g applies its KP write records (distinct slots, or the scratch row for null records): the
+//   S3 write  group g applies its KP write records (distinct slots; null records write nothing): the
 //             writers' faded values, divided by mu after the fade, are added to the slot's row, and lane l8 adds
 //             record l8's coefficients to the slot's count (one owner per row: no atomics)
 // All sums run in fixed orders, so results are deterministic.
@@ -1250,6 +1273,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M + 1));
   float* s_v = reinterpret_cast<float*>(var + pg.max_var());
   float* pw = s_v + kChunk * CW;
+  int32_t* s_sizes = reinterpret_cast<int32_t*>(pw + 68);   // read from LDS: a scalar load in the loop would hold up
+                                                            // every LDS wait behind a memory round trip
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
@@ -1268,6 +1293,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     A[i] = (a.state_in_mem && m < M) ? a.state_in_mem[(slab * M + m) * a.dh + col0 + c] : 0.f;
   }
   for (int m = tid; m <= M; m += kScanThreads) cnt[m] = (a.state_in_cnt && m < M) ? a.state_in_cnt[slab * M + m] : 0.f;
+  for (int i = tid; i < a.n_chunks; i += kScanThreads) s_sizes[i] = sizes[i];
   if (tid <= kChunk) {
     float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
     for (int e = 0; e < tid; ++e) v *= lam;
@@ -1275,11 +1301,16 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   }
   float mu = 1.f;
 
-  ChunkRegs<KP, NV, VT, CPL> nx = fetch_chunk<KP, NV, VT, CPL>(a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
+  // the next chunk's registers alternate between two sets (the loop below is unrolled by two), so nothing is copied
+  ChunkRegs<KP, NV, VT, CPL> ra, rb;
+  fetch_chunk<0>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
+  fetch_chunk<1>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
+  fetch_chunk<2>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
   int next_bytes = a.n_chunks > 1 ? sizes[1] : 0;
   lds_barrier();
+  const float lam_chunk = pw[kChunk];   // the fade of a full chunk, kept in a register
 
-  for (int c = 0; c < a.n_chunks; ++c) {
+  auto chunk = [&](const int c, const ChunkRegs<KP, NV, VT, CPL>& nx, ChunkRegs<KP, NV, VT, CPL>& fut) {
     const int c0 = c * kChunk;
     const int L = min(kChunk, a.T - c0);
     // S1: stage
@@ -1330,9 +1361,11 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       own_wt[k] = nx.own_wt[k];
     }
     lds_barrier();
-    if (c + 1 < a.n_chunks) {
-      nx = fetch_chunk<KP, NV, VT, CPL>(a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
-      next_bytes = c + 2 < a.n_chunks ? sizes[c + 2] : 0;
+    const bool more = c + 1 < a.n_chunks;
+    if (more) {
+      fetch_chunk<2>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
+      fetch_chunk<0>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
+      next_bytes = c + 2 < a.n_chunks ? s_sizes[c + 2] : 0;
     }
     const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
     const int n_ri = hdr[0], n_ext = hdr[2];
@@ -1386,7 +1419,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       const float cn = sum8(cpart);
       if (a.read_mean) {
         const float den = fmaf(fin, cn, csum);
-        const float inv = 1.f / (den + a.read_eps);
+        const float inv = fast_rcp(den + a.read_eps);
 #pragma unroll
         for (int k = 0; k < CPL; ++k) acc[k] *= inv;
       }
@@ -1394,17 +1427,20 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
                                static_cast<int64_t>(h) * a.dh + col0 + CPL * l8, acc);
     }
     lds_barrier();
+    if (more) fetch_chunk<1>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
-    float mu_new = mu * pw[L];
+    float fade = lam_chunk;
+    if (L != kChunk) fade = pw[L];
+    float mu_new = mu * fade;
     if (!(mu_new >= kMuFloor)) {
       for (int i = tid; i < (M + 1) * CW; i += kScanThreads) A[i] *= mu_new;
       for (int i = tid; i <= M; i += kScanThreads) cnt[i] *= mu_new;
       mu_new = 1.f;
       lds_barrier();
     }
-    // S3: write; group p applies records p + 64 k, NB at a time (distinct slots; null records hit the scratch row)
+    // S3: write; group p applies records p + 64 k, NB at a time (distinct slots; null records write nothing)
     {
-      const float inv_mu = 1.f / mu_new;
+      const float inv_mu = fast_rcp(mu_new);
 #pragma unroll
       for (int k0 = 0; k0 < KP; k0 += NB) {
         Seg<CPL> x[NB], vq[NB];
@@ -1446,12 +1482,20 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         }
         const float cold = cnt[mc];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) lds_seg_store<CPL>(&A[(wr[k0 + j].x & 0xffffu) * CW + CPL * l8], x[j]);
-        cnt[mc] = cold + dcc;
+        for (int j = 0; j < NB; ++j) {   // null records (row M) write nothing: no same-row write conflicts
+          const int mj = static_cast<int>(wr[k0 + j].x & 0xffffu);
+          if (mj != M) lds_seg_store<CPL>(&A[mj * CW + CPL * l8], x[j]);
+        }
+        if (mc != M) cnt[mc] = cold + dcc;
       }
     }
     mu = mu_new;
     lds_barrier();
+  };
+  for (int c = 0; c < a.n_chunks; c += 2) {
+    chunk(c, ra, rb);
+    if (c + 1 >= a.n_chunks) break;
+    chunk(c + 1, rb, ra);
   }
 
   if (a.state_out_mem) {
@@ -1588,12 +1632,13 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   if (p->M > 65535) return set_err(SDM_RT_EUNSUPPORTED, "n_sub^2 = %d locations exceed 65535", p->M);
   p->cap = p->c1 <= 8 && p->kk <= 8 ? 8 : 16;
   p->pitch = (p->kk + 7) / 8 * 8;
-  if (scan_lds_bytes(p->M, p->pitch, 8) > kLdsBytes)
-    return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations do not fit a slab of 8 columns in LDS", p->M);
+  p->n_chunks = (p->T + kChunk - 1) / kChunk;
+  if (scan_lds_bytes(p->M, p->pitch, 8, p->n_chunks) > kLdsBytes)
+    return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations and T = %d do not fit a slab of 8 columns in LDS", p->M,
+                   p->T);
   if (plan_static_lds(p->pitch) + 8 * static_cast<size_t>(p->M) + 8 * static_cast<size_t>(p->n_sub) * p->half + 256 >
       kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations: writer masks and sub-keys do not fit in LDS", p->M);
-  p->n_chunks = (p->T + kChunk - 1) / kChunk;
   const size_t tok = static_cast<size_t>(p->B) * p->T;
   const size_t n_plans = static_cast<size_t>(p->B) * p->H * p->n_chunks;
   size_t o = 0;
@@ -1706,7 +1751,7 @@ struct PlanLaunch {
 
 template <int CW, int KP, typename VT, typename OutT>
 int launch_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  const size_t lds = scan_lds_bytes(p.M, KP, CW);
+  const size_t lds = scan_lds_bytes(p.M, KP, CW, p.n_chunks);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<CW, KP, VT, OutT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(kLdsBytes));
@@ -1725,7 +1770,7 @@ int launch_scan_k(const Plan& p, const ScanArgs& a, hipStream_t st) {
 template <typename VT>
 int scan_columns(const Plan& p) {
   for (int cw : {32, 16, 8})
-    if (p.dh % cw == 0 && scan_lds_bytes(p.M, p.pitch, cw) <= kLdsBytes) return cw;
+    if (p.dh % cw == 0 && scan_lds_bytes(p.M, p.pitch, cw, p.n_chunks) <= kLdsBytes) return cw;
   return 0;
 }
 
