@@ -114,6 +114,30 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    float* state_out_mem, float* state_out_cnt,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace sdm_rt_decode_step needs (the picks of one token per stream; 0 on invalid dims). */
+size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);
+
+/* One decode step: one token for each of B = dims->batch streams (dims->seq_len must be 1), with the recurrence of
+ * RunTimeSdm.forward_sequential (track4_onesdm_models.py:276-300): optional reset, read, then faded write.  The
+ * reference keeps no state across calls (it only exposes last_state, :299); this entry point carries it.
+ *   kz, qz, v, gate_logits   one row per stream, as in sdm_rt_forward
+ *   reset        [B] uint8 or NULL: 1 empties that stream's memory before it reads (a BOS, :287-289)
+ *   state_mem    [B][H][M][dh] float32, state_cnt [B][H][M] float32, state_scale [B][H] float32, read and
+ *                updated in place: the true memory is state_scale * state_mem and the true counts
+ *                state_scale * state_cnt.  A new stream starts from mem = cnt = 0, scale = 1; a state from
+ *                sdm_rt_forward (state_out_*) continues with scale = 1.  Keeping the scale apart makes the fade
+ *                O(1) per step: the cost of a step does not grow with the position (the slab is rescaled once
+ *                when the scale falls below 2^-60, and on every step of a head whose decay is 0).
+ *   r_out        one row per stream of H * dh read-outs (after the mean read and the output norm, before wo),
+ *                dtype out_dtype */
+int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                       const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
+                       const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
+                       sdm_rt_dtype in_dtype, const uint8_t* reset,
+                       float* state_mem, float* state_cnt, float* state_scale,
+                       void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* The input norm of RunTimeSdm (RMSNorm, experiments/track4/sdmllm/track4_sdmllm_models.py:63-71) with the
  * reference's rounding: out = cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), the mean and product in float32,
  * cast_in rounding to the input dtype and cast_out to out_dtype.

@@ -106,11 +106,13 @@ def address_weights(sv, log_scale, gate=None):
     return w
 
 
-def scan_recurrence(siw, ww, sir, wr, V, lam, state=None):
-    """The token recurrence of the memory (OM:276-300), read first then write.
+def scan_recurrence(siw, ww, sir, wr, V, lam, state=None, reset=None):
+    """The token recurrence of the memory (OM:276-300): (empty at a reset,) read, then write.
 
     siw, sir (B, H, T, k) int; ww, wr (B, H, T, k); V (B, H, T, dh); lam (H,).
     state: optional (mem (B, H, M, dh), cnt (B, H, M)) to start from; M is taken from it or from max slot id.
+    reset: optional (B, T) bool; where set, the memory of that batch row is emptied before position t reads
+    (OM:287-289).
     Returns num (B, H, T, dh), den (B, H, T), mem, cnt (the state after the last write)."""
     B, H, T, k = siw.shape
     dh = V.shape[-1]
@@ -127,6 +129,10 @@ def scan_recurrence(siw, ww, sir, wr, V, lam, state=None):
     num = np.zeros((B, H, T, dh))
     den = np.zeros((B, H, T))
     for t in range(T):
+        if reset is not None:
+            live = (~np.asarray(reset[:, t], bool)).astype(np.float64)
+            mem *= live[:, None, None, None]
+            cnt *= live[:, None, None]
         rows = sir[:, :, t]                                  # (B, H, k)
         got = mem[bi, hi, rows]                              # (B, H, k, dh)
         num[:, :, t] = np.einsum("bhk,bhkd->bhd", wr[:, :, t], got)

@@ -45,6 +45,17 @@ def _rows(x, name, B, T, width):
     return x.stride(1)
 
 
+def _rows2(x, name, B, width):
+    """Row stride (elements) of a [B, >=width] activation with unit stride in the last dimension."""
+    if x.dim() != 2 or x.shape[0] != B or x.shape[1] < width:
+        raise ValueError(f"{name}: expected [B={B}, >={width}], got {tuple(x.shape)}")
+    if x.dtype not in _DT:
+        raise ValueError(f"{name}: dtype {x.dtype} is not float32 or bfloat16")
+    if x.numel() and x.stride(1) != 1:
+        raise ValueError(f"{name}: last dimension must have unit stride")
+    return x.stride(0) if B > 1 else max(x.shape[1], width)
+
+
 def _params(device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias):
     held = [_f32(t, device) for t in (keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)]
     prm = _lib.SdmRtParams(*[_ptr(t) for t in held])
@@ -151,6 +162,87 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
     _lib.check(rc, lib)
     if want_state:
         return out, (mem_out, cnt_out)
+    return out
+
+
+class DecodeState:
+    """State of B decode streams: the true memory is ``scale * mem`` and the true counts ``scale * cnt``
+    (mem [B, H, M, dh], cnt [B, H, M], scale [B, H], float32, on the device).  Keeping the scale apart lets a decode
+    step fade the whole state in O(1)."""
+
+    def __init__(self, mem, cnt, scale):
+        B, H, M, dh = mem.shape
+        if tuple(cnt.shape) != (B, H, M) or tuple(scale.shape) != (B, H):
+            raise ValueError("DecodeState needs mem [B, H, M, dh], cnt [B, H, M] and scale [B, H]")
+        for t in (mem, cnt, scale):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.device != mem.device:
+                raise ValueError("DecodeState tensors must be contiguous float32 on one device")
+        self.mem, self.cnt, self.scale = mem, cnt, scale
+
+    @classmethod
+    def empty(cls, B, H, M, dh, device):
+        return cls(torch.zeros(B, H, M, dh, device=device), torch.zeros(B, H, M, device=device),
+                   torch.ones(B, H, device=device))
+
+    @classmethod
+    def from_state(cls, mem, cnt):
+        """Continue from a true state, e.g. the (mem, cnt) of core_forward(..., want_state=True)."""
+        mem = mem.detach().to(torch.float32).contiguous().clone()
+        cnt = cnt.detach().to(torch.float32).contiguous().clone()
+        return cls(mem, cnt, torch.ones(mem.shape[:2], device=mem.device))
+
+    def state(self):
+        """The true (mem, cnt), as forward's last_state holds them (a format conversion, not a decode step)."""
+        return self.mem * self.scale[..., None, None], self.cnt * self.scale[..., None]
+
+
+def decode_step(kz, qz, v, gate_logits, state, *, keys1, keys2, log_scale, decay, addr_b=None, onorm_w=None,
+                gate_bias=None, k, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2, reset=None,
+                out_dtype=None, out=None, workspace=None, params=None):
+    """One token for each of B streams (RunTimeSdm.forward_sequential's recurrence, one step): optional reset, read,
+    then faded write, updating ``state`` (a DecodeState) in place.
+
+    kz, qz [B, H * d_a]; v [B, H * dh]; gate_logits [B, H] or None; reset [B] bool or None.  Returns r [B, H * dh]
+    (before wo), out_dtype defaulting to v's dtype."""
+    lib = _lib.load()
+    B = v.shape[0]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dh = v.shape[1] // H
+    M = n_sub * n_sub
+    dims = make_dims(B, 1, H, dh, d_a, n_sub, k, read_mode, out_norm, gate_logits is not None, read_eps,
+                     out_norm_eps)
+    dt = v.dtype
+    for name, x in (("kz", kz), ("qz", qz), ("gate_logits", gate_logits)):
+        if x is not None and x.dtype != dt:
+            raise ValueError(f"{name} has dtype {x.dtype}, expected {dt}")
+    ks = _rows2(kz, "kz", B, H * d_a)
+    qs = _rows2(qz, "qz", B, H * d_a)
+    vs = _rows2(v, "v", B, H * dh)
+    gs = 0 if gate_logits is None else _rows2(gate_logits, "gate_logits", B, H)
+    if tuple(state.mem.shape) != (B, H, M, dh):
+        raise ValueError(f"state holds {tuple(state.mem.shape)}, expected [B={B}, H={H}, M={M}, dh={dh}]")
+    dev = v.device
+    if params is None:
+        params = _params(dev, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)
+    prm = params[0]
+    rs = None
+    if reset is not None:
+        if tuple(reset.shape) != (B,):
+            raise ValueError(f"reset must be [B={B}]")
+        rs = reset.to(device=dev, dtype=torch.uint8).contiguous()
+    out_dtype = out_dtype or dt
+    if out is None:
+        out = torch.empty(B, H * dh, dtype=out_dtype, device=dev)
+    ostride = _rows2(out, "out", B, H * dh)
+    nbytes = lib.sdm_rt_decode_workspace_bytes(ctypes.byref(dims))
+    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_decode_step(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
+                                _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(state.mem), _ptr(state.cnt),
+                                _ptr(state.scale), _ptr(out), ostride, _DT[out_dtype], _ptr(ws), ws.numel(),
+                                ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
     return out
 
 

@@ -9,7 +9,8 @@
 //                   the M write counts stays in LDS for the whole sequence; each chunk reads the carried state and
 //                   the in-chunk writes its plan lists, then adds the chunk's faded writes (_chunk :215-241)
 //   finish_kernel   per (token, head): r * rsqrt(mean(r^2) + eps) * onorm_w (finish :243-246)
-// address_kernel runs the addressing alone for sdm_rt_address.
+// address_kernel runs the addressing alone for sdm_rt_address; a decode step (sdm_rt_decode_step) is two addressing
+// launches and decode_kernel, one token per stream.
 //
 // Decay bookkeeping in scan_kernel: the slab holds A with the true state S = mu * A (mu a per-slab scalar).  A chunk
 // of L positions reads mu * lam^p * A[slot] at offset p, then mu <- mu * lam^L and each write at offset q adds
@@ -1597,6 +1598,130 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// decode step: one token per stream (the recurrence of forward_sequential, track4_onesdm_models.py:276-300)
+//
+// The state of stream b, head h is kept as (mem, cnt, scale): the true memory is scale * mem and the true counts
+// scale * cnt.  A step (after an optional reset, which empties the memory) reads first, then fades the state by lam
+// in O(1) (scale <- lam * scale) and adds its writes divided by the new scale; when the scale falls below 2^-60 (or
+// to 0) the slab is multiplied by it once and the scale reset to 1.  So the cost of a step does not grow with the
+// position.  One wave per (head, stream); lane l takes columns l, l + 64, ...
+struct DecodeArgs {
+  const int32_t* wslot;   // [B][H][pitch] write picks of this token (from the addressing)
+  const float* wwt;       //   and their weights (gate included)
+  const int32_t* rslot;   // read picks
+  const float* rwt;
+  const void* v;          // value rows (one per stream)
+  int64_t v_stride;
+  const float* decay;     // [H]
+  const float* onorm_w;   // [H][dh]
+  const uint8_t* reset;   // [B] or nullptr: 1 empties the stream's memory before it reads
+  float* mem;             // [B][H][M][dh]
+  float* cnt;             // [B][H][M]
+  float* scale;           // [B][H]
+  void* r_out;            // rows of H * dh (one per stream)
+  int64_t r_stride;
+  int out_bf16, H, dh, M, kk, pitch, read_mean, out_norm;
+  float read_eps, out_norm_eps;
+};
+
+template <typename VT>
+__global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
+  constexpr int kCols = 8;   // columns per lane: head_dim <= 512
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t sl = static_cast<int64_t>(b) * a.H + h;
+  float* mem = a.mem + sl * a.M * a.dh;
+  float* cnt = a.cnt + sl * a.M;
+  float mu = a.scale[sl];
+  if (a.reset && a.reset[b]) {   // a document starts here: the memory is emptied before the read
+    for (int m = 0; m < a.M; ++m)
+      for (int c = lane; c < a.dh; c += 64) mem[static_cast<int64_t>(m) * a.dh + c] = 0.f;
+    for (int m = lane; m < a.M; m += 64) cnt[m] = 0.f;
+    mu = 1.f;
+    __threadfence_block();
+    __syncthreads();
+  }
+  // read: mu * sum_j wr_j * mem[sir_j], mu * sum_j wr_j * cnt[sir_j] (track4_onesdm_models.py:290-293)
+  const int32_t* rs = a.rslot + sl * a.pitch;
+  const float* rw = a.rwt + sl * a.pitch;
+  float acc[kCols];
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) acc[q] = 0.f;
+  float den = 0.f;
+  for (int j = 0; j < a.kk; ++j) {
+    const int s = rs[j];
+    const float w = rw[j];
+    const float* row = mem + static_cast<int64_t>(s) * a.dh;
+#pragma unroll
+    for (int q = 0; q < kCols; ++q) {
+      const int c = lane + 64 * q;
+      if (c < a.dh) acc[q] = fmaf(w, row[c], acc[q]);
+    }
+    den = fmaf(w, cnt[s], den);
+  }
+  // finish (:243-246, without wo): mean read, then the per-head output norm
+  const float dn = mu * den;
+  const float rinv = a.read_mean ? 1.f / (dn + a.read_eps) : 1.f;
+  float r[kCols];
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) {
+    const int c = lane + 64 * q;
+    r[q] = c < a.dh ? (a.read_mean ? (mu * acc[q]) * rinv : mu * acc[q]) : 0.f;
+    ss = fmaf(r[q], r[q], ss);
+  }
+  float on = 1.f;
+  if (a.out_norm) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    on = rsqrtf(ss / static_cast<float>(a.dh) + a.out_norm_eps);
+  }
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) {
+    const int c = lane + 64 * q;
+    if (c < a.dh) {
+      float o = r[q];
+      if (a.out_norm) o = o * on * a.onorm_w[h * a.dh + c];
+      const int64_t at = static_cast<int64_t>(b) * a.r_stride + static_cast<int64_t>(h) * a.dh + c;
+      if (a.out_bf16) static_cast<bf16_t*>(a.r_out)[at] = from_f32<bf16_t>(o);
+      else static_cast<float*>(a.r_out)[at] = o;
+    }
+  }
+  // fade (O(1) through the scale; rescale the slab when the scale gets small), then write (:294-298)
+  float mu2 = mu * a.decay[h];
+  if (!(mu2 >= kMuFloor)) {
+    for (int m = 0; m < a.M; ++m)
+      for (int c = lane; c < a.dh; c += 64) mem[static_cast<int64_t>(m) * a.dh + c] *= mu2;
+    for (int m = lane; m < a.M; m += 64) cnt[m] *= mu2;
+    mu2 = 1.f;
+    __threadfence_block();
+    __syncthreads();
+  }
+  const float inv = 1.f / mu2;
+  const int32_t* ws = a.wslot + sl * a.pitch;
+  const float* ww = a.wwt + sl * a.pitch;
+  const VT* vrow = static_cast<const VT*>(a.v) + static_cast<int64_t>(b) * a.v_stride + static_cast<int64_t>(h) * a.dh;
+  float vv[kCols];
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) {
+    const int c = lane + 64 * q;
+    vv[q] = c < a.dh ? to_f32(vrow[c]) : 0.f;
+  }
+  for (int j = 0; j < a.kk; ++j) {   // the picks of one token are distinct slots
+    const int s = ws[j];
+    const float w = ww[j] * inv;
+    float* row = mem + static_cast<int64_t>(s) * a.dh;
+#pragma unroll
+    for (int q = 0; q < kCols; ++q) {
+      const int c = lane + 64 * q;
+      if (c < a.dh) row[c] = fmaf(w, vv[q], row[c]);
+    }
+    if (lane == 0) cnt[s] += w;
+  }
+  if (lane == 0) a.scale[sl] = mu2;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // host side
 struct Plan {
   int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, n_chunks;
@@ -1997,6 +2122,102 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   s.r_out = r_out;
   s.r_stride = out_row_stride;
   return launch_scan(p, s, in_dtype, out_dtype, st);
+}
+
+size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims) {
+  Plan p;
+  if (make_plan(dims, &p) != SDM_RT_OK) return 0;
+  return 2 * align_up(sizeof(int32_t) * static_cast<size_t>(p.B) * p.H * p.pitch, 256) +
+         2 * align_up(sizeof(float) * static_cast<size_t>(p.B) * p.H * p.pitch, 256);
+}
+
+int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* kz, int64_t kz_row_stride,
+                       const void* qz, int64_t qz_row_stride, const void* v, int64_t v_row_stride,
+                       const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype,
+                       const uint8_t* reset, float* state_mem, float* state_cnt, float* state_scale, void* r_out,
+                       int64_t out_row_stride, sdm_rt_dtype out_dtype, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p);
+  if (rc) return rc;
+  if (p.T != 1) return set_err(SDM_RT_EINVAL, "a decode step takes one token per stream: seq_len must be 1, not %d", p.T);
+  if ((rc = check_params(params, dims->out_norm != 0))) return rc;
+  if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (p.B == 0) return SDM_RT_OK;
+  if (!kz || !qz || !v || !r_out) return set_err(SDM_RT_EINVAL, "kz, qz, v and r_out must not be NULL");
+  if (!state_mem || !state_cnt || !state_scale)
+    return set_err(SDM_RT_EINVAL, "state_mem, state_cnt and state_scale must not be NULL");
+  if (dims->write_gate && !gate_logits) return set_err(SDM_RT_EINVAL, "write_gate is set but gate_logits is NULL");
+  const int64_t wa = static_cast<int64_t>(p.H) * p.d_a;
+  const int64_t wv = static_cast<int64_t>(p.H) * p.dh;
+  if (kz_row_stride < wa || qz_row_stride < wa)
+    return set_err(SDM_RT_EINVAL, "kz/qz row stride (%lld, %lld) < heads * addr_dim", (long long)kz_row_stride,
+                   (long long)qz_row_stride);
+  if (v_row_stride < wv) return set_err(SDM_RT_EINVAL, "v_row_stride %lld < heads * head_dim", (long long)v_row_stride);
+  if (gate_logits && gate_row_stride < p.H)
+    return set_err(SDM_RT_EINVAL, "gate_row_stride %lld < heads", (long long)gate_row_stride);
+  if (out_row_stride < wv)
+    return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
+  const size_t need = sdm_rt_decode_workspace_bytes(dims);
+  if (!workspace || workspace_bytes < need)
+    return set_err(SDM_RT_ENOSPACE, "workspace %zu bytes < required %zu", workspace_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const size_t si = align_up(sizeof(int32_t) * static_cast<size_t>(p.B) * p.H * p.pitch, 256);
+  const size_t sf = align_up(sizeof(float) * static_cast<size_t>(p.B) * p.H * p.pitch, 256);
+  int32_t* wslot = reinterpret_cast<int32_t*>(ws);
+  int32_t* rslot = reinterpret_cast<int32_t*>(ws + si);
+  float* wwt = reinterpret_cast<float*>(ws + 2 * si);
+  float* rwt = reinterpret_cast<float*>(ws + 2 * si + sf);
+  // the picks of this token: write keys (gated) and read queries, [B][H][1][pitch]
+  AddrArgs aa{};
+  aa.g = addr_geom(p, params);
+  aa.B = p.B;
+  aa.T = 1;
+  aa.pitch = p.pitch;
+  for (int set = 0; set < 2; ++set) {
+    aa.z = set == 0 ? kz : qz;
+    aa.z_stride = set == 0 ? kz_row_stride : qz_row_stride;
+    aa.gl = set == 0 && dims->write_gate ? gate_logits : nullptr;
+    aa.g_stride = gate_row_stride;
+    aa.slot_out = set == 0 ? wslot : rslot;
+    aa.w_out = set == 0 ? wwt : rwt;
+    aa.s_out = nullptr;
+    rc = in_dtype == SDM_RT_BF16 ? by_half<AddressLaunch, bf16_t>(p.half, p, aa, st)
+                                 : by_half<AddressLaunch, float>(p.half, p, aa, st);
+    if (rc) return rc;
+  }
+  DecodeArgs da{};
+  da.wslot = wslot;
+  da.wwt = wwt;
+  da.rslot = rslot;
+  da.rwt = rwt;
+  da.v = v;
+  da.v_stride = v_row_stride;
+  da.decay = params->decay;
+  da.onorm_w = params->onorm_w;
+  da.reset = reset;
+  da.mem = state_mem;
+  da.cnt = state_cnt;
+  da.scale = state_scale;
+  da.r_out = r_out;
+  da.r_stride = out_row_stride;
+  da.out_bf16 = out_dtype == SDM_RT_BF16;
+  da.H = p.H;
+  da.dh = p.dh;
+  da.M = p.M;
+  da.kk = p.kk;
+  da.pitch = p.pitch;
+  da.read_mean = dims->read_mean;
+  da.out_norm = dims->out_norm;
+  da.read_eps = dims->read_eps;
+  da.out_norm_eps = dims->out_norm_eps;
+  dim3 grid(p.H, p.B);
+  if (in_dtype == SDM_RT_BF16) hipLaunchKernelGGL((decode_kernel<bf16_t>), grid, dim3(64), 0, st, da);
+  else hipLaunchKernelGGL((decode_kernel<float>), grid, dim3(64), 0, st, da);
+  return check_launch("decode");
 }
 
 }  // extern "C"

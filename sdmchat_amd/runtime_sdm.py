@@ -176,6 +176,34 @@ class RunTimeSdm(nn.Module):
         self._last_gate = value
         self._gate_src = None
 
+    # -- decoding ----------------------------------------------------------------------------------------------------
+    def decode_state(self, batch, device=None):
+        """An empty state for ``batch`` decode streams (a core.DecodeState)."""
+        device = device if device is not None else self.keys1.device
+        return core.DecodeState.empty(batch, self.h, self.M, self.dh, device)
+
+    def step(self, x, state, reset=None):
+        """One token for each of B streams: x [B, d] (or [B, 1, d]) -> y of the same shape, with the recurrence of
+        forward_sequential (track4_onesdm_models.py:276-300) carried in ``state`` (updated in place).  reset [B] bool
+        or None empties a stream's memory before its token reads (a BOS, :287-289)."""
+        squeeze = x.dim() == 3
+        x2 = x.reshape(x.shape[0], x.shape[-1]) if squeeze else x
+        if not self.enabled:
+            return torch.zeros_like(x)
+        self._check(x2.unsqueeze(1), None)
+        dt = self._compute_dtype(x2)
+        with torch.autocast("cuda", enabled=False):
+            kz, qz, V, g = self._project(x2.unsqueeze(1), dt)
+            wo = self._fused_weight(dt)[1]
+            r = core.decode_step(
+                kz[:, 0], qz[:, 0], V[:, 0], None if g is None else g[:, 0], state, keys1=self.keys1,
+                keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(), addr_b=self.addr_b,
+                onorm_w=self.onorm_w if self.out_norm else None, gate_bias=self.wg.bias if self.write_gate else None,
+                k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
+                out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws)
+            y = torch.matmul(r, wo.t()).to(x.dtype)
+        return y.reshape(x.shape)
+
     def forward_sequential(self, x, reset=None):
         """The token recurrence of the reference (track4_onesdm_models.py:276-300).  It is the same function as
         forward; the HIP core computes it once, so this is forward."""

@@ -216,3 +216,28 @@ def check_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, tol=1e-5
                                       out_norm, None if on is None else on[h:h + 1], M)
             assert_close(r[b:b + 1, :, sl], want, tol, bf16_out, f"slab b={b} h={h}")
     return flips
+
+
+def gpu_decode(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, read_mode="mean", out_norm=True,
+               reset=None, state=None):
+    """Run sdm_rt_decode_step once per position (B streams, T steps); returns r (numpy float32, (B, T, H*dh)) and
+    the final DecodeState.  reset: (B, T) bool or None; state: a DecodeState to continue from, or None (empty)."""
+    B, T = V.shape[0], V.shape[1]
+    H, n_sub, half = p["keys1"].shape
+    dh = V.shape[2] // H
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    kz_d, qz_d, V_d, g_d = (to_dev(x, dtype) for x in (kz, qz, V, g))
+    if state is None:
+        state = core.DecodeState.empty(B, H, n_sub * n_sub, dh, "cuda")
+    rs = None if reset is None else torch.from_numpy(np.asarray(reset, bool)).cuda()
+    ws = core.CoreWorkspace()
+    outs = []
+    for t in range(T):
+        outs.append(core.decode_step(
+            kz_d[:, t], qz_d[:, t], V_d[:, t], None if g_d is None else g_d[:, t], state, keys1=tp["keys1"],
+            keys2=tp["keys2"], log_scale=tp["log_scale"], decay=tp["decay"], addr_b=tp["addr_b"],
+            onorm_w=tp["onorm_w"], gate_bias=tp["gate_bias"] if g is not None else None, k=k, read_mode=read_mode,
+            out_norm=out_norm, reset=None if rs is None else rs[:, t], out_dtype=out_dtype, workspace=ws))
+    torch.cuda.synchronize()
+    r = torch.stack(outs, 1) if outs else torch.zeros(B, 0, H * dh)
+    return r.float().cpu().numpy(), state

@@ -97,3 +97,23 @@ def test_rms_norm_validation():
     assert lib.sdm_rt_rms_norm(one, 8, 1, 4, 16, one, 1e-6, one, 16, 1, None) == -1    # row stride < d
     assert lib.sdm_rt_rms_norm(one, 16, 5, 4, 16, one, 1e-6, one, 16, 1, None) == -1   # unknown dtype
     assert lib.sdm_rt_rms_norm(None, 16, 1, 0, 16, None, 1e-6, None, 16, 1, None) == 0  # no rows: nothing to do
+
+
+def test_decode_step_validation():
+    """sdm_rt_decode_step checks its arguments on the host: one token per stream, a state, enough workspace."""
+    lib = _lib.load()
+    dims = _dims(B=4, T=1)
+    need = lib.sdm_rt_decode_workspace_bytes(ctypes.byref(dims))
+    assert 0 < need < (1 << 20)
+    assert lib.sdm_rt_decode_workspace_bytes(ctypes.byref(_dims(k=0))) == 0
+    prm = _lib.SdmRtParams(*([ctypes.c_void_p(256)] * 7))
+    fake = ctypes.c_void_p(256)
+    I, F = _lib.SDM_RT_F32, _lib.SDM_RT_F32
+
+    def call(d, state=fake, ws_bytes=need):
+        return lib.sdm_rt_decode_step(ctypes.byref(d), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12,
+                                      I, None, state, state, state, fake, 768, F, fake, ws_bytes, None)
+    assert call(_dims(B=4, T=2)) == -1 and b"seq_len must be 1" in lib.sdm_rt_last_error()
+    assert call(dims, state=None) == -1 and b"state" in lib.sdm_rt_last_error()
+    assert call(dims, ws_bytes=need - 1) == -2 and b"workspace" in lib.sdm_rt_last_error()
+    assert call(_dims(B=0, T=1)) == 0

@@ -55,6 +55,38 @@ def test_recurrence_state_carry_is_the_same_as_one_pass():
     np.testing.assert_allclose(c2, c_all, atol=1e-12)
 
 
+
+def test_reset_empties_the_memory_before_the_read():
+    """A reset at position t (OM:287-289) equals a fresh recurrence started at t from an empty memory, computed
+    independently on the segment; rows without a reset are unaffected."""
+    rng = np.random.Generator(np.random.PCG64(24))
+    B, H, T, k, M, dh = 3, 2, 30, 3, 10, 4
+    siw = _distinct_ids(rng, (B, H, T), k, M)
+    sir = _distinct_ids(rng, (B, H, T), k, M)
+    ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
+    V = rng.standard_normal((B, H, T, dh))
+    lam = np.array([0.8, 1.0])
+    z = (np.zeros((B, H, M, dh)), np.zeros((B, H, M)))
+    reset = np.zeros((B, T), bool)
+    reset[0, 11] = True
+    reset[2, 0] = True
+    reset[2, 25] = True
+    num, den, mem, cnt = O.scan_recurrence(siw, ww, sir, wr, V, lam, state=z, reset=reset)
+    n0, d0, _, _ = O.scan_recurrence(siw, ww, sir, wr, V, lam, state=z)
+    np.testing.assert_array_equal(num[1], n0[1])                        # no reset in row 1
+    np.testing.assert_array_equal(num[0, :, :11], n0[0, :, :11])        # row 0 before its reset
+    zr = (np.zeros((1, H, M, dh)), np.zeros((1, H, M)))
+    sl = np.s_[0:1, :, 11:]
+    ns, ds, ms, cs = O.scan_recurrence(siw[sl], ww[sl], sir[sl], wr[sl], V[sl], lam, state=zr)
+    np.testing.assert_allclose(num[0:1, :, 11:], ns, atol=1e-12)
+    np.testing.assert_allclose(den[0:1, :, 11:], ds, atol=1e-12)
+    np.testing.assert_allclose(mem[0:1], ms, atol=1e-12)
+    assert np.all(num[0, :, 11] == 0) and np.all(den[0, :, 11] == 0)   # the reset position reads an empty memory
+    sl = np.s_[2:3, :, 25:]
+    ns, _, ms, cs = O.scan_recurrence(siw[sl], ww[sl], sir[sl], wr[sl], V[sl], lam, state=zr)
+    np.testing.assert_allclose(num[2:3, :, 25:], ns, atol=1e-12)
+    np.testing.assert_allclose(cnt[2:3], cs, atol=1e-12)
+
 def _small_layer(seed=3, **over):
     cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8, **over)
     p = S.layer_params(cfg, seed=seed, decays=(0.0, 0.6, 0.97, 1.0))
