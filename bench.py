@@ -21,6 +21,11 @@ FLOPs / 2.5 PFLOP/s) / module time.  copy_gbs: a 1 GiB device-to-device copy, fo
 cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle/sdm_torch32.py, the reference's
 dense chunk algorithm) on the same workload, all host cores, one warm call then best of three.
 
+decode: the decode step (sdm_rt_decode_step, one token for each of 64 streams, 12 heads, float32 state carried in
+place) timed as a HIP graph of 64 steps replayed 513 times, so the state runs through 32,832 positions; us_per_step
+= replay time / 64 (device time, no host launch cost), reported overall (median) and at positions 0, 1,024, 8,192
+and 32,768 to show that the cost of a step does not grow with the position.  --no-decode skips it.
+
 --copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
 """
 import argparse
@@ -82,6 +87,48 @@ def cpu_baseline():
                       f"1 warm call then best of 3 ({best:.2f} s per call)"}
 
 
+def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
+    """Device time of sdm_rt_decode_step for `streams` streams of the layer, by position (see the module doc)."""
+    import numpy as np
+    import torch
+
+    from sdmchat_amd import core
+
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    xt = torch.randn(streams, 1, D, generator=gen).to(dev).to(torch.bfloat16)
+    kz, qz, V, g = m._project(xt, torch.bfloat16)
+    kz, qz, V, g = kz[:, 0], qz[:, 0], V[:, 0], g[:, 0]
+    st = m.decode_state(streams, dev)
+    prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, m.wg.bias)
+    ws = core.CoreWorkspace()
+    out = torch.empty(streams, D, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        core.decode_step(kz, qz, V, g, st, keys1=m.keys1, keys2=m.keys2, log_scale=m.log_scale, decay=m.decay(),
+                         k=K, out=out, workspace=ws, params=prm)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(graph_steps):
+            step()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for e0, e1 in evs:
+        e0.record()
+        graph.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
+    by_pos = {str(pos): round(float(us[pos // graph_steps]), 2) for pos in (0, 1024, 8192, 32768)}
+    log(f"decode: {np.median(us):.2f} us per step (median over {replays} replays), by position {by_pos}")
+    return {"workload": f"RunTimeSdm decode step: {streams} streams x {H} heads, one token each, float32 state",
+            "us_per_step": round(float(np.median(us)), 2), "us_per_step_by_position": by_pos,
+            "steps_timed": replays * graph_steps, "method": f"HIP graph of {graph_steps} steps, replay time / "
+            f"{graph_steps}"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +137,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
@@ -159,6 +207,7 @@ def main():
         big2 = torch.empty_like(big)
         copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
         del big, big2
+        decode = None if a.no_decode else decode_bench(m, dev)
 
     ms_per_step = wall * 1e3 / a.steps
     tokens = B * T
@@ -190,6 +239,8 @@ def main():
                                  / (mod_ms * 1e-3), 4)},
         "copy_gbs": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
     }
+    if decode is not None:
+        rec["decode"] = decode
     if not a.no_cpu:
         log("cpu baseline ...")
         rec["cpu_baseline"] = cpu_baseline()

@@ -9,8 +9,8 @@
 //                   the M write counts stays in LDS for the whole sequence; each chunk reads the carried state and
 //                   the in-chunk writes its plan lists, then adds the chunk's faded writes (_chunk :215-241)
 //   finish_kernel   per (token, head): r * rsqrt(mean(r^2) + eps) * onorm_w (finish :243-246)
-// address_kernel runs the addressing alone for sdm_rt_address; a decode step (sdm_rt_decode_step) is two addressing
-// launches and decode_kernel, one token per stream.
+// address_kernel runs the addressing alone for sdm_rt_address; a decode step (sdm_rt_decode_step) is one addressing
+// launch for both address sets and decode_kernel, one token per stream.
 //
 // Decay bookkeeping in scan_kernel: the slab holds A with the true state S = mu * A (mu a per-slab scalar).  A chunk
 // of L positions reads mu * lam^p * A[slot] at offset p, then mu <- mu * lam^L and each write at offset q adds
@@ -760,6 +760,11 @@ struct AddrArgs {
   int32_t* slot_out;          // [B][H][T][pitch]
   float* w_out;
   float* s_out;
+  // a second address set (gridDim.z = 2, blockIdx.z = 1): its rows, picks and weights; no gate, no scores
+  const void* z2;
+  int64_t z2_stride;
+  int32_t* slot_out2;
+  float* w_out2;
 };
 
 // Head h's sub-keys of both halves, unit-normalised ([2][n_sub][HALF] floats), into LDS: one row per thread.
@@ -785,6 +790,14 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   const int64_t N = static_cast<int64_t>(a.B) * a.T;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int64_t n = n0 + threadIdx.x;
+  if (blockIdx.z == 1) {   // the second address set
+    a.z = a.z2;
+    a.z_stride = a.z2_stride;
+    a.gl = nullptr;
+    a.slot_out = a.slot_out2;
+    a.w_out = a.w_out2;
+    a.s_out = nullptr;
+  }
   const float gate =
       (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
   int slot[CAP];
@@ -1624,7 +1637,23 @@ struct DecodeArgs {
   float read_eps, out_norm_eps;
 };
 
-template <typename VT>
+// the slab of one (stream, head) times f (0 empties it), float4 at a time; the caller fences
+__device__ __forceinline__ void scale_slab(float* mem, float* cnt, int M, int dh, float f, int lane) {
+  float4* m4 = reinterpret_cast<float4*>(mem);
+  const int n4 = M * dh / 4;
+  for (int i = lane; i < n4; i += 4 * 64) {
+    float4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = i + 64 * u < n4 ? m4[i + 64 * u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i + 64 * u < n4) m4[i + 64 * u] = make_float4(x[u].x * f, x[u].y * f, x[u].z * f, x[u].w * f);
+    }
+  }
+  for (int m = lane; m < M; m += 64) cnt[m] *= f;
+}
+
+template <typename VT, int KP>
 __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   constexpr int kCols = 8;   // columns per lane: head_dim <= 512
   const int h = blockIdx.x, b = blockIdx.y;
@@ -1632,33 +1661,52 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   const int64_t sl = static_cast<int64_t>(b) * a.H + h;
   float* mem = a.mem + sl * a.M * a.dh;
   float* cnt = a.cnt + sl * a.M;
+  const int kk = a.kk;
+  // every load that does not depend on the state first: the picks (pads: slot -1, weight 0) and the value row
+  int rsl[KP], wsl[KP];
+  float rwv[KP], wwv[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    rsl[j] = max(a.rslot[sl * KP + j], 0);
+    rwv[j] = a.rwt[sl * KP + j];
+    wsl[j] = max(a.wslot[sl * KP + j], 0);
+    wwv[j] = a.wwt[sl * KP + j];
+  }
+  const VT* vrow = static_cast<const VT*>(a.v) + static_cast<int64_t>(b) * a.v_stride + static_cast<int64_t>(h) * a.dh;
+  float vv[kCols];
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) {
+    const int c = lane + 64 * q;
+    vv[q] = c < a.dh ? to_f32(vrow[c]) : 0.f;
+  }
   float mu = a.scale[sl];
   if (a.reset && a.reset[b]) {   // a document starts here: the memory is emptied before the read
-    for (int m = 0; m < a.M; ++m)
-      for (int c = lane; c < a.dh; c += 64) mem[static_cast<int64_t>(m) * a.dh + c] = 0.f;
-    for (int m = lane; m < a.M; m += 64) cnt[m] = 0.f;
+    scale_slab(mem, cnt, a.M, a.dh, 0.f, lane);
     mu = 1.f;
     __threadfence_block();
     __syncthreads();
   }
-  // read: mu * sum_j wr_j * mem[sir_j], mu * sum_j wr_j * cnt[sir_j] (track4_onesdm_models.py:290-293)
-  const int32_t* rs = a.rslot + sl * a.pitch;
-  const float* rw = a.rwt + sl * a.pitch;
+  // read: mu * sum_j wr_j * mem[sir_j], mu * sum_j wr_j * cnt[sir_j] (track4_onesdm_models.py:290-293); the rows
+  // of all picks are loaded at once
   float acc[kCols];
 #pragma unroll
-  for (int q = 0; q < kCols; ++q) acc[q] = 0.f;
-  float den = 0.f;
-  for (int j = 0; j < a.kk; ++j) {
-    const int s = rs[j];
-    const float w = rw[j];
-    const float* row = mem + static_cast<int64_t>(s) * a.dh;
+  for (int q = 0; q < kCols; ++q) {
+    acc[q] = 0.f;
+    const int c = lane + 64 * q;
+    if (c < a.dh) {
+      float row[KP];
 #pragma unroll
-    for (int q = 0; q < kCols; ++q) {
-      const int c = lane + 64 * q;
-      if (c < a.dh) acc[q] = fmaf(w, row[c], acc[q]);
+      for (int j = 0; j < KP; ++j) row[j] = j < kk ? mem[static_cast<int64_t>(rsl[j]) * a.dh + c] : 0.f;
+#pragma unroll
+      for (int j = 0; j < KP; ++j) acc[q] = fmaf(rwv[j], row[j], acc[q]);
     }
-    den = fmaf(w, cnt[s], den);
   }
+  float cr[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) cr[j] = j < kk ? cnt[rsl[j]] : 0.f;
+  float den = 0.f;
+#pragma unroll
+  for (int j = 0; j < KP; ++j) den = fmaf(rwv[j], cr[j], den);
   // finish (:243-246, without wo): mean read, then the per-head output norm
   const float dn = mu * den;
   const float rinv = a.read_mean ? 1.f / (dn + a.read_eps) : 1.f;
@@ -1690,35 +1738,35 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   // fade (O(1) through the scale; rescale the slab when the scale gets small), then write (:294-298)
   float mu2 = mu * a.decay[h];
   if (!(mu2 >= kMuFloor)) {
-    for (int m = 0; m < a.M; ++m)
-      for (int c = lane; c < a.dh; c += 64) mem[static_cast<int64_t>(m) * a.dh + c] *= mu2;
-    for (int m = lane; m < a.M; m += 64) cnt[m] *= mu2;
+    scale_slab(mem, cnt, a.M, a.dh, mu2, lane);
     mu2 = 1.f;
     __threadfence_block();
     __syncthreads();
   }
   const float inv = 1.f / mu2;
-  const int32_t* ws = a.wslot + sl * a.pitch;
-  const float* ww = a.wwt + sl * a.pitch;
-  const VT* vrow = static_cast<const VT*>(a.v) + static_cast<int64_t>(b) * a.v_stride + static_cast<int64_t>(h) * a.dh;
-  float vv[kCols];
 #pragma unroll
-  for (int q = 0; q < kCols; ++q) {
+  for (int q = 0; q < kCols; ++q) {   // the picks of one token are distinct slots
     const int c = lane + 64 * q;
-    vv[q] = c < a.dh ? to_f32(vrow[c]) : 0.f;
-  }
-  for (int j = 0; j < a.kk; ++j) {   // the picks of one token are distinct slots
-    const int s = ws[j];
-    const float w = ww[j] * inv;
-    float* row = mem + static_cast<int64_t>(s) * a.dh;
+    if (c < a.dh) {
+      float old[KP];
 #pragma unroll
-    for (int q = 0; q < kCols; ++q) {
-      const int c = lane + 64 * q;
-      if (c < a.dh) row[c] = fmaf(w, vv[q], row[c]);
+      for (int j = 0; j < KP; ++j) old[j] = j < kk ? mem[static_cast<int64_t>(wsl[j]) * a.dh + c] : 0.f;
+#pragma unroll
+      for (int j = 0; j < KP; ++j) {
+        if (j < kk) mem[static_cast<int64_t>(wsl[j]) * a.dh + c] = fmaf(wwv[j] * inv, vv[q], old[j]);
+      }
     }
-    if (lane == 0) cnt[s] += w;
   }
-  if (lane == 0) a.scale[sl] = mu2;
+  if (lane == 0) {
+    float oc[KP];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) oc[j] = j < kk ? cnt[wsl[j]] : 0.f;
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      if (j < kk) cnt[wsl[j]] = oc[j] + wwv[j] * inv;
+    }
+    a.scale[sl] = mu2;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1836,7 +1884,7 @@ struct AddressLaunch {
   template <int CAP, int MODE>
   static void go(const Plan& p, const AddrArgs& a, hipStream_t st) {
     const int64_t N = static_cast<int64_t>(p.B) * p.T;
-    dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H);
+    dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H, a.z2 ? 2 : 1);
     const size_t lds = MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF;
     hipLaunchKernelGGL((address_kernel<HALF, CAP, InT, MODE>), grid, dim3(64), lds, st, a);
   }
@@ -2149,6 +2197,7 @@ int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params, con
   if (!kz || !qz || !v || !r_out) return set_err(SDM_RT_EINVAL, "kz, qz, v and r_out must not be NULL");
   if (!state_mem || !state_cnt || !state_scale)
     return set_err(SDM_RT_EINVAL, "state_mem, state_cnt and state_scale must not be NULL");
+  if (reinterpret_cast<uintptr_t>(state_mem) % 16 != 0) return set_err(SDM_RT_EINVAL, "state_mem must be 16-byte aligned");
   if (dims->write_gate && !gate_logits) return set_err(SDM_RT_EINVAL, "write_gate is set but gate_logits is NULL");
   const int64_t wa = static_cast<int64_t>(p.H) * p.d_a;
   const int64_t wv = static_cast<int64_t>(p.H) * p.dh;
@@ -2171,24 +2220,25 @@ int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params, con
   int32_t* rslot = reinterpret_cast<int32_t*>(ws + si);
   float* wwt = reinterpret_cast<float*>(ws + 2 * si);
   float* rwt = reinterpret_cast<float*>(ws + 2 * si + sf);
-  // the picks of this token: write keys (gated) and read queries, [B][H][1][pitch]
+  // the picks of this token, [B][H][1][pitch]: write keys (gated) and read queries, in one launch
   AddrArgs aa{};
   aa.g = addr_geom(p, params);
   aa.B = p.B;
   aa.T = 1;
   aa.pitch = p.pitch;
-  for (int set = 0; set < 2; ++set) {
-    aa.z = set == 0 ? kz : qz;
-    aa.z_stride = set == 0 ? kz_row_stride : qz_row_stride;
-    aa.gl = set == 0 && dims->write_gate ? gate_logits : nullptr;
-    aa.g_stride = gate_row_stride;
-    aa.slot_out = set == 0 ? wslot : rslot;
-    aa.w_out = set == 0 ? wwt : rwt;
-    aa.s_out = nullptr;
-    rc = in_dtype == SDM_RT_BF16 ? by_half<AddressLaunch, bf16_t>(p.half, p, aa, st)
-                                 : by_half<AddressLaunch, float>(p.half, p, aa, st);
-    if (rc) return rc;
-  }
+  aa.z = kz;
+  aa.z_stride = kz_row_stride;
+  aa.gl = dims->write_gate ? gate_logits : nullptr;
+  aa.g_stride = gate_row_stride;
+  aa.slot_out = wslot;
+  aa.w_out = wwt;
+  aa.z2 = qz;
+  aa.z2_stride = qz_row_stride;
+  aa.slot_out2 = rslot;
+  aa.w_out2 = rwt;
+  rc = in_dtype == SDM_RT_BF16 ? by_half<AddressLaunch, bf16_t>(p.half, p, aa, st)
+                               : by_half<AddressLaunch, float>(p.half, p, aa, st);
+  if (rc) return rc;
   DecodeArgs da{};
   da.wslot = wslot;
   da.wwt = wwt;
@@ -2215,8 +2265,15 @@ int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params, con
   da.read_eps = dims->read_eps;
   da.out_norm_eps = dims->out_norm_eps;
   dim3 grid(p.H, p.B);
-  if (in_dtype == SDM_RT_BF16) hipLaunchKernelGGL((decode_kernel<bf16_t>), grid, dim3(64), 0, st, da);
-  else hipLaunchKernelGGL((decode_kernel<float>), grid, dim3(64), 0, st, da);
+#define SDM_RT_DECODE(VT, KP) hipLaunchKernelGGL((decode_kernel<VT, KP>), grid, dim3(64), 0, st, da)
+  if (in_dtype == SDM_RT_BF16) {
+    if (p.pitch == 8) SDM_RT_DECODE(bf16_t, 8);
+    else SDM_RT_DECODE(bf16_t, 16);
+  } else {
+    if (p.pitch == 8) SDM_RT_DECODE(float, 8);
+    else SDM_RT_DECODE(float, 16);
+  }
+#undef SDM_RT_DECODE
   return check_launch("decode");
 }
 

@@ -118,3 +118,38 @@ def test_module_step_equals_forward():
         ys = torch.stack([m.step(x[:, t], st) for t in range(50)], 1)
     torch.cuda.synchronize()
     np.testing.assert_allclose(ys.cpu().numpy(), y.cpu().numpy(), atol=2e-5, rtol=1e-4)
+
+
+def test_decode_graph_replays_match_eager():
+    """Decode steps captured in a HIP graph: every replay (three, with eager work and synchronisations between them)
+    equals the same steps run eagerly from the same state."""
+    kz, qz, V, g, p = core_inputs(4, 1, 4, 16, 16, 8, seed=79, decays=(0.0, 0.5, 0.9, 1.0))
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    kz_d, qz_d, V_d, g_d = (torch.from_numpy(a[:, 0]).cuda() for a in (kz, qz, V, g))
+    prm = core._params("cuda", tp["keys1"], tp["keys2"], tp["addr_b"], tp["log_scale"], tp["decay"], tp["onorm_w"],
+                       tp["gate_bias"])
+    ws = core.CoreWorkspace()
+
+    def step(st, out):
+        core.decode_step(kz_d, qz_d, V_d, g_d, st, keys1=tp["keys1"], keys2=tp["keys2"], log_scale=tp["log_scale"],
+                         decay=tp["decay"], k=8, out=out, workspace=ws, params=prm)
+
+    eager, ge = core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda")
+    graphed, gg = core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda")
+    step(core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda"))   # sizes the workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(graphed, gg)
+        step(graphed, gg)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        step(eager, ge)
+        step(eager, ge)
+        junk = torch.randn(1000, device="cuda").sum()   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(gg, ge), f"replay {rep}: read-out differs"
+        assert torch.equal(graphed.mem, eager.mem) and torch.equal(graphed.cnt, eager.cnt)
+        assert torch.equal(graphed.scale, eager.scale)
+        del junk
