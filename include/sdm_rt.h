@@ -70,8 +70,8 @@ typedef struct {
   const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
 } sdm_rt_params;
 
-/* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (about
- * 22.5 KB per 64 positions of one head at k <= 8) and, with out_norm, a float32 copy of the read-out. */
+/* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (24 KB per
+ * 64 positions of one head at k <= 8) and, with out_norm, a float32 copy of the read-out. */
 size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
 
 /* Row pitch (entries per token and head) of the pick arrays sdm_rt_address writes: kk rounded up to 8. */
@@ -94,12 +94,14 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* The SDM core of RunTimeSdm.forward (track4_onesdm_models.py:195-274 between the projections and wo, with
- * finish :243-246 minus wo), reset = None.
+ * finish :243-246 minus wo).
  *   kz, qz       [B*T rows] write keys / read queries (H * d_a each, before addr_b), dtype in_dtype
  *   v            [B*T rows] values (H * dh), dtype in_dtype
  *   gate_logits  [B*T rows] gate logits (H, before gate_bias), dtype in_dtype; may be NULL when write_gate is 0
  *   *_row_stride    element stride between consecutive rows of each input (they may be column slices of one
  *                fused projection output)
+ *   reset        [B*T rows] uint8 or NULL: 1 empties the memory before that position reads (a BOS, the reset
+ *                masks of forward(x, reset), :229-233); NULL for none
  *   r_out        [B*T rows] of H * dh read-outs, dtype out_dtype, row stride out_row_stride
  *   state_in_mem / state_in_cnt    [B][H][M][dh] / [B][H][M] float32 state to start from, or both NULL to
  *                start from an empty memory (the reference always starts empty, :257-258)
@@ -108,7 +110,7 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params,
 int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
                    const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
-                   sdm_rt_dtype in_dtype,
+                   sdm_rt_dtype in_dtype, const uint8_t* reset,
                    void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                    const float* state_in_mem, const float* state_in_cnt,
                    float* state_out_mem, float* state_out_cnt,

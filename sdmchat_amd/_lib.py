@@ -53,7 +53,7 @@ SIGNATURES = {
                                       c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     "sdm_rt_forward": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
                                       c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
-                                      ctypes.c_int,
+                                      ctypes.c_int, c_void_p,
                                       c_void_p, c_i64, ctypes.c_int,
                                       c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, ctypes.c_size_t, c_void_p]),

@@ -842,7 +842,9 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
 //                    their entries are ext[xo], ext[xo + 1], ... up to the one flagged last.  Slots with later
 //                    writers come first.  Entries past the chunk's n_wu slots are null records {M, 0}: they read
 //                    row M (always zero) and write nothing
-//   variable part    u32 {n_ri, n_wu, n_ext, bytes}; ext[n_ext] = {c = lam^(L-1-q) * ww, q | last << 31};
+//   variable part    u32 {n_ri, n_wu | reset << 31, n_ext, bytes} (reset: the chunk holds a reset, so the state it
+//                    leaves holds only the writes after its last reset); ext[n_ext] = {c = lam^(L-1-q) * ww,
+//                    q | last << 31};
 //                    f32 ri_c[n_ri]; u8 ri_q[n_ri]
 // An in-chunk read contribution (q, c) of position p: position q < p of the chunk wrote some of p's read slots;
 // c = the sum over those slots of wr * ww * lam^(p-1-q).  Contributions run in ascending q.  sizes[] holds the
@@ -869,6 +871,7 @@ struct PlanArgs {
   const void* gl;          // gate logit rows or nullptr
   int64_t g_stride;
   const float* decay;      // [H]
+  const uint8_t* reset;    // [B*T rows] or nullptr: 1 empties the memory before that position reads
   unsigned char* plans;    // [B][H][n_chunks][stride]
   int32_t* sizes;          // [B][H][n_chunks] bytes of each plan's variable part
   int B, T, M, n_chunks;
@@ -944,6 +947,13 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
       pk_w[set][p][j] = p < L ? w[j] : 0.f;
     }
   }
+  // resets of the chunk (OM:229-233, 287-289): a reader sees the writers of its own segment only, no carried state
+  // after a reset, and only the writers after the chunk's last reset reach the state the chunk leaves
+  const unsigned long long rmask = __ballot(a.reset && p < L && a.reset[static_cast<int64_t>(b) * a.T + c0 + p]);
+  const unsigned long long upto = rmask & (p == 63 ? ~0ull : (2ull << p) - 1ull);
+  const int seg0 = upto ? 63 - __builtin_clzll(upto) : -1;          // this position's segment start in the chunk
+  const int last = rmask ? 63 - __builtin_clzll(rmask) : -1;        // the chunk's last reset
+  const unsigned long long keep = last >= 0 ? ~((1ull << last) - 1ull) : ~0ull;   // writers that reach the state
   __syncthreads();
   // mark the writers of every slot
   if (set == 0 && p < L) {
@@ -981,7 +991,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   int n_m = 0;                         // write side: owned slots with later writers
   if (p < L) {
     if (set == 1) {
-      const unsigned long long below = (1ull << p) - 1ull;
+      const unsigned long long below = ((1ull << p) - 1ull) & (seg0 >= 0 ? ~((1ull << seg0) - 1ull) : ~0ull);
 #pragma unroll
       for (int i = 0; i < KP; ++i) {
         mk[i] = i < kk ? wmask[ms[i]] & below : 0ull;
@@ -992,8 +1002,8 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
         if (j < kk) {
-          const unsigned long long mm = wmask[ms[j]];
-          if (__builtin_ctzll(mm) == p) {
+          const unsigned long long mm = wmask[ms[j]] & keep;
+          if (mm && __builtin_ctzll(mm) == p) {
             const int later = __builtin_popcountll(mm) - 1;
             ++n_a;
             n_b += later;
@@ -1025,7 +1035,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
   if (tid == 0) {
     const int bytes = 16 + 8 * n_ext + 5 * n_ri;
-    *reinterpret_cast<uint4*>(var) = make_uint4(n_ri, n_wu, n_ext, bytes);
+    *reinterpret_cast<uint4*>(var) = make_uint4(n_ri, n_wu | (rmask ? 0x80000000u : 0u), n_ext, bytes);
     a.sizes[plan_id] = bytes;
   }
   if (set == 1) {
@@ -1036,7 +1046,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
 #pragma unroll
     for (int i = 0; i < KP; i += 2) rec[i / 2] = static_cast<uint32_t>(ms[i]) | (static_cast<uint32_t>(ms[i + 1]) << 16);
 #pragma unroll
-    for (int i = 0; i < KP; ++i) rec[KP / 2 + i] = __float_as_uint(ws[i]);
+    for (int i = 0; i < KP; ++i) rec[KP / 2 + i] = seg0 >= 0 ? 0u : __float_as_uint(ws[i]);   // no state after a reset
     // in-chunk contributions in ascending q, and their coefficient sum: the first kInline into the record
     const int e0 = inc_a - n_a;
     int k = e0, j = 0;
@@ -1084,8 +1094,8 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     for (int j = 0; j < KP; ++j) {
       if (j >= kk) break;
       const int m = ms[j];
-      unsigned long long mm = wmask[m];
-      if (__builtin_ctzll(mm) != p) continue;   // p is the slot's first writer in the chunk
+      unsigned long long mm = wmask[m] & keep;
+      if (!mm || __builtin_ctzll(mm) != p) continue;   // p is the slot's first (kept) writer in the chunk
       mm &= mm - 1ull;
       const uint32_t cw = __float_as_uint(pw[L - 1 - p] * ws[j]) | (mm ? 0x80000000u : 0u);
       const int u = mm ? u_m++ : u_s++;
@@ -1383,6 +1393,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     }
     const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
     const int n_ri = hdr[0], n_ext = hdr[2];
+    const bool chunk_reset = hdr[1] & 0x80000000u;
     const uint2* ext = reinterpret_cast<const uint2*>(var + 16);
     const float* ri_c = reinterpret_cast<const float*>(var + 16 + 8 * n_ext);
     const unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
@@ -1442,11 +1453,17 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     }
     lds_barrier();
     if (more) fetch_chunk<1>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
-    // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small)
+    // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
     float fade = lam_chunk;
     if (L != kChunk) fade = pw[L];
     float mu_new = mu * fade;
-    if (!(mu_new >= kMuFloor)) {
+    if (chunk_reset) {
+      float4* a4 = reinterpret_cast<float4*>(A);
+      for (int i = tid; i < (M + 1) * CW / 4; i += kScanThreads) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = tid; i <= M; i += kScanThreads) cnt[i] = 0.f;
+      mu_new = 1.f;
+      lds_barrier();
+    } else if (!(mu_new >= kMuFloor)) {
       for (int i = tid; i < (M + 1) * CW; i += kScanThreads) A[i] *= mu_new;
       for (int i = tid; i <= M; i += kScanThreads) cnt[i] *= mu_new;
       mu_new = 1.f;
@@ -2062,7 +2079,8 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
 
 int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* kz, int64_t kz_row_stride,
                    const void* qz, int64_t qz_row_stride, const void* v, int64_t v_row_stride,
-                   const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype, void* r_out,
+                   const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype, const uint8_t* reset,
+                   void* r_out,
                    int64_t out_row_stride, sdm_rt_dtype out_dtype, const float* state_in_mem,
                    const float* state_in_cnt, float* state_out_mem, float* state_out_cnt, void* workspace,
                    size_t workspace_bytes, void* stream) {
@@ -2122,6 +2140,7 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   pa.gl = dims->write_gate ? gate_logits : nullptr;
   pa.g_stride = gate_row_stride;
   pa.decay = params->decay;
+  pa.reset = reset;
   pa.plans = plans;
   pa.sizes = sizes;
   pa.B = p.B;

@@ -104,8 +104,8 @@ class RunTimeSdm(nn.Module):
         return W, wo
 
     def _check(self, x, reset):
-        if reset is not None:
-            raise NotImplementedError("RunTimeSdm HIP core: reset (BOS segment masks) is not implemented")
+        if reset is not None and (reset.dim() != 2 or tuple(reset.shape) != tuple(x.shape[:2])):
+            raise ValueError(f"reset must be [B, T] = {tuple(x.shape[:2])}, got {tuple(reset.shape)}")
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             raise RuntimeError("RunTimeSdm HIP core is forward-only: call it under torch.no_grad() or "
                                "torch.inference_mode()")
@@ -137,7 +137,8 @@ class RunTimeSdm(nn.Module):
 
     def forward(self, x, reset=None):
         """x [B, T, d] -> y [B, T, d] in x.dtype; every call starts from an empty memory
-        (track4_onesdm_models.py:249-274).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)."""
+        (track4_onesdm_models.py:249-274).  reset [B, T] bool: where True the memory is emptied before that position
+        reads (a BOS starts a new document, :229-233).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)."""
         B, T, _ = x.shape
         if not self.enabled:
             return torch.zeros_like(x)
@@ -152,7 +153,7 @@ class RunTimeSdm(nn.Module):
                 addr_b=self.addr_b, onorm_w=self.onorm_w if self.out_norm else None,
                 gate_bias=self.wg.bias if self.write_gate else None, k=self.k, read_mode=self.read_mode,
                 out_norm=self.out_norm, read_eps=self.read_eps, out_norm_eps=self.out_norm_eps, out_dtype=dt,
-                want_state=self.keep_state, workspace=self._ws)
+                want_state=self.keep_state, workspace=self._ws, reset=reset)
             r, state = (res if self.keep_state else (res, None))
             y = torch.matmul(r, wo.t()).to(x.dtype)
         self._gate_src = (g, self.wg.bias.detach() if self.write_gate else None, (B, T, H), x.device)

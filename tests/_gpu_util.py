@@ -45,7 +45,7 @@ def to_dev(a, dtype):
 
 
 def gpu_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, read_mode="mean", out_norm=True,
-             state_in=None, want_state=False, fused=False):
+             state_in=None, want_state=False, fused=False, reset=None):
     """Run sdm_rt_forward; returns r (numpy float32, (B, T, H*dh)) and optionally the state."""
     if fused:   # one buffer with all four inputs side by side (the layout of a fused projection)
         parts = [kz, qz, V] + ([g] if g is not None else [])
@@ -69,7 +69,8 @@ def gpu_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, read_mode=
     res = core.core_forward(kz_d, qz_d, V_d, g_d, keys1=tp["keys1"], keys2=tp["keys2"], log_scale=tp["log_scale"],
                             decay=tp["decay"], addr_b=tp["addr_b"], onorm_w=tp["onorm_w"],
                             gate_bias=tp["gate_bias"] if g is not None else None, k=k, read_mode=read_mode,
-                            out_norm=out_norm, out_dtype=out_dtype, state_in=st, want_state=want_state)
+                            out_norm=out_norm, out_dtype=out_dtype, state_in=st, want_state=want_state,
+                            reset=None if reset is None else torch.from_numpy(np.asarray(reset, bool)).cuda())
     torch.cuda.synchronize()
     if want_state:
         r, (m, c) = res

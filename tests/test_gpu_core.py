@@ -109,3 +109,53 @@ def test_bench_shape_bf16():
     kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
     flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, slabs=[(0, 0), (3, 7), (7, 11)])
     say("bench-shape picks that differ from the oracle (all at near-ties):", flips)
+
+
+@pytest.mark.parametrize("T", [64, 150])
+def test_resets_match_the_oracle(T):
+    """BOS resets (forward(x, reset), OM:229-233): the memory is emptied before the position reads.  Resets at chunk
+    starts, inside chunks, twice in one chunk, at the last position, and a row without any; fades 0, 0.5, 0.97, 1."""
+    from oracle import sdm_fp64 as O
+    from tests._gpu_util import assert_close, gpu_address
+    B, H, dh = 3, 4, 16
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 16, 8, seed=90 + T, decays=(0.0, 0.5, 0.97, 1.0))
+    reset = np.zeros((B, T), bool)
+    reset[0, [0, 20, 31, T - 1]] = True
+    reset[1, [1, 63]] = True
+    if T > 64:
+        reset[1, [64, 100, 101]] = True
+    r, (mem, cnt) = gpu_core(kz, qz, V, g, p, 8, want_state=True, reset=reset)
+    siw, _, ww = gpu_address(kz, p, 8, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8)
+    Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    num, den, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                           wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
+                                           (np.zeros((B, H, 64, dh)), np.zeros((B, H, 64))), reset=reset)
+    r64 = O.finish(num, den, "mean", 1e-3, True, p["onorm_w"].astype(np.float64), 1e-2)
+    assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 1e-5, msg="read-out with resets")
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+    # a reset at position 0 changes nothing but rounding (the memory starts empty; the slab's scale restarts at 1)
+    reset0 = np.zeros((B, T), bool)
+    reset0[:, 0] = True
+    np.testing.assert_allclose(gpu_core(kz, qz, V, g, p, 8, reset=reset0), gpu_core(kz, qz, V, g, p, 8),
+                               atol=1e-5, rtol=1e-5)
+
+
+def test_module_forward_with_resets_equals_decode_steps():
+    """RunTimeSdm.forward(x, reset) = RunTimeSdm.step token by token with the same resets (float32)."""
+    from sdmchat_amd import RunTimeSdm, synthetic as S
+    cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8)
+    prm = S.layer_params(cfg, seed=91, decays=(0.0, 0.6, 0.97, 1.0))
+    m = RunTimeSdm(64, heads=4, n_sub=8, d_a=16, k=8, decays=tuple(float(v) for v in prm["decays_fixed"]))
+    m.load_state_dict({n: torch.from_numpy(v) for n, v in prm.items()}, strict=True)
+    m = m.cuda().eval()
+    x = torch.from_numpy(S.layer_input(2, 90, 64, seed=92)).cuda()
+    reset = torch.zeros(2, 90, dtype=torch.bool, device="cuda")
+    reset[0, 30] = reset[0, 70] = reset[1, 64] = True
+    with torch.no_grad():
+        y = m(x, reset)
+        st = m.decode_state(2)
+        ys = torch.stack([m.step(x[:, t], st, reset=reset[:, t]) for t in range(90)], 1)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(ys.cpu().numpy(), y.cpu().numpy(), atol=2e-5, rtol=1e-4)

@@ -63,7 +63,7 @@ def test_invalid_dims_are_rejected_before_launch(over, msg):
     assert lib.sdm_rt_workspace_bytes(ctypes.byref(dims)) == 0
     prm = _lib.SdmRtParams()
     one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, one, 4096, 0,
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, None, one, 4096, 0,
                             None, None, None, None, one, 1 << 30, None)
     assert rc != 0
     assert msg in lib.sdm_rt_last_error().decode()
@@ -74,17 +74,17 @@ def test_missing_pointers_and_small_workspace_are_rejected():
     dims = _dims()
     prm = _lib.SdmRtParams()
     one = ctypes.c_void_p(16)
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, one, 4096, 0,
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, None, one, 4096, 0,
                             None, None, None, None, one, 1 << 30, None)
     assert rc == -1 and "keys1" in lib.sdm_rt_last_error().decode()
     prm = _lib.SdmRtParams(one, one, None, one, one, one, None)
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, one, 4096, 0,
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 0, None, one, 4096, 0,
                             None, None, None, None, one, 1024, None)
     assert rc == -2 and "workspace" in lib.sdm_rt_last_error().decode()
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, one, 4096, 0,
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, None, 0, 0, None, one, 4096, 0,
                             None, None, None, None, one, 1 << 30, None)
     assert rc == -1 and "gate_logits" in lib.sdm_rt_last_error().decode()
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 7, one, 4096, 0,
+    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), one, 4096, one, 4096, one, 4096, one, 4096, 7, None, one, 4096, 0,
                             None, None, None, None, one, 1 << 30, None)
     assert rc == -1 and "dtype" in lib.sdm_rt_last_error().decode()
 

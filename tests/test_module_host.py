@@ -63,8 +63,10 @@ def test_no_cpu_fallback():
         m(x)
     with pytest.raises(RuntimeError, match="forward-only"):
         m(x)
-    with torch.no_grad(), pytest.raises(NotImplementedError):
+    with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm device"):
         m(x, reset=torch.zeros(1, 4, dtype=torch.bool))
+    with torch.no_grad(), pytest.raises(ValueError, match="reset must be"):
+        m(x, reset=torch.zeros(1, 5, dtype=torch.bool))
 
 
 def test_disabled_returns_zeros_without_the_library():
