@@ -26,6 +26,12 @@ place) timed as a HIP graph of 64 steps replayed 513 times, so the state runs th
 = replay time / 64 (device time, no host launch cost), reported overall (median) and at positions 0, 1,024, 8,192
 and 32,768 to show that the cost of a step does not grow with the position.  --no-decode skips it.
 
+model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12 layers of d=768 with this mixer
+(12 heads, M=1,024, k=8): "swiglu" = each layer's per-token step a SwiGLU of hidden 2,048 (the survey's config 3),
+"trained_sdm" = a TrainedSdm of 4,096 slots, one head of width 768, k=16 (config 4); bf16 weights and activations,
+synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm.
+--no-model skips it.
+
 --copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
 """
 import argparse
@@ -129,6 +135,49 @@ def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
             f"{graph_steps}"}
 
 
+def model_bench(dev, vocab=32768, layers=12, mlp_f=2048):
+    """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms (see the module doc)."""
+    import numpy as np
+    import torch
+
+    from sdmchat_amd import OneSdmLM
+
+    out = {}
+    gen = torch.Generator().manual_seed(11)
+    idx = torch.randint(0, vocab, (B, T), generator=gen).to(dev)
+    decays = tuple(float(v) for v in np.random.Generator(np.random.PCG64(3)).uniform(0.9, 0.999, H))
+    for name, kw in (("swiglu", dict(ffn="mlp")),
+                     ("trained_sdm", dict(ffn="sdm", sdm_n_sub=64, sdm_heads=1, sdm_k=16))):
+        torch.manual_seed(5)
+        m = OneSdmLM(vocab, d=D, layers=layers, mlp_f=mlp_f, heads=H, n_sub=N_SUB, d_a=D_A, k=K, decays=decays, **kw)
+        with torch.no_grad():
+            for n, p in m.named_parameters():
+                if n.endswith(("wo.weight", "wg.weight", "values")):
+                    p.normal_(0.0, 0.02, generator=gen)
+        m = m.to(dev).to(torch.bfloat16).eval()
+        with torch.no_grad():
+            for _ in range(2):
+                m(idx)
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                m(idx)
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+        ms = sorted(ts)[2]
+        out[name] = {"ms": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
+        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
+        del m
+        torch.cuda.empty_cache()
+    out["workload"] = (f"OneSdmLM forward (logits): B={B} T={T}, vocabulary {vocab}, {layers} layers, d={D}, mixer "
+                       f"{H} heads M={N_SUB * N_SUB} k={K}; swiglu: hidden {mlp_f}; trained_sdm: 4,096 slots, 1 head, "
+                       f"k=16; bf16")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +187,7 @@ def main():
     ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
+    ap.add_argument("--no-model", action="store_true", help="skip the whole-model measurement")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
@@ -208,6 +258,7 @@ def main():
         copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
         del big, big2
         decode = None if a.no_decode else decode_bench(m, dev)
+        model = None if a.no_model else model_bench(dev)
 
     ms_per_step = wall * 1e3 / a.steps
     tokens = B * T
@@ -241,6 +292,8 @@ def main():
     }
     if decode is not None:
         rec["decode"] = decode
+    if model is not None:
+        rec["model"] = model
     if not a.no_cpu:
         log("cpu baseline ...")
         rec["cpu_baseline"] = cpu_baseline()

@@ -65,7 +65,8 @@ typedef struct {
   const float* keys2;     /* [H][n_sub][d_a/2] */
   const float* addr_b;    /* [H][d_a] added to every key and query; may be NULL (zero) */
   const float* log_scale; /* [H]; softmax temperature is exp(log_scale) */
-  const float* decay;     /* [H] per-head fade lambda in [0, 1] (RunTimeSdm.decay(), :192-193) */
+  const float* decay;     /* [H] per-head fade lambda in [0, 1] (RunTimeSdm.decay(), :192-193); not read by
+                           * sdm_rt_address (may be NULL there) */
   const float* onorm_w;   /* [H][dh]; read only when out_norm */
   const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
 } sdm_rt_params;
@@ -139,6 +140,16 @@ int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params,
                        float* state_mem, float* state_cnt, float* state_scale,
                        void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* The weighted read of the picked rows of per-head value tables: TrainedSdm.forward's embedding_bag
+ * (track4_onesdm_models.py:448-455), out[n][h*dh + c] = sum_j weight[b][h][t][j] * values[h][slot[b][h][t][j]][c]
+ * over the kk picks of token n = b*T + t, summed in float32 in pick order.
+ *   slots, weights  [B][H][T][pitch] as sdm_rt_address writes them (pitch = sdm_rt_pick_pitch(dims))
+ *   values          [H][M][dh] (M = n_sub^2, dh = dims->head_dim, a multiple of 4 of any size), dtype values_dtype
+ *   out             [B*T rows] of H * dh, dtype out_dtype, row stride out_row_stride (elements) */
+int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float* weights,
+                      const void* values, sdm_rt_dtype values_dtype,
+                      void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype, void* stream);
 
 /* The input norm of RunTimeSdm (RMSNorm, experiments/track4/sdmllm/track4_sdmllm_models.py:63-71) with the
  * reference's rounding: out = cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), the mean and product in float32,

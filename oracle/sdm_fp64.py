@@ -173,7 +173,7 @@ def finish(num, den, read_mode="mean", read_eps=1e-3, out_norm=True, onorm_w=Non
     return r
 
 
-def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False):
+def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False, reset=None):
     """The SDM core between the projections and the output map.
 
     kz, qz (B, T, H, d_a) already include addr_b; V (B, T, H, dh); gate_logits (B, T, H) or None (gate off).
@@ -195,7 +195,7 @@ def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False):
     n_sub = p["keys1"].shape[1]
     M = n_sub * n_sub
     state = (np.zeros((B, H, M, Vb.shape[-1])), np.zeros((B, H, M)))
-    num, den, mem, cnt = scan_recurrence(bh(siw), bh(ww), bh(sir), bh(wr), Vb, p["decay"], state)
+    num, den, mem, cnt = scan_recurrence(bh(siw), bh(ww), bh(sir), bh(wr), Vb, p["decay"], state, reset=reset)
     r = finish(num, den, cfg.get("read_mode", "mean"), cfg.get("read_eps", 1e-3), cfg.get("out_norm", True),
                p.get("onorm_w"), cfg.get("out_norm_eps", 1e-2)).transpose(0, 2, 1, 3)
     if return_parts:
@@ -203,7 +203,7 @@ def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False):
     return r
 
 
-def layer_forward(x, p, cfg):
+def layer_forward(x, p, cfg, reset=None):
     """Whole RunTimeSdm.forward in float64 (OM:195-213 prepare, OM:249-274 forward, OM:243-247 finish).
 
     x (B, T, d); p holds the module's parameters under their state_dict names ('norm.w', 'wk.weight', ...,
@@ -220,5 +220,78 @@ def layer_forward(x, p, cfg):
     g = (hx @ p["wg.weight"].T + p["wg.bias"]) if cfg.get("write_gate", True) else None
     core_p = dict(keys1=p["keys1"], keys2=p["keys2"], log_scale=p["log_scale"], decay=p["decay"],
                   onorm_w=p.get("onorm_w"))
-    r = core_forward(kz, qz, V, g, core_p, cfg)
+    r = core_forward(kz, qz, V, g, core_p, cfg, reset=reset)
     return r.reshape(B, T, d) @ p["wo.weight"].T
+
+
+def table_read(si, w, values):
+    """The weighted read of picked table rows (TrainedSdm.forward's embedding_bag, OM:448-455).
+
+    si (N, H, kk) int, w (N, H, kk), values (H, M, dh) -> (N, H, dh)."""
+    H = values.shape[0]
+    rows = np.asarray(values, np.float64)[np.arange(H)[None, :, None], si]   # (N, H, kk, dh)
+    return np.einsum("nhk,nhkd->nhd", np.asarray(w, np.float64), rows)
+
+
+def trained_sdm_forward(x, p, cfg, return_parts=False):
+    """TrainedSdm.forward (OM:414-457) in float64: RMSNorm, the query map, pk_address, softmax(exp(log_scale) *
+    score), the weighted sum of the picked value rows, the output map.  p: norm.w, wq.weight, keys1, keys2, values,
+    log_scale, wo.weight.  cfg: heads, d_a, k."""
+    B, T, d = x.shape
+    H, d_a, k = cfg["heads"], cfg["d_a"], cfg["k"]
+    hx = rms_norm(np.asarray(x, np.float64), p["norm.w"])
+    q = (hx @ np.asarray(p["wq.weight"], np.float64).T).reshape(B * T, H, d_a)
+    sv, si = pk_address(q, p["keys1"], p["keys2"], k)
+    w = address_weights(sv, p["log_scale"])
+    r = table_read(si, w, p["values"]).reshape(B, T, d)
+    y = r @ np.asarray(p["wo.weight"], np.float64).T
+    if return_parts:
+        return y, dict(q=q, sv=sv, si=si, w=w, r=r)
+    return y
+
+
+def silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def swiglu(x, gate_w, up_w, down_w):
+    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97)."""
+    return (silu(x @ gate_w.T) * (x @ up_w.T)) @ down_w.T
+
+
+def model_forward(idx, p, cfg, margins=None):
+    """OneSdmLM.forward (OM:471-555, archive off) in float64: embedding, per layer x + RunTimeSdm(x, reset) and
+    x + SwiGLU(RMSNorm x) (ffn 'mlp') or x + TrainedSdm(x) (ffn 'sdm'), final RMSNorm, tied head.
+
+    idx (B, T) int; p: the model's state dict as float64 arrays; cfg: layers, heads, d_a, k, ffn, mem, tie,
+    reset_at_bos, bos_id, sdm_heads, sdm_d_a, sdm_k and the mixer options of core_forward.  When ``margins`` is a
+    list, the smallest fp64 top-k margin of every addressing is appended to it.  Returns logits (B, T, V)."""
+    E = p["emb.weight"]
+    x = E[np.asarray(idx)]
+    B, T, d = x.shape
+    reset = (np.asarray(idx) == cfg.get("bos_id", 0)) if cfg.get("reset_at_bos") else None
+    for i in range(cfg["layers"]):
+        if cfg.get("mem", True):
+            pre = f"mems.{i}."
+            lp = {n[len(pre):]: v for n, v in p.items() if n.startswith(pre)}
+            lp["decay"] = lp["decays_fixed"] if "decays_fixed" in lp else 1.0 / (1.0 + np.exp(-lp["decay_logit"]))
+            if margins is not None:
+                H, d_a = cfg["heads"], cfg["d_a"]
+                hx = rms_norm(x, lp["norm.w"])
+                for wn in ("wk.weight", "wq.weight"):
+                    z = (hx @ lp[wn].T).reshape(B * T, H, d_a) + lp["addr_b"]
+                    margins.append(float(topk_margin(z, lp["keys1"], lp["keys2"], cfg["k"]).min()))
+            x = x + layer_forward(x, lp, cfg, reset)
+        if cfg.get("ffn", "mlp") == "mlp":
+            x = x + swiglu(rms_norm(x, p[f"mnorms.{i}.w"]), p[f"mlps.{i}.gate.weight"], p[f"mlps.{i}.up.weight"],
+                           p[f"mlps.{i}.down.weight"])
+        elif cfg["ffn"] == "sdm":
+            pre = f"sdms.{i}."
+            sp = {n[len(pre):]: v for n, v in p.items() if n.startswith(pre)}
+            scfg = dict(heads=cfg["sdm_heads"], d_a=cfg["sdm_d_a"], k=cfg["sdm_k"])
+            y, parts = trained_sdm_forward(x, sp, scfg, return_parts=True)
+            if margins is not None:
+                margins.append(float(topk_margin(parts["q"], sp["keys1"], sp["keys2"], scfg["k"]).min()))
+            x = x + y
+    h = rms_norm(x, p["nf.w"])
+    return h @ (E.T if cfg.get("tie", True) else p["head.weight"].T)

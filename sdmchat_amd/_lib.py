@@ -64,6 +64,8 @@ SIGNATURES = {
                                           c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_i64, ctypes.c_int,
                                           c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_table_read": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), c_void_p, c_void_p, c_void_p, ctypes.c_int,
+                                         c_void_p, c_i64, ctypes.c_int, c_void_p]),
     "sdm_rt_rms_norm": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p,
                                        ctypes.c_float, c_void_p, c_i64, ctypes.c_int, c_void_p]),
     "sdm_rt_last_error": (ctypes.c_char_p, []),

@@ -62,11 +62,31 @@ def _params(device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias):
     return prm, held
 
 
+class ParamCache:
+    """The float32, contiguous copies of a module's core parameters and their SdmRtParams, rebuilt only when one of
+    the source tensors changes (data pointer or version)."""
+
+    def __init__(self):
+        self.key = None
+        self.value = None
+
+    def get(self, device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias, decay_source=None):
+        """decay may be a callable computing it; decay_source is then the tensor it derives from (the cache key)."""
+        srcs = (keys1, keys2, addr_b, log_scale, decay_source if callable(decay) else decay, onorm_w, gate_bias)
+        key = (device,) + tuple(None if t is None else (t.data_ptr(), t._version, t.dtype) for t in srcs)
+        if self.key != key:
+            dec = decay() if callable(decay) else decay
+            self.value = _params(device, keys1, keys2, addr_b, log_scale, dec, onorm_w, gate_bias)
+            self.key = key
+        return self.value
+
+
 def workspace_bytes(dims):
     return _lib.load().sdm_rt_workspace_bytes(ctypes.byref(dims))
 
 
-def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_bias=None):
+def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_bias=None, padded=False,
+            params=None):
     """Product-key addressing of one address set (pk_address + softmax weights [+ gate]).
 
     z [B, T, H * d_a]; keys [H, n_sub, d_a/2].  Returns slots int32, scores and weights float32, each
@@ -83,8 +103,9 @@ def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_b
             raise ValueError("gate_logits must have the dtype of z")
         gs = _rows(gate_logits, "gate_logits", B, T, H)
     dev = z.device
-    decay = torch.zeros(H, device=dev)
-    prm, held = _params(dev, keys1, keys2, addr_b, log_scale, decay, None, gate_bias)
+    if params is None:   # the addressing reads no fade
+        params = _params(dev, keys1, keys2, addr_b, log_scale, None, None, gate_bias)
+    prm, held = params
     pitch = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
     if pitch <= 0:
         raise _lib.SdmRtError(lib.sdm_rt_last_error().decode() or "invalid dimensions")
@@ -97,6 +118,8 @@ def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_b
                             _ptr(slots), _ptr(scores), _ptr(weights), None, 0, ctypes.c_void_p(stream))
     _lib.check(rc, lib)
     del held
+    if padded:   # the kernel's own [B, H, T, pitch] arrays (pads: slot -1, weight 0)
+        return slots, scores, weights
     return slots[..., :kk], scores[..., :kk], weights[..., :kk]
 
 
@@ -169,6 +192,45 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
     _lib.check(rc, lib)
     if want_state:
         return out, (mem_out, cnt_out)
+    return out
+
+
+def table_read(slots, weights, values, k, out_dtype=torch.float32, out=None):
+    """The weighted read of picked table rows (TrainedSdm.forward's embedding_bag, track4_onesdm_models.py:448-455).
+
+    slots, weights [B, H, T, pitch] as address() returns them (the first kk entries are the picks); values
+    [H, M, dh] float32 or bfloat16 (M = n_sub^2).  Returns out [B, T, H * dh] in out_dtype: the float32 sum over
+    the picks of weight * row."""
+    lib = _lib.load()
+    B, H, T, pitch = slots.shape
+    Hv, M, dh = values.shape
+    n_sub = int(round(M ** 0.5))
+    if Hv != H or n_sub * n_sub != M:
+        raise ValueError(f"values must be [H={H}, n_sub^2, dh], got {tuple(values.shape)}")
+    if slots.dtype != torch.int32 or weights.dtype != torch.float32 or tuple(weights.shape) != tuple(slots.shape):
+        raise ValueError("slots must be int32 and weights float32, both [B, H, T, pitch]")
+    if values.dtype not in _DT:
+        raise ValueError(f"values: dtype {values.dtype} is not float32 or bfloat16")
+    dims = make_dims(B, T, H, dh, 2, n_sub, k, out_norm=False, write_gate=False)
+    want = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
+    kk = min(k, min(k, n_sub) ** 2)
+    if pitch < kk or want <= 0:
+        raise ValueError(f"slots hold {pitch} picks per (token, head); k={k}, n_sub={n_sub} needs {kk}")
+    if pitch != want:   # repack into the kernel's pitch (pads: slot -1, weight 0)
+        ps = torch.full((B, H, T, want), -1, dtype=torch.int32, device=slots.device)
+        pw = torch.zeros((B, H, T, want), dtype=torch.float32, device=slots.device)
+        ps[..., :kk] = slots[..., :kk]
+        pw[..., :kk] = weights[..., :kk]
+        slots, weights = ps, pw
+    dev = values.device
+    sl, wt, vals = slots.contiguous(), weights.contiguous(), values.detach().contiguous()
+    if out is None:
+        out = torch.empty(B, T, H * dh, dtype=out_dtype, device=dev)
+    ostride = _rows(out, "out", B, T, H * dh)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_table_read(ctypes.byref(dims), _ptr(sl), _ptr(wt), _ptr(vals), _DT[vals.dtype], _ptr(out), ostride,
+                               _DT[out.dtype], ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
     return out
 
 

@@ -10,7 +10,8 @@
 //                   the in-chunk writes its plan lists, then adds the chunk's faded writes (_chunk :215-241)
 //   finish_kernel   per (token, head): r * rsqrt(mean(r^2) + eps) * onorm_w (finish :243-246)
 // address_kernel runs the addressing alone for sdm_rt_address; a decode step (sdm_rt_decode_step) is one addressing
-// launch for both address sets and decode_kernel, one token per stream.
+// launch for both address sets and decode_kernel, one token per stream; table_read_kernel is the weighted row read of
+// TrainedSdm (sdm_rt_table_read).
 //
 // Decay bookkeeping in scan_kernel: the slab holds A with the true state S = mu * A (mu a per-slab scalar).  A chunk
 // of L positions reads mu * lam^p * A[slot] at offset p, then mu <- mu * lam^L and each write at offset q adds
@@ -316,7 +317,8 @@ __device__ __forceinline__ void top_k_desc(double (&c)[N]) {
   for (int g = 1; g < N / K; ++g) merge_top_desc<K>(c, c + g * K);
 }
 
-// n values of type InT from p into floats: 16-byte loads when p is 16-byte aligned, element loads otherwise
+// n values of type InT from p into floats: 16-byte (or, for 4 bfloat16, 8-byte) loads when p is aligned to them,
+// element loads otherwise
 template <int n, typename InT>
 __device__ __forceinline__ void load_vals(const InT* p, float (&out)[n]) {
   constexpr int kBytes = n * static_cast<int>(sizeof(InT));
@@ -336,6 +338,16 @@ __device__ __forceinline__ void load_vals(const InT* p, float (&out)[n]) {
           }
         }
       }
+      return;
+    }
+  }
+  if constexpr (kBytes == 8 && sizeof(InT) == 2) {
+    if ((reinterpret_cast<uintptr_t>(p) & 7u) == 0) {
+      const uint2 u = *reinterpret_cast<const uint2*>(p);
+      out[0] = __uint_as_float(u.x << 16);
+      out[1] = __uint_as_float(u.x & 0xffff0000u);
+      out[2] = __uint_as_float(u.y << 16);
+      out[3] = __uint_as_float(u.y & 0xffff0000u);
       return;
     }
   }
@@ -1787,6 +1799,53 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// table read: the weighted sum of the picked rows of per-head value tables (TrainedSdm.forward's embedding_bag,
+// track4_onesdm_models.py:448-455): out[n][h * dh + c] = sum_j w[n][h][j] * values[h][slot[n][h][j]][c] in float32,
+// picks in order.  One wave per (token, head); lane l takes columns 4l, 4l + 256, ... (dh a multiple of 4).
+template <int KP, typename VT, typename OutT>
+__global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restrict__ slots,
+                                                         const float* __restrict__ wts,
+                                                         const VT* __restrict__ values, OutT* __restrict__ out,
+                                                         int64_t out_stride, int B, int T, int H, int M, int dh,
+                                                         int kk) {
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave >= static_cast<int64_t>(B) * T * H) return;   // whole waves
+  const int64_t n = wave / H;
+  const int h = static_cast<int>(wave - n * H);
+  const int b = static_cast<int>(n / T);
+  const int t = static_cast<int>(n - static_cast<int64_t>(b) * T);
+  const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
+  int sl[KP];
+  float w[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    sl[j] = min(max(slots[pb + j], 0), M - 1);   // pads (-1) and stray ids stay inside the table
+    w[j] = j < kk ? wts[pb + j] : 0.f;
+  }
+  const VT* tab = values + static_cast<int64_t>(h) * M * dh;
+  for (int c0 = 4 * lane; c0 < dh; c0 += 256) {
+    float v[KP][4];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      if (j < kk) {
+        load_vals<4, VT>(tab + static_cast<int64_t>(sl[j]) * dh + c0, v[j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[j][e] = 0.f;
+      }
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(w[j], v[j][e], acc[e]);
+    }
+    store_vals<4, OutT>(out + n * out_stride + static_cast<int64_t>(h) * dh + c0, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // host side
 struct Plan {
   int B, T, H, dh, d_a, half, n_sub, M, k, c1, kk, pitch, cap, n_chunks;
@@ -1796,13 +1855,14 @@ struct Plan {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int make_plan(const sdm_rt_dims* d, Plan* p) {
+// core: the shape must suit the scan and the decode step too (head_dim); the addressing alone needs only the keys
+int make_plan(const sdm_rt_dims* d, Plan* p, bool core = true) {
   if (!d) return set_err(SDM_RT_EINVAL, "dims is NULL");
   if (d->batch < 0 || d->seq_len < 0) return set_err(SDM_RT_EINVAL, "negative batch or seq_len");
   if (d->heads < 1) return set_err(SDM_RT_EINVAL, "heads must be >= 1");
-  if (d->head_dim < 8 || d->head_dim % 8 != 0)
+  if (core && (d->head_dim < 8 || d->head_dim % 8 != 0))
     return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d must be a positive multiple of 8", d->head_dim);
-  if (d->head_dim > 512) return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d exceeds 512", d->head_dim);
+  if (core && d->head_dim > 512) return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d exceeds 512", d->head_dim);
   if (d->addr_dim < 2 || d->addr_dim % 2 != 0) return set_err(SDM_RT_EINVAL, "addr_dim %d must be even", d->addr_dim);
   if (d->n_sub < 1) return set_err(SDM_RT_EINVAL, "n_sub must be >= 1");
   if (d->top_k < 1) return set_err(SDM_RT_EINVAL, "top_k must be >= 1");
@@ -1823,6 +1883,7 @@ int make_plan(const sdm_rt_dims* d, Plan* p) {
   p->cap = p->c1 <= 8 && p->kk <= 8 ? 8 : 16;
   p->pitch = (p->kk + 7) / 8 * 8;
   p->n_chunks = (p->T + kChunk - 1) / kChunk;
+  if (!core) return SDM_RT_OK;
   if (scan_lds_bytes(p->M, p->pitch, 8, p->n_chunks) > kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations and T = %d do not fit a slab of 8 columns in LDS", p->M,
                    p->T);
@@ -1986,11 +2047,11 @@ int check_dtype(sdm_rt_dtype t, const char* what) {
   return SDM_RT_OK;
 }
 
-int check_params(const sdm_rt_params* prm, bool need_onorm) {
+int check_params(const sdm_rt_params* prm, bool need_onorm, bool need_decay = true) {
   if (!prm) return set_err(SDM_RT_EINVAL, "params is NULL");
   if (!prm->keys1 || !prm->keys2) return set_err(SDM_RT_EINVAL, "keys1/keys2 must not be NULL");
   if (!prm->log_scale) return set_err(SDM_RT_EINVAL, "log_scale must not be NULL");
-  if (!prm->decay) return set_err(SDM_RT_EINVAL, "decay must not be NULL");
+  if (need_decay && !prm->decay) return set_err(SDM_RT_EINVAL, "decay must not be NULL");
   if (need_onorm && !prm->onorm_w) return set_err(SDM_RT_EINVAL, "onorm_w must not be NULL when out_norm is set");
   return SDM_RT_OK;
 }
@@ -2009,7 +2070,7 @@ size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims) {
 
 int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims) {
   Plan p;
-  if (make_plan(dims, &p) != SDM_RT_OK) return 0;
+  if (make_plan(dims, &p, false) != SDM_RT_OK) return 0;
   return p.pitch;
 }
 
@@ -2048,9 +2109,9 @@ int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
                    float* score_out, float* weight_out, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   Plan p;
-  int rc = make_plan(dims, &p);
+  int rc = make_plan(dims, &p, false);
   if (rc) return rc;
-  if ((rc = check_params(params, false))) return rc;
+  if ((rc = check_params(params, false, false))) return rc;
   if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
   if (p.B == 0 || p.T == 0) return SDM_RT_OK;
   if (!z || !slot_out) return set_err(SDM_RT_EINVAL, "z and slot_out must not be NULL");
@@ -2189,6 +2250,39 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
   s.r_out = r_out;
   s.r_stride = out_row_stride;
   return launch_scan(p, s, in_dtype, out_dtype, st);
+}
+
+int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float* weights, const void* values,
+                      sdm_rt_dtype values_dtype, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                      void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p, false);
+  if (rc) return rc;
+  if ((rc = check_dtype(values_dtype, "values_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (p.dh < 4 || p.dh % 4 != 0) return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d must be a positive multiple of 4", p.dh);
+  if (p.B == 0 || p.T == 0) return SDM_RT_OK;
+  if (!slots || !weights || !values || !out) return set_err(SDM_RT_EINVAL, "slots, weights, values and out must not be NULL");
+  if (out_row_stride < static_cast<int64_t>(p.H) * p.dh)
+    return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t waves = static_cast<int64_t>(p.B) * p.T * p.H;
+  const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+#define SDM_RT_TABLE(KP, VT, OT)                                                                                   \
+  hipLaunchKernelGGL((table_read_kernel<KP, VT, OT>), dim3(blocks), dim3(256), 0, st, slots, weights,             \
+                     static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, p.H, p.M, p.dh, \
+                     p.kk)
+#define SDM_RT_TABLE_KP(VT, OT) \
+  if (p.pitch == 8) SDM_RT_TABLE(8, VT, OT); else SDM_RT_TABLE(16, VT, OT)
+  if (values_dtype == SDM_RT_BF16) {
+    if (out_dtype == SDM_RT_BF16) { SDM_RT_TABLE_KP(bf16_t, bf16_t); } else { SDM_RT_TABLE_KP(bf16_t, float); }
+  } else {
+    if (out_dtype == SDM_RT_BF16) { SDM_RT_TABLE_KP(float, bf16_t); } else { SDM_RT_TABLE_KP(float, float); }
+  }
+#undef SDM_RT_TABLE_KP
+#undef SDM_RT_TABLE
+  return check_launch("table_read");
 }
 
 size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims) {

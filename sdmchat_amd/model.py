@@ -1,0 +1,130 @@
+"""OneSdmLM: the whole language model around the run-time SDM mixer (experiments/track4/sdmllm/
+track4_onesdm_models.py:471-555), for its forward.
+
+A drop-in for the reference model: the same constructor, module names and parameter creation order, and the same
+initialisation rule, so a reference state dict loads with ``strict=True``.  Per layer, ``x + mems[i](x, reset)`` runs
+the HIP mixer (RunTimeSdm) and the per-token step is either ``x + SwiGLU(RMSNorm x)`` (dense GEMMs) or
+``x + TrainedSdm(x)`` (the product-key table layer); then the final RMSNorm and the tied head ``h @ E^T``.  The RMSNorms
+run on the RMSNorm kernel; the dense maps are hipBLASLt GEMMs through torch.  The reference's archive memory is a
+separate subsystem and is not built here (archive=True raises).
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import core
+from .runtime_sdm import RMSNorm, RunTimeSdm
+from .trained_sdm import TrainedSdm
+
+
+def _norm(x, norm):
+    """RMSNorm on the kernel with the reference's dtype rule: cast_in(x * rsqrt(mean x^2 + eps)) * w, the result in
+    the promoted dtype of x and w (track4_sdmllm_models.py:69-71)."""
+    return core.rms_norm(x, norm.w, norm.eps, out_dtype=torch.promote_types(x.dtype, norm.w.dtype))
+
+
+class SwiGLU(nn.Module):
+    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97), on dense GEMMs."""
+
+    def __init__(self, d, f):
+        super().__init__()
+        self.gate = nn.Linear(d, f, bias=False)
+        self.up = nn.Linear(d, f, bias=False)
+        self.down = nn.Linear(f, d, bias=False)
+
+    def forward(self, x):
+        return self.down(F.silu(self.gate(x)) * self.up(x))
+
+
+def trained_sdm_params(d, n_sub, heads, d_a):
+    """Parameter count of one TrainedSdm (track4_onesdm_models.py:459-462)."""
+    return d + d * heads * d_a + heads * n_sub * d_a + heads * n_sub * n_sub * (d // heads) + heads + d * d
+
+
+def matched_sdm_n_sub(d, mlp_f, heads, d_a):
+    """The n_sub whose TrainedSdm weight count is closest to one SwiGLU(d, mlp_f) plus its RMSNorm (:465-468)."""
+    target = 3 * d * mlp_f + d
+    return min(range(2, 4097), key=lambda n: abs(trained_sdm_params(d, n, heads, d_a) - target))
+
+
+class OneSdmLM(nn.Module):
+    """Embedding, layers of [x + RunTimeSdm(x); x + FFN(x)], final RMSNorm, tied (or separate) head."""
+
+    kind = "onesdm"
+
+    def __init__(self, V, d=256, layers=4, mlp_f=688, mem=True, heads=4, n_sub=32, d_a=32, k=16,
+                 decays=(0.0, 0.8, 0.99, 1.0), learn_decay=False, write_gate=True, gate_bias=0.0, read_mode="mean",
+                 out_norm=True, addr_scale=8.0, learn_scale=True, chunk=128, mem_in_grad=1.0, out_norm_eps=1e-2,
+                 read_eps=1e-3, addr_bias=0.0, archive=False,
+                 arc_layers=None, arc_d_c=64, arc_n_sub=16, arc_k=4, arc_slot_keep=4, arc_window=16, arc_n_fetch=4,
+                 arc_weighting="soft", tie=True, ffn="mlp", sdm_n_sub=0, sdm_heads=4, sdm_d_a=0, sdm_k=32,
+                 sdm_scale=8.0, sdm_learn_scale=True, reset_at_bos=False, bos_id=0, seed=0):
+        super().__init__()
+        if ffn not in ("mlp", "sdm", "none"):
+            raise ValueError("ffn must be 'mlp', 'sdm' or 'none'")
+        if archive:
+            raise NotImplementedError("OneSdmLM: the archive memory is a separate subsystem, not built here")
+        self.V, self.d, self.n_layers, self.mlp_f, self.tie = V, d, layers, mlp_f, tie
+        self.reset_at_bos, self.bos_id = reset_at_bos, bos_id
+        self.ffn = ffn
+        self.has_mem, self.has_arc = mem, False
+        self.emb = nn.Embedding(V, d)
+        self.mems = nn.ModuleList([RunTimeSdm(d, heads, n_sub, d_a, k, tuple(decays), learn_decay, write_gate,
+                                              gate_bias, read_mode, out_norm, addr_scale, learn_scale, chunk,
+                                              read_eps=read_eps, mem_in_grad=mem_in_grad, out_norm_eps=out_norm_eps,
+                                              addr_bias=addr_bias, seed=seed + 31 * i) for i in range(layers)])
+        for m in self.mems:
+            m.enabled = mem
+        if ffn == "mlp":
+            self.mnorms = nn.ModuleList([RMSNorm(d) for _ in range(layers)])
+            self.mlps = nn.ModuleList([SwiGLU(d, mlp_f) for _ in range(layers)])
+        elif ffn == "sdm":
+            self.sdm_d_a = sdm_d_a or min(32, (d // sdm_heads) // 2 * 2)
+            self.sdm_n_sub = sdm_n_sub or matched_sdm_n_sub(d, mlp_f, sdm_heads, self.sdm_d_a)
+            self.sdms = nn.ModuleList([TrainedSdm(d, self.sdm_n_sub, sdm_heads, self.sdm_d_a, sdm_k, sdm_scale,
+                                                  sdm_learn_scale, seed=seed + 53 * i) for i in range(layers)])
+        self.nf = RMSNorm(d)
+        if not tie:
+            self.head = nn.Linear(d, V, bias=False)
+        nn.init.normal_(self.emb.weight, std=0.02)
+        for n, p in self.named_parameters():
+            if p.dim() == 2 and "emb" not in n and "onorm_w" not in n and "addr_b" not in n:
+                out_map = n.endswith("down.weight") or (n.startswith("sdms.") and n.endswith("wo.weight"))
+                nn.init.normal_(p, std=0.02 / math.sqrt(2 * layers) if out_map else 0.02)
+        for m in self.mems:
+            m.reset_init()
+        for s in getattr(self, "sdms", []):
+            s.reset_init()
+
+    def enfold(self, idx):
+        return self.emb(idx)
+
+    def project(self, h):
+        return h @ self.emb.weight.t() if self.tie else self.head(h)
+
+    def unfold(self, x):
+        return self.project(_norm(x, self.nf))
+
+    def residual(self, idx, sequential=False):
+        """The residual stream after the last layer (track4_onesdm_models.py:534-548).  ``sequential`` selects the
+        token recurrence, which the HIP mixer computes in one pass either way."""
+        x = self.enfold(idx)
+        reset = (idx == self.bos_id) if self.reset_at_bos else None
+        for i in range(self.n_layers):
+            m = self.mems[i]
+            if m.enabled:
+                x = x + (m.forward_sequential(x, reset) if sequential else m(x, reset))
+            if self.ffn == "mlp":
+                x = x + self.mlps[i](_norm(x, self.mnorms[i]))
+            elif self.ffn == "sdm":
+                x = x + self.sdms[i](x)
+        return x
+
+    def hidden(self, idx, sequential=False):
+        """The final normalised state the tied head reads (logits = hidden @ E^T)."""
+        return _norm(self.residual(idx, sequential), self.nf)
+
+    def forward(self, idx, sequential=False):
+        return self.project(self.hidden(idx, sequential))

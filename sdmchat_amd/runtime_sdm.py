@@ -76,6 +76,7 @@ class RunTimeSdm(nn.Module):
         self.last_state = None
         self._fused = None
         self._ws = core.CoreWorkspace()
+        self._prm = core.ParamCache()
 
     def reset_init(self):
         """Zero output map and gate weights, constant gate bias (track4_onesdm_models.py:187-190)."""
@@ -102,6 +103,12 @@ class RunTimeSdm(nn.Module):
         wo = self.wo.weight.detach().to(dtype)
         self._fused = (key, W, wo)
         return W, wo
+
+    def _core_params(self, device):
+        """The core's float32 parameters, converted once per change of the module's tensors."""
+        return self._prm.get(device, self.keys1, self.keys2, self.addr_b, self.log_scale, self.decay,
+                             self.onorm_w if self.out_norm else None, self.wg.bias if self.write_gate else None,
+                             decay_source=self.decay_logit if self.learn_decay else self.decays_fixed)
 
     def _check(self, x, reset):
         if reset is not None and (reset.dim() != 2 or tuple(reset.shape) != tuple(x.shape[:2])):
@@ -153,7 +160,7 @@ class RunTimeSdm(nn.Module):
                 addr_b=self.addr_b, onorm_w=self.onorm_w if self.out_norm else None,
                 gate_bias=self.wg.bias if self.write_gate else None, k=self.k, read_mode=self.read_mode,
                 out_norm=self.out_norm, read_eps=self.read_eps, out_norm_eps=self.out_norm_eps, out_dtype=dt,
-                want_state=self.keep_state, workspace=self._ws, reset=reset)
+                want_state=self.keep_state, workspace=self._ws, reset=reset, params=self._core_params(x.device))
             r, state = (res if self.keep_state else (res, None))
             y = torch.matmul(r, wo.t()).to(x.dtype)
         self._gate_src = (g, self.wg.bias.detach() if self.write_gate else None, (B, T, H), x.device)
@@ -201,7 +208,8 @@ class RunTimeSdm(nn.Module):
                 keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(), addr_b=self.addr_b,
                 onorm_w=self.onorm_w if self.out_norm else None, gate_bias=self.wg.bias if self.write_gate else None,
                 k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
-                out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws)
+                out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
+                params=self._core_params(x.device))
             y = torch.matmul(r, wo.t()).to(x.dtype)
         return y.reshape(x.shape)
 

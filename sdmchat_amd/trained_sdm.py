@@ -1,0 +1,98 @@
+"""TrainedSdm: the trained product-key table layer of SDMCHAT (experiments/track4/sdmllm/track4_onesdm_models.py:414-457)
+on the MI355X kernels.
+
+A drop-in for the reference module: the same constructor, parameter names, shapes and initialisation (a
+``Generator(9876 + seed)`` draws keys1 then keys2; values start at zero), so a reference state dict loads with
+``strict=True``.  The forward runs the RMSNorm kernel, the query map as one GEMM, the product-key addressing kernel
+(sdm_rt_address: top-k of the n_sub^2 slots and the softmax weights) and the weighted table read (sdm_rt_table_read,
+the reference's embedding_bag), then the output map.  Forward only; there is no CPU or torch fallback.
+"""
+import math
+
+import torch
+import torch.nn as nn
+
+from . import core
+from .runtime_sdm import RMSNorm
+
+
+class TrainedSdm(nn.Module):
+    """x [B, T, d] -> y [B, T, d]: per token and head, the softmax-weighted sum of the k table rows that the
+    query's product-key address picks (track4_onesdm_models.py:414-457).  It never mixes positions."""
+
+    def __init__(self, d, n_sub, heads=4, d_a=32, k=32, scale=8.0, learn_scale=True, seed=0):
+        super().__init__()
+        if not (d % heads == 0 and d_a % 2 == 0 and heads * d_a <= d):
+            raise ValueError("TrainedSdm needs d % heads == 0, an even d_a and heads * d_a <= d")
+        g = torch.Generator().manual_seed(9876 + seed)
+        self.d, self.h, self.dh, self.d_a, self.k = d, heads, d // heads, d_a, k
+        self.n_sub, self.M = n_sub, n_sub * n_sub
+        self.norm = RMSNorm(d)
+        self.wq = nn.Linear(d, heads * d_a, bias=False)
+        self.keys1 = nn.Parameter(torch.randn(heads, n_sub, d_a // 2, generator=g))
+        self.keys2 = nn.Parameter(torch.randn(heads, n_sub, d_a // 2, generator=g))
+        self.values = nn.Parameter(torch.zeros(heads, self.M, self.dh))
+        self.log_scale = nn.Parameter(torch.full((heads,), math.log(scale)), requires_grad=learn_scale)
+        self.wo = nn.Linear(d, d, bias=False)
+        self.last_si = None
+        self._cast = None
+        self._prm = core.ParamCache()
+
+    def reset_init(self):
+        """Zero start: every read is exactly zero, so the layer adds nothing at init (track4_onesdm_models.py:433-436)."""
+        nn.init.zeros_(self.values)
+
+    def _check(self, x):
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise RuntimeError("TrainedSdm HIP path is forward-only: call it under torch.no_grad() or "
+                               "torch.inference_mode()")
+        if x.device.type != "cuda":
+            raise RuntimeError("TrainedSdm HIP path needs a ROCm device tensor")
+        if x.dim() != 3 or x.shape[-1] != self.d:
+            raise ValueError(f"expected x of shape [B, T, {self.d}], got {tuple(x.shape)}")
+
+    def _compute_dtype(self, x):
+        if x.dtype == torch.bfloat16:
+            return torch.bfloat16
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return torch.bfloat16
+        if x.dtype == torch.float32:
+            return torch.float32
+        raise ValueError(f"unsupported input dtype {x.dtype}")
+
+    def _weights(self, dt):
+        """wq and wo in the compute dtype, cached until either changes."""
+        ws = (self.wq.weight, self.wo.weight)
+        key = (dt,) + tuple((w.data_ptr(), w._version) for w in ws)
+        if self._cast is None or self._cast[0] != key:
+            self._cast = (key,) + tuple(w.detach().to(dt) for w in ws)
+        return self._cast[1], self._cast[2]
+
+    def _picks(self, x, dt):
+        """RMSNorm, the query map and the addressing: slots, scores, weights [B, H, T, pitch]."""
+        hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
+        q = torch.matmul(hx, self._weights(dt)[0].t())
+        prm = self._prm.get(x.device, self.keys1, self.keys2, None, self.log_scale, None, None, None)
+        return core.address(q, self.keys1, self.keys2, self.k, self.log_scale, padded=True, params=prm)
+
+    def address(self, x):
+        """x (B, T, d) -> soft weights (B*T, h, kk) and slot ids (B*T, h, kk), as the reference's address()."""
+        self._check(x)
+        B, T, _ = x.shape
+        with torch.autocast("cuda", enabled=False):
+            si, _, w = self._picks(x, self._compute_dtype(x))
+        kk = min(self.k, min(self.k, self.n_sub) ** 2)
+        return (w[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk),
+                si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk).long())
+
+    def forward(self, x):
+        self._check(x)
+        B, T, _ = x.shape
+        dt = self._compute_dtype(x)
+        with torch.autocast("cuda", enabled=False):
+            si, _, w = self._picks(x, dt)
+            r = core.table_read(si, w, self.values, self.k, out_dtype=dt)
+            y = torch.matmul(r, self._weights(dt)[1].t()).to(x.dtype)
+        kk = min(self.k, min(self.k, self.n_sub) ** 2)
+        self.last_si = si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
+        return y

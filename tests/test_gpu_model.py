@@ -1,0 +1,61 @@
+"""GPU parity of the whole OneSdmLM forward (track4_onesdm_models.py:471-555): logits against the fp64 oracle's
+model (oracle.sdm_fp64.model_forward) for the SwiGLU and the TrainedSdm arms, with and without resets at BOS.
+
+Seeds are taken from a deterministic search (on the CPU oracle) for inputs whose every addressing in every layer
+has an fp64 top-k margin above 2e-6, so no pick sits at a near-tie and the logits must agree to float32 accuracy
+(1e-4 relative to the logits' scale, after 2 layers)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sdm_fp64 as O
+from sdmchat_amd import OneSdmLM
+from tests._gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(ffn, reset_at_bos, seed):
+    torch.manual_seed(seed)
+    m = OneSdmLM(97, d=64, layers=2, mlp_f=96, heads=4, n_sub=8, d_a=16, k=8, decays=(0.0, 0.6, 0.95, 1.0),
+                 ffn=ffn, sdm_n_sub=10, sdm_heads=2, sdm_d_a=16, sdm_k=8, reset_at_bos=reset_at_bos, bos_id=3,
+                 addr_bias=0.2, seed=seed)
+    g = torch.Generator().manual_seed(1000 + seed)
+    with torch.no_grad():   # leave the zero start: make every map and table carry signal
+        for n, p in m.named_parameters():
+            if n.endswith(("wo.weight", "wg.weight", "values")):
+                p.copy_(torch.randn(p.shape, generator=g) * (0.3 if n.endswith("values") else 0.1))
+    return m
+
+
+def _clean_seed(ffn, reset_at_bos, idx_fn):
+    for seed in range(30):
+        m = _model(ffn, reset_at_bos, seed)
+        idx = idx_fn(seed)
+        p = {n: v.detach().double().numpy() for n, v in m.state_dict().items()}
+        cfg = dict(layers=2, heads=4, d_a=16, k=8, ffn=ffn, reset_at_bos=reset_at_bos, bos_id=3, sdm_heads=2,
+                   sdm_d_a=16, sdm_k=8)
+        margins = []
+        logits = O.model_forward(idx, p, cfg, margins)
+        if min(margins) > 2e-6:
+            return m, idx, logits
+    pytest.fail("no seed with clean margins")
+
+
+def _idx(seed):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    idx = rng.integers(0, 97, size=(2, 70))
+    idx[0, [0, 25, 64]] = 3   # BOS tokens
+    idx[1, 40] = 3
+    return idx
+
+
+@pytest.mark.parametrize("ffn,reset_at_bos", [("mlp", False), ("mlp", True), ("sdm", True)])
+def test_model_logits_match_oracle(ffn, reset_at_bos):
+    m, idx, want = _clean_seed(ffn, reset_at_bos, _idx)
+    say("OneSdmLM", ffn, "reset_at_bos", reset_at_bos)
+    m = m.cuda().eval()
+    with torch.no_grad():
+        got = m(torch.from_numpy(idx).cuda()).double().cpu().numpy()
+    scale = np.abs(want).max()
+    np.testing.assert_allclose(got, want, atol=1e-4 * scale, rtol=1e-4)
