@@ -188,6 +188,7 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model measurement")
+    ap.add_argument("--model-only", action="store_true", help="only the whole-model measurement (for profiler runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
@@ -199,6 +200,9 @@ def main():
     from sdmchat_amd import RunTimeSdm, core, synthetic as S
 
     dev = torch.device("cuda:0")
+    if a.model_only:
+        print(json.dumps({"model": model_bench(dev)}), flush=True)
+        return
     cfg = S.layer_cfg(d=D, heads=H, n_sub=N_SUB, d_a=D_A, k=K)
     params = S.layer_params(cfg, seed=0)
     m = RunTimeSdm(D, heads=H, n_sub=N_SUB, d_a=D_A, k=K, decays=tuple(float(v) for v in params["decays_fixed"]))
