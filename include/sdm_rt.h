@@ -161,6 +161,68 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
                     const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                     void* stream);
 
+/* ---- training: forward with saved tensors, and the backward ------------------------------------------------
+ * The reference trains RunTimeSdm through torch autograd of its chunked dense forward (RunTimeSdm.forward under
+ * torch.utils.checkpoint, track4_onesdm_models.py:259-268).  These two entry points replace that autograd for the
+ * part between the projections and wo: sdm_rt_forward_train computes what sdm_rt_forward computes and keeps what the
+ * backward needs; sdm_rt_backward returns the gradients of the inputs and core parameters for a gradient dy of r_out.
+ * The picks are held fixed (topk and the slot ids carry no gradient, as in autograd).  The memory starts empty (no
+ * state input) and the state is not returned. */
+
+/* What the forward keeps for the backward (caller-owned device buffers; pitch = sdm_rt_pick_pitch(dims)). */
+typedef struct {
+  int32_t* slots_w;   /* [B][H][T][pitch] write picks, as sdm_rt_address writes them */
+  float* weights_w;   /*   their weights (softmax times the gate) */
+  float* scores_w;    /*   their scores */
+  int32_t* slots_r;   /* [B][H][T][pitch] read picks */
+  float* weights_r;
+  float* scores_r;
+  float* read;        /* [B*T rows] of H * dh float32: the read before the output norm (num / (den + read_eps), or
+                       * num with read_mean 0) */
+  float* den;         /* [B*T][H] float32 read denominators; needed only with read_mean */
+} sdm_rt_saved;
+
+/* Gradients written by sdm_rt_backward (overwritten, not accumulated; float32 device buffers). */
+typedef struct {
+  float* d_kz;                 /* [B*T rows] of H * d_a: d loss / d kz (rows as kz, before addr_b) */
+  int64_t d_kz_row_stride;
+  float* d_qz;                 /* d loss / d qz */
+  int64_t d_qz_row_stride;
+  float* d_v;                  /* [B*T rows] of H * dh */
+  int64_t d_v_row_stride;
+  float* d_gate_logits;        /* [B*T rows] of H; required when write_gate */
+  int64_t d_gate_row_stride;
+  float* d_keys1;              /* [H][n_sub][d_a/2] raw sub-key gradients, or NULL (then d_keys2 NULL too) */
+  float* d_keys2;
+  float* d_addr_b;             /* [H][d_a] or NULL */
+  float* d_log_scale;          /* [H] or NULL */
+  float* d_onorm_w;            /* [H][dh] or NULL (written only with out_norm) */
+  float* d_gate_bias;          /* [H] or NULL (0 without the gate) */
+  float* d_log_decay;          /* [H] or NULL: lambda * d loss / d lambda, the gradient with respect to log lambda
+                                * (finite at lambda = 0); d decay_logit = d_log_decay * (1 - lambda) */
+} sdm_rt_grads;
+
+/* sdm_rt_forward (no state input or output) that also fills *saved.  Workspace: sdm_rt_workspace_bytes(dims). */
+int sdm_rt_forward_train(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                         const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
+                         const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
+                         sdm_rt_dtype in_dtype, const uint8_t* reset,
+                         void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                         const sdm_rt_saved* saved, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace sdm_rt_backward needs (0 on invalid dims or a shape the backward does not cover). */
+size_t sdm_rt_backward_workspace_bytes(const sdm_rt_dims* dims);
+
+/* The backward of sdm_rt_forward_train: the same inputs (kz, qz, v, gate_logits, reset, params), its *saved, and dy,
+ * the gradient of r_out ([B*T rows] of H * dh, dtype dy_dtype).  Writes *grads.  The sums over tokens run in a fixed
+ * order, so the result is deterministic. */
+int sdm_rt_backward(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                    const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
+                    const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
+                    sdm_rt_dtype in_dtype, const uint8_t* reset, const sdm_rt_saved* saved,
+                    const void* dy, int64_t dy_row_stride, sdm_rt_dtype dy_dtype,
+                    const sdm_rt_grads* grads, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Description of the last failure on the calling thread ("" if none). */
 const char* sdm_rt_last_error(void);
 

@@ -45,6 +45,39 @@ class SdmRtParams(ctypes.Structure):
     ]
 
 
+class SdmRtSaved(ctypes.Structure):
+    _fields_ = [
+        ("slots_w", c_void_p),
+        ("weights_w", c_void_p),
+        ("scores_w", c_void_p),
+        ("slots_r", c_void_p),
+        ("weights_r", c_void_p),
+        ("scores_r", c_void_p),
+        ("read", c_void_p),
+        ("den", c_void_p),
+    ]
+
+
+class SdmRtGrads(ctypes.Structure):
+    _fields_ = [
+        ("d_kz", c_void_p),
+        ("d_kz_row_stride", c_i64),
+        ("d_qz", c_void_p),
+        ("d_qz_row_stride", c_i64),
+        ("d_v", c_void_p),
+        ("d_v_row_stride", c_i64),
+        ("d_gate_logits", c_void_p),
+        ("d_gate_row_stride", c_i64),
+        ("d_keys1", c_void_p),
+        ("d_keys2", c_void_p),
+        ("d_addr_b", c_void_p),
+        ("d_log_scale", c_void_p),
+        ("d_onorm_w", c_void_p),
+        ("d_gate_bias", c_void_p),
+        ("d_log_decay", c_void_p),
+    ]
+
+
 SIGNATURES = {
     "sdm_rt_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
     "sdm_rt_pick_pitch": (ctypes.c_int32, [ctypes.POINTER(SdmRtDims)]),
@@ -68,6 +101,17 @@ SIGNATURES = {
                                          c_void_p, c_i64, ctypes.c_int, c_void_p]),
     "sdm_rt_rms_norm": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p,
                                        ctypes.c_float, c_void_p, c_i64, ctypes.c_int, c_void_p]),
+    "sdm_rt_forward_train": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                            c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                                            ctypes.c_int, c_void_p,
+                                            c_void_p, c_i64, ctypes.c_int,
+                                            ctypes.POINTER(SdmRtSaved), c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_backward_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
+    "sdm_rt_backward": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                       c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                                       ctypes.c_int, c_void_p, ctypes.POINTER(SdmRtSaved),
+                                       c_void_p, c_i64, ctypes.c_int,
+                                       ctypes.POINTER(SdmRtGrads), c_void_p, ctypes.c_size_t, c_void_p]),
     "sdm_rt_last_error": (ctypes.c_char_p, []),
 }
 

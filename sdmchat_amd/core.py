@@ -338,3 +338,165 @@ def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
                              ctypes.c_void_p(stream))
     _lib.check(rc, lib)
     return out
+
+
+# -- training: forward with saved tensors, backward, and the autograd Function -------------------------------------
+def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
+    B, T = v.shape[0], v.shape[1]
+    H, n_sub, half = keys1.shape
+    dh = v.shape[2] // H
+    return make_dims(B, T, H, dh, 2 * half, n_sub, k, read_mode, out_norm, gated, read_eps, out_norm_eps)
+
+
+def core_forward_train(kz, qz, v, gate_logits, *, params, k, read_mode="mean", out_norm=True, read_eps=1e-3,
+                       out_norm_eps=1e-2, out_dtype=torch.float32, reset=None, workspace=None):
+    """core_forward (empty start, no state out) that also keeps what core_backward needs.
+
+    params: a prepared (SdmRtParams, held) pair (_params).  Returns (r [B, T, H * dh] out_dtype, saved dict of
+    device tensors: slots_w/weights_w/scores_w, slots_r/weights_r/scores_r [B, H, T, pitch], read [B, T, H * dh] and
+    den [B, T, H] float32)."""
+    lib = _lib.load()
+    keys1 = params[1][0]
+    B, T = v.shape[0], v.shape[1]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dh = v.shape[2] // H
+    dims = _dims_of(kz, v, keys1, k, read_mode, out_norm, gate_logits is not None, read_eps, out_norm_eps)
+    dt = v.dtype
+    for name, x in (("kz", kz), ("qz", qz), ("gate_logits", gate_logits)):
+        if x is not None and x.dtype != dt:
+            raise ValueError(f"{name} has dtype {x.dtype}, expected {dt}")
+    vs = _rows(v, "v", B, T, H * dh)
+    ks = _rows(kz, "kz", B, T, H * d_a)
+    qs = _rows(qz, "qz", B, T, H * d_a)
+    gs = 0 if gate_logits is None else _rows(gate_logits, "gate_logits", B, T, H)
+    dev = v.device
+    pitch = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
+    if pitch <= 0:
+        raise _lib.SdmRtError(lib.sdm_rt_last_error().decode() or "invalid dimensions")
+    saved = dict(
+        slots_w=torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev),
+        weights_w=torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev),
+        scores_w=torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev),
+        slots_r=torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev),
+        weights_r=torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev),
+        scores_r=torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev),
+        read=torch.empty(B, T, H * dh, dtype=torch.float32, device=dev),
+        den=torch.empty(B, T, H, dtype=torch.float32, device=dev),
+    )
+    sv = _lib.SdmRtSaved(*[_ptr(saved[n]) for n in ("slots_w", "weights_w", "scores_w", "slots_r", "weights_r",
+                                                    "scores_r", "read", "den")])
+    out = torch.empty(B, T, H * dh, dtype=out_dtype, device=dev)
+    rs = None
+    if reset is not None:
+        if tuple(reset.shape) != (B, T):
+            raise ValueError(f"reset must be [B={B}, T={T}]")
+        rs = reset.to(device=dev, dtype=torch.uint8).contiguous()
+    saved["reset"] = rs
+    nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))
+    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_forward_train(ctypes.byref(dims), ctypes.byref(params[0]), _ptr(kz), ks, _ptr(qz), qs, _ptr(v),
+                                  vs, _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(out), H * dh, _DT[out_dtype],
+                                  ctypes.byref(sv), _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return out, saved
+
+
+def core_backward(kz, qz, v, gate_logits, saved, dy, *, params, k, read_mode="mean", out_norm=True, read_eps=1e-3,
+                  out_norm_eps=1e-2, workspace=None):
+    """Gradients of the core for dy = d loss / d r (r from core_forward_train with the same inputs and params).
+
+    Returns a dict of float32 device tensors: kz, qz [B, T, H * d_a], v [B, T, H * dh], gate_logits [B, T, H] (None
+    without the gate), keys1, keys2, addr_b, log_scale, onorm_w (None without the out-norm), gate_bias, log_decay
+    (lam * d loss / d lam)."""
+    lib = _lib.load()
+    keys1 = params[1][0]
+    B, T = v.shape[0], v.shape[1]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dh = v.shape[2] // H
+    gated = gate_logits is not None
+    dims = _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps)
+    vs = _rows(v, "v", B, T, H * dh)
+    ks = _rows(kz, "kz", B, T, H * d_a)
+    qs = _rows(qz, "qz", B, T, H * d_a)
+    gs = 0 if gate_logits is None else _rows(gate_logits, "gate_logits", B, T, H)
+    if dy.dtype not in _DT:
+        dy = dy.float()
+    if dy.dim() != 3 or dy.stride(2) != 1:
+        dy = dy.contiguous()
+    dys = _rows(dy, "dy", B, T, H * dh)
+    dev = v.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    g = dict(kz=torch.empty(B, T, H * d_a, **f32), qz=torch.empty(B, T, H * d_a, **f32),
+             v=torch.empty(B, T, H * dh, **f32), gate_logits=torch.empty(B, T, H, **f32) if gated else None,
+             keys1=torch.empty(H, n_sub, half, **f32), keys2=torch.empty(H, n_sub, half, **f32),
+             addr_b=torch.empty(H, d_a, **f32), log_scale=torch.empty(H, **f32),
+             onorm_w=torch.empty(H, dh, **f32) if out_norm else None, gate_bias=torch.empty(H, **f32),
+             log_decay=torch.empty(H, **f32))
+    gr = _lib.SdmRtGrads(_ptr(g["kz"]), H * d_a, _ptr(g["qz"]), H * d_a, _ptr(g["v"]), H * dh,
+                         _ptr(g["gate_logits"]), H, _ptr(g["keys1"]), _ptr(g["keys2"]), _ptr(g["addr_b"]),
+                         _ptr(g["log_scale"]), _ptr(g["onorm_w"]), _ptr(g["gate_bias"]), _ptr(g["log_decay"]))
+    sv = _lib.SdmRtSaved(*[_ptr(saved[n]) for n in ("slots_w", "weights_w", "scores_w", "slots_r", "weights_r",
+                                                    "scores_r", "read", "den")])
+    nbytes = lib.sdm_rt_backward_workspace_bytes(ctypes.byref(dims))
+    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_backward(ctypes.byref(dims), ctypes.byref(params[0]), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
+                             _ptr(gate_logits), gs, _DT[v.dtype], _ptr(saved["reset"]), ctypes.byref(sv), _ptr(dy),
+                             dys, _DT[dy.dtype], ctypes.byref(gr), _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return g
+
+
+class SdmCoreFunction(torch.autograd.Function):
+    """The SDM core as an autograd function: forward sdm_rt_forward_train, backward sdm_rt_backward.
+
+    apply(kz, qz, v, gate_logits, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias, cfg) -> r float32
+    [B, T, H * dh].  kz, qz, v, gate_logits share one dtype (float32 or bfloat16); gate_logits, addr_b, onorm_w and
+    gate_bias may be None.  cfg: dict with k, read_mode, out_norm, read_eps, out_norm_eps, reset ([B, T] bool or
+    None) and optionally workspace (a CoreWorkspace).  The picks carry no gradient (as topk in the reference)."""
+
+    @staticmethod
+    def forward(ctx, kz, qz, v, gate_logits, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias, cfg):
+        if v.device.type != "cuda":
+            raise RuntimeError("the SDM core needs ROCm device tensors")
+        params = _params(v.device, keys1, keys2, addr_b, log_scale, decay, onorm_w if cfg["out_norm"] else None,
+                         gate_bias)
+        opts = dict(k=cfg["k"], read_mode=cfg["read_mode"], out_norm=cfg["out_norm"], read_eps=cfg["read_eps"],
+                    out_norm_eps=cfg["out_norm_eps"])
+        r, saved = core_forward_train(kz, qz, v, gate_logits, params=params, reset=cfg.get("reset"),
+                                      workspace=cfg.get("workspace"), **opts)
+        ctx.opts = opts
+        ctx.params = params
+        ctx.saved = saved
+        ctx.workspace = cfg.get("workspace")
+        ctx.has = (gate_logits is not None, addr_b is not None, onorm_w is not None, gate_bias is not None)
+        ctx.dtypes = (kz.dtype, keys1.dtype, log_scale.dtype, decay.dtype)
+        ctx.save_for_backward(kz, qz, v, gate_logits, decay)
+        return r
+
+    @staticmethod
+    def backward(ctx, dr):
+        kz, qz, v, gate_logits, decay = ctx.saved_tensors
+        g = core_backward(kz, qz, v, gate_logits, ctx.saved, dr, params=ctx.params, workspace=ctx.workspace,
+                          **ctx.opts)
+        has_g, has_ab, has_on, has_gb = ctx.has
+        dt = ctx.dtypes[0]
+        need = ctx.needs_input_grad
+
+        def cast(t, like_dtype, i):
+            return t.to(like_dtype) if (t is not None and need[i]) else None
+        d_decay = None
+        if need[8]:
+            lam = decay.detach().to(torch.float32)
+            d_decay = torch.where(lam > 0, g["log_decay"] / torch.where(lam > 0, lam, torch.ones_like(lam)),
+                                  torch.zeros_like(lam)).to(decay.dtype)
+        return (cast(g["kz"], dt, 0), cast(g["qz"], dt, 1), cast(g["v"], dt, 2),
+                cast(g["gate_logits"], dt, 3) if has_g else None,
+                cast(g["keys1"], ctx.dtypes[1], 4), cast(g["keys2"], ctx.dtypes[1], 5),
+                cast(g["addr_b"], ctx.dtypes[1], 6) if has_ab else None,
+                cast(g["log_scale"], ctx.dtypes[2], 7), d_decay,
+                cast(g["onorm_w"], ctx.dtypes[1], 9) if has_on else None,
+                cast(g["gate_bias"], ctx.dtypes[1], 10) if has_gb else None, None)

@@ -772,11 +772,12 @@ struct AddrArgs {
   int32_t* slot_out;          // [B][H][T][pitch]
   float* w_out;
   float* s_out;
-  // a second address set (gridDim.z = 2, blockIdx.z = 1): its rows, picks and weights; no gate, no scores
+  // a second address set (gridDim.z = 2, blockIdx.z = 1): its rows, picks, weights and scores (or nullptr); no gate
   const void* z2;
   int64_t z2_stride;
   int32_t* slot_out2;
   float* w_out2;
+  float* s_out2;
 };
 
 // Head h's sub-keys of both halves, unit-normalised ([2][n_sub][HALF] floats), into LDS: one row per thread.
@@ -808,7 +809,7 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
     a.gl = nullptr;
     a.slot_out = a.slot_out2;
     a.w_out = a.w_out2;
-    a.s_out = nullptr;
+    a.s_out = a.s_out2;
   }
   const float gate =
       (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
@@ -1138,6 +1139,7 @@ struct ScanArgs {
   float* state_out_cnt;
   void* r_out;                 // rows of H * dh; OutT
   int64_t r_stride;
+  float* den_out;              // [B*T][H] read denominators (mean read), or nullptr
   int B, T, H, dh, M, n_chunks, read_mean;
   float read_eps;
 };
@@ -1456,6 +1458,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       const float cn = sum8(cpart);
       if (a.read_mean) {
         const float den = fmaf(fin, cn, csum);
+        if (a.den_out && cg == 0 && l8 == 0) a.den_out[(static_cast<int64_t>(b) * a.T + c0 + p) * a.H + h] = den;
         const float inv = fast_rcp(den + a.read_eps);
 #pragma unroll
         for (int k = 0; k < CPL; ++k) acc[k] *= inv;
@@ -1554,7 +1557,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// finish: 8 lanes per (token, head) row of dh float32 read-outs, 8 columns per lane and step
+// finish: 8 lanes per (token, head) row of dh float32 read-outs, 8 columns per lane and step (onorm_w nullptr: no
+// norm, a copy in OutT)
 template <typename OutT>
 __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r, int64_t r_stride,
                                                      OutT* __restrict__ out, int64_t out_stride,
@@ -1583,15 +1587,14 @@ __global__ void __launch_bounds__(256) finish_kernel(const float* __restrict__ r
   }
   ss = sum8(ss);
   if (!live) return;
-  const float inv = 1.f / sqrtf(ss / static_cast<float>(dh) + eps);
+  const float inv = onorm_w ? 1.f / sqrtf(ss / static_cast<float>(dh) + eps) : 1.f;
   OutT* dst = out + n * out_stride + static_cast<int64_t>(h) * dh;
-  const float* wr = onorm_w + h * dh;
 #pragma unroll
   for (int k = 0; k < kMaxSteps; ++k) {
     const int c = 8 * l8 + 64 * k;
     if (c < dh) {
-      float wv[8], o[8];
-      load_vals<8, float>(wr + c, wv);
+      float wv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f}, o[8];
+      if (onorm_w) load_vals<8, float>(onorm_w + h * dh + c, wv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = v[k][e] * inv * wv[e];
       store_vals<8, OutT>(dst + c, o);
@@ -2391,3 +2394,6 @@ int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params, con
 }
 
 }  // extern "C"
+
+// the backward (forward with saved tensors, sdm_rt_backward)
+#include "sdm_rt_grad.inc"

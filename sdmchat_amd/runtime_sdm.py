@@ -12,15 +12,27 @@ faded write / causal read of the memory and the mean read with its per-head norm
 ``libsdm_rt.so`` (sdm_rt_forward).  There is no CPU or pure-torch fallback: a missing library, a CPU tensor or an
 unsupported option raises.
 
-Forward only.  Gradients are not implemented: calling with autograd recording raises.  ``reset`` (segment resets at
-BOS) is not implemented yet and raises.
+Training: with autograd recording (grad enabled and x or a parameter requiring grad) forward takes the reference's
+own torch path for the input norm (with grad_scale), the projections and wo, and runs the core through
+``core.SdmCoreFunction``, whose backward is ``sdm_rt_backward``: the gradients reach every parameter (the sub-keys,
+addr_b, log_scale, decay_logit with learn_decay, onorm_w, the projections and the gate bias) as under the
+reference's autograd of its chunked form (:259-268).
 """
 import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import core
+
+
+def grad_scale(x, alpha):
+    """Identity forward; the gradient into x is scaled by alpha (track4_sdmllm_models.py:170-174)."""
+    if alpha == 1.0:
+        return x
+    xd = x.detach()
+    return xd if alpha == 0.0 else xd + alpha * (x - xd)
 
 
 class RMSNorm(nn.Module):
@@ -113,9 +125,6 @@ class RunTimeSdm(nn.Module):
     def _check(self, x, reset):
         if reset is not None and (reset.dim() != 2 or tuple(reset.shape) != tuple(x.shape[:2])):
             raise ValueError(f"reset must be [B, T] = {tuple(x.shape[:2])}, got {tuple(reset.shape)}")
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            raise RuntimeError("RunTimeSdm HIP core is forward-only: call it under torch.no_grad() or "
-                               "torch.inference_mode()")
         if x.device.type != "cuda":
             raise RuntimeError("RunTimeSdm HIP core needs a ROCm device tensor")
         if x.dim() != 3 or x.shape[-1] != self.d:
@@ -142,14 +151,46 @@ class RunTimeSdm(nn.Module):
         g = proj[..., o_g:o_g + H] if self.write_gate else None
         return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
 
+    def _training(self, x):
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _forward_train(self, x, reset):
+        """The differentiable forward: the reference's prepare (:195-213) in torch ops up to the projections, the
+        core through SdmCoreFunction, finish's wo (:247).  Under autocast the projections and wo run in its dtype,
+        as in the reference."""
+        B, T, _ = x.shape
+        H, d_a, d = self.h, self.d_a, self.d
+        hx = self.norm(grad_scale(x, self.mem_in_grad)).float()
+        ws = [self.wk.weight, self.wq.weight, self.wv.weight]
+        bias = None
+        if self.write_gate:   # the gate bias inside the projection, so the logit rounds as wg(hx) does
+            ws.append(self.wg.weight)
+            bias = torch.cat([self.wg.bias.new_zeros(2 * H * d_a + d), self.wg.bias])
+        proj = F.linear(hx, torch.cat(ws, 0), bias)
+        o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
+        kz, qz, V = proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g]
+        g = proj[..., o_g:o_g + H] if self.write_gate else None
+        cfg = dict(k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
+                   out_norm_eps=self.out_norm_eps, reset=reset, workspace=self._ws)
+        r = core.SdmCoreFunction.apply(kz, qz, V, g, self.keys1, self.keys2, self.addr_b, self.log_scale,
+                                       self.decay(), self.onorm_w if self.out_norm else None, None, cfg)
+        y = self.wo(r).to(x.dtype)
+        self._gate_src = (g.detach() if g is not None else None, None, (B, T, H), x.device)
+        self._last_gate = None
+        self.last_state = None
+        return y
+
     def forward(self, x, reset=None):
         """x [B, T, d] -> y [B, T, d] in x.dtype; every call starts from an empty memory
         (track4_onesdm_models.py:249-274).  reset [B, T] bool: where True the memory is emptied before that position
-        reads (a BOS starts a new document, :229-233).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)."""
+        reads (a BOS starts a new document, :229-233).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)
+        (inference only).  With autograd recording the forward is differentiable (SdmCoreFunction)."""
         B, T, _ = x.shape
         if not self.enabled:
             return torch.zeros_like(x)
         self._check(x, reset)
+        if self._training(x):
+            return self._forward_train(x, reset)
         dt = self._compute_dtype(x)
         H = self.h
         with torch.autocast("cuda", enabled=False):
@@ -174,8 +215,8 @@ class RunTimeSdm(nn.Module):
         computed from the kept gate logits when first read."""
         if self._last_gate is None and self._gate_src is not None:
             g, bias, shape, dev = self._gate_src
-            self._last_gate = (torch.sigmoid(g.float() + bias.float()) if g is not None
-                               else torch.ones(shape, device=dev))
+            self._last_gate = (torch.sigmoid(g.float() + (bias.float() if bias is not None else 0.0))
+                               if g is not None else torch.ones(shape, device=dev))
             self._gate_src = None
         return self._last_gate
 
@@ -199,6 +240,9 @@ class RunTimeSdm(nn.Module):
         if not self.enabled:
             return torch.zeros_like(x)
         self._check(x2.unsqueeze(1), None)
+        if self._training(x2):
+            raise RuntimeError("RunTimeSdm.step is inference only: call it under torch.no_grad() or "
+                               "torch.inference_mode()")
         dt = self._compute_dtype(x2)
         with torch.autocast("cuda", enabled=False):
             kz, qz, V, g = self._project(x2.unsqueeze(1), dt)

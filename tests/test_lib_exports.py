@@ -117,3 +117,34 @@ def test_decode_step_validation():
     assert call(dims, state=None) == -1 and b"state" in lib.sdm_rt_last_error()
     assert call(dims, ws_bytes=need - 1) == -2 and b"workspace" in lib.sdm_rt_last_error()
     assert call(_dims(B=0, T=1)) == 0
+
+
+def test_backward_validation():
+    """sdm_rt_forward_train / sdm_rt_backward check their arguments on the host before any launch."""
+    lib = _lib.load()
+    dims = _dims(B=2, T=100)
+    need = lib.sdm_rt_backward_workspace_bytes(ctypes.byref(dims))
+    # dnum (N x H*dh float32) and the per-pick partial dots of both scans are the bulk of it
+    N = 2 * 100
+    assert need >= 4 * N * 12 * 64 + 2 * 4 * 2 * N * 12 * 8
+    assert lib.sdm_rt_backward_workspace_bytes(ctypes.byref(_dims(addr_dim=130))) == 0   # d_a > 64
+    prm = _lib.SdmRtParams(*([ctypes.c_void_p(256)] * 7))
+    fake = ctypes.c_void_p(256)
+    saved = _lib.SdmRtSaved(*([fake] * 8))
+    grads = _lib.SdmRtGrads(fake, 768, fake, 768, fake, 768, fake, 12, *([None] * 7))
+    F = _lib.SDM_RT_F32
+
+    def bwd(d=dims, sv=saved, gr=grads, ws=need, dy_stride=768):
+        return lib.sdm_rt_backward(ctypes.byref(d), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12, F,
+                                   None, ctypes.byref(sv) if sv is not None else None, fake, dy_stride, F,
+                                   ctypes.byref(gr) if gr is not None else None, fake, ws, None)
+    assert bwd(sv=None) == -1 and b"saved" in lib.sdm_rt_last_error()
+    assert bwd(gr=None) == -1 and b"grads" in lib.sdm_rt_last_error()
+    assert bwd(ws=need - 1) == -2 and b"workspace" in lib.sdm_rt_last_error()
+    assert bwd(dy_stride=700) == -1 and b"stride" in lib.sdm_rt_last_error()
+    no_gl = _lib.SdmRtGrads(fake, 768, fake, 768, fake, 768, None, 0, *([None] * 7))
+    assert bwd(gr=no_gl) == -1 and b"d_gate_logits" in lib.sdm_rt_last_error()
+    assert bwd(d=_dims(B=0, T=100)) == 0
+    rc = lib.sdm_rt_forward_train(ctypes.byref(dims), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12,
+                                  F, None, fake, 768, F, None, fake, 1 << 30, None)
+    assert rc == -1 and b"saved" in lib.sdm_rt_last_error()
