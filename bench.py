@@ -32,6 +32,10 @@ model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12
 synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm.
 --no-model skips it.
 
+train: the backward -- the core's training forward (sdm_rt_forward_train: the forward plus the saved picks, weights,
+scores, read and denominators) and backward (sdm_rt_backward) on the layer's bf16 projections, median of 20 calls,
+and one RunTimeSdm layer training step (forward + backward under bf16 autocast), median of 10.  --no-train skips it.
+
 --copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
 """
 import argparse
@@ -178,6 +182,49 @@ def model_bench(dev, vocab=32768, layers=12, mlp_f=2048):
     return out
 
 
+def train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms):
+    """The backward: the core's training forward (sdm_rt_forward_train) and backward (sdm_rt_backward) on the
+    layer's bf16 projections, and one whole layer training step (forward + backward of RunTimeSdm under bf16
+    autocast, the reference's training setting)."""
+    import torch
+
+    from sdmchat_amd import core
+
+    opts = dict(k=K, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2)
+    ws_f, ws_b = core.CoreWorkspace(), core.CoreWorkspace()
+    state = {}
+
+    def fwd():
+        state["r"], state["saved"] = core.core_forward_train(kz, qz, V, g, params=prm, workspace=ws_f, **opts)
+
+    fwd()
+    dy = torch.randn(B, T, D, generator=torch.Generator().manual_seed(9)).to(dev)
+
+    def bwd():
+        core.core_backward(kz, qz, V, g, state["saved"], dy, params=prm, workspace=ws_b, **opts)
+
+    f_ms = median_call_ms(fwd, n=20, warm=3)
+    b_ms = median_call_ms(bwd, n=20, warm=3)
+    log(f"train: core forward_train {f_ms * 1e3:.1f} us, core backward {b_ms * 1e3:.1f} us")
+    m.train()
+    xg = x.detach().clone().requires_grad_(True)
+    wgt = torch.randn(B, T, D, generator=torch.Generator().manual_seed(10)).to(dev).to(torch.bfloat16)
+
+    def step():
+        with torch.enable_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            y = m(xg)
+            (y.float() * wgt.float()).sum().backward()
+
+    s_ms = median_call_ms(step, n=10, warm=2)
+    m.eval()
+    m.zero_grad(set_to_none=True)
+    log(f"train: layer step (forward + backward) {s_ms:.3f} ms")
+    return {"core_forward_train_ms": round(f_ms, 4), "core_backward_ms": round(b_ms, 4),
+            "layer_step_ms": round(s_ms, 4), "layer_step_tokens_per_s": round(B * T / (s_ms * 1e-3), 1),
+            "workload": f"RunTimeSdm layer training step at B={B} T={T} d={D}, 12 heads, M=1,024, k=8, bf16 autocast; "
+                        "core = sdm_rt_forward_train / sdm_rt_backward on the bf16 projections"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +236,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model measurement")
     ap.add_argument("--model-only", action="store_true", help="only the whole-model measurement (for profiler runs)")
+    ap.add_argument("--no-train", action="store_true", help="skip the backward measurement")
+    ap.add_argument("--train-only", action="store_true", help="only the backward measurement (for profiler runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
@@ -250,6 +299,9 @@ def main():
             torch.cuda.synchronize()
             return time.perf_counter() - t0
 
+        if a.train_only:
+            print(json.dumps({"train": train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms)}), flush=True)
+            return
         core_ms = median_call_ms(core_call)
         log(f"core: {core_ms * 1e3:.1f} us per call (median of 50)")
         if a.core_only:
@@ -262,6 +314,7 @@ def main():
         copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
         del big, big2
         decode = None if a.no_decode else decode_bench(m, dev)
+        train = None if a.no_train else train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms)
         model = None if a.no_model else model_bench(dev)
 
     ms_per_step = wall * 1e3 / a.steps
@@ -298,6 +351,8 @@ def main():
         rec["decode"] = decode
     if model is not None:
         rec["model"] = model
+    if train is not None:
+        rec["train"] = train
     if not a.no_cpu:
         log("cpu baseline ...")
         rec["cpu_baseline"] = cpu_baseline()
