@@ -1,5 +1,5 @@
 """OneSdmLM: the whole language model around the run-time SDM mixer (experiments/track4/sdmllm/
-track4_onesdm_models.py:471-555), for its forward.
+track4_onesdm_models.py:471-555).
 
 A drop-in for the reference model: the same constructor, module names and parameter creation order, and the same
 initialisation rule, so a reference state dict loads with ``strict=True``.  Per layer, ``x + mems[i](x, reset)`` runs
@@ -7,6 +7,10 @@ the HIP mixer (RunTimeSdm) and the per-token step is either ``x + SwiGLU(RMSNorm
 ``x + TrainedSdm(x)`` (the product-key table layer); then the final RMSNorm and the tied head ``h @ E^T``.  The RMSNorms
 run on the RMSNorm kernel; the dense maps are hipBLASLt GEMMs through torch.  The reference's archive memory is a
 separate subsystem and is not built here (archive=True raises).
+
+Training: with autograd recording the mixers run their differentiable path (RunTimeSdm's SdmCoreFunction, backward
+on the HIP kernels) and the norms the reference's torch ops, so ffn="mlp" (and "none") models train; the TrainedSdm
+table layer (ffn="sdm") is forward-only and raises under autograd.
 """
 import math
 
@@ -20,8 +24,11 @@ from .trained_sdm import TrainedSdm
 
 
 def _norm(x, norm):
-    """RMSNorm on the kernel with the reference's dtype rule: cast_in(x * rsqrt(mean x^2 + eps)) * w, the result in
-    the promoted dtype of x and w (track4_sdmllm_models.py:69-71)."""
+    """RMSNorm with the reference's dtype rule: cast_in(x * rsqrt(mean x^2 + eps)) * w, the result in the promoted
+    dtype of x and w (track4_sdmllm_models.py:69-71).  On the kernel for inference; with autograd recording, the
+    reference's own differentiable ops (the kernel has no backward)."""
+    if torch.is_grad_enabled() and (x.requires_grad or norm.w.requires_grad):
+        return norm(x)
     return core.rms_norm(x, norm.w, norm.eps, out_dtype=torch.promote_types(x.dtype, norm.w.dtype))
 
 

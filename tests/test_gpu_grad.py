@@ -247,3 +247,82 @@ def test_grad_empty_batch_returns_nothing_to_do():
                                    dev["keys2"], None, dev["log_scale"], dev["decay"], dev["onorm_w"], None,
                                    dict(k=4, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2))
     assert r.shape == (0, 10, 16)
+
+
+# -- a whole OneSdmLM training step ---------------------------------------------------------------------------------
+def _rms64(x, w):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * w
+
+
+def _mixer64(P, pre, m, x, reset, siw, sir):
+    """float64 RunTimeSdm.forward (prepare :195-213 with the oracle core, wo :247) from the parameter dict P."""
+    B, T, d = x.shape
+    H, d_a, dh = m.h, m.d_a, m.dh
+    hx = _rms64(x, P[pre + "norm.w"])
+    kz = (hx @ P[pre + "wk.weight"].T).view(B, T, H, d_a)
+    qz = (hx @ P[pre + "wq.weight"].T).view(B, T, H, d_a)
+    V = (hx @ P[pre + "wv.weight"].T).view(B, T, H, dh)
+    gl = hx @ P[pre + "wg.weight"].T + P[pre + "wg.bias"]
+    lam = torch.sigmoid(P[pre + "decay_logit"])
+    cfg = dict(k=m.k, read_mode=m.read_mode, out_norm=m.out_norm, read_eps=m.read_eps, out_norm_eps=m.out_norm_eps)
+    r = G.core_from_picks(kz, qz, V, gl, P[pre + "keys1"], P[pre + "keys2"], P[pre + "addr_b"], P[pre + "log_scale"],
+                          lam, P[pre + "onorm_w"], None, siw, sir, cfg, reset=reset)
+    return r.reshape(B, T, d) @ P[pre + "wo.weight"].T
+
+
+def test_onesdm_training_step_matches_the_oracle():
+    """Two layers of [x + RunTimeSdm(x); x + SwiGLU(RMSNorm x)], final norm, tied head, BOS resets and learned fades:
+    every parameter's gradient of a weighted sum of the logits against a float64 autograd model that runs the same
+    picks (each mixer's picks from its own input in the GPU forward)."""
+    from sdmchat_amd import OneSdmLM
+    torch.manual_seed(0)
+    Vv, d, L, H, n_sub, d_a, k = 50, 96, 2, 4, 8, 16, 8
+    model = OneSdmLM(Vv, d=d, layers=L, mlp_f=128, heads=H, n_sub=n_sub, d_a=d_a, k=k, decays=(0.6, 0.8, 0.95, 0.99),
+                     learn_decay=True, addr_bias=0.2, reset_at_bos=True, bos_id=0).cuda()
+    with torch.no_grad():   # the zero-start output maps and gate weights would leave the mixers silent
+        for m in model.mems:
+            torch.nn.init.xavier_uniform_(m.wo.weight)
+            torch.nn.init.xavier_uniform_(m.wg.weight)
+            m.wq.weight.copy_(0.7 * m.wk.weight + 0.3 * m.wq.weight)
+    idx = torch.randint(1, Vv, (2, 120), generator=torch.Generator().manual_seed(1))
+    idx[0, 40] = idx[1, 77] = 0   # BOS: the memory is emptied there
+    idx = idx.cuda()
+    inputs = {}
+    hooks = [m.register_forward_pre_hook(lambda mod, args, i=i: inputs.__setitem__(i, args[0].detach()))
+             for i, m in enumerate(model.mems)]
+    say(f"[grad] OneSdmLM: layers={L} d={d} V={Vv} B=2 T=120, resets at BOS, learned fades")
+    logits = model(idx)
+    for hk in hooks:
+        hk.remove()
+    wgt = torch.randn(logits.shape, generator=torch.Generator().manual_seed(2)).cuda()
+    (logits * wgt).sum().backward()
+    torch.cuda.synchronize()
+    picks = []
+    with torch.no_grad():
+        for i, m in enumerate(model.mems):
+            hx = m.norm(inputs[i]).float()
+            W = torch.cat([m.wk.weight, m.wq.weight, m.wv.weight, m.wg.weight], 0)
+            bias = torch.cat([m.wg.bias.new_zeros(2 * H * d_a + d), m.wg.bias])
+            proj = torch.nn.functional.linear(hx, W, bias)
+            sw = core.address(proj[..., :H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
+            sr = core.address(proj[..., H * d_a:2 * H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
+            picks.append((sw.permute(0, 2, 1, 3).long().cpu(), sr.permute(0, 2, 1, 3).long().cpu()))
+    P = {n: p.detach().double().cpu().clone().requires_grad_(True) for n, p in model.named_parameters()}
+    reset = (idx == 0).cpu()
+    x = P["emb.weight"][idx.cpu()]
+    for i, m in enumerate(model.mems):
+        x = x + _mixer64(P, f"mems.{i}.", m, x, reset, *picks[i])
+        hm = _rms64(x, P[f"mnorms.{i}.w"])
+        x = x + (torch.nn.functional.silu(hm @ P[f"mlps.{i}.gate.weight"].T) * (hm @ P[f"mlps.{i}.up.weight"].T)) \
+            @ P[f"mlps.{i}.down.weight"].T
+    ref = _rms64(x, P["nf.w"]) @ P["emb.weight"].T
+    err = (logits.detach().double().cpu() - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item(), f"logits differ by {err}"
+    (ref * wgt.double().cpu()).sum().backward()
+    for n, p in model.named_parameters():
+        g, gr = p.grad, P[n].grad
+        assert g is not None and gr is not None, n
+        scale = gr.abs().max().item()
+        e = (g.double().cpu() - gr).abs().max().item()
+        say(f"  d{n}: max err {e:.3e} of scale {scale:.3e}")
+        assert e <= 1e-4 * max(scale, 1e-2), f"d{n}: {e:.3e} vs {scale:.3e}"
