@@ -34,7 +34,8 @@ synthetic seeded weights (the zero-start output maps and tables filled), median 
 
 train: the backward -- the core's training forward (sdm_rt_forward_train: the forward plus the saved picks, weights,
 scores, read and denominators) and backward (sdm_rt_backward) on the layer's bf16 projections, median of 20 calls,
-and one RunTimeSdm layer training step (forward + backward under bf16 autocast), median of 10.  --no-train skips it.
+and one RunTimeSdm layer training step (forward + backward under bf16 autocast), median of 10; and the TrainedSdm table
+layer of the FULL model (addressing + table read, and sdm_rt_table_backward), median of 20.  --no-train skips it.
 
 --copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
 """
@@ -219,10 +220,38 @@ def train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms):
     m.eval()
     m.zero_grad(set_to_none=True)
     log(f"train: layer step (forward + backward) {s_ms:.3f} ms")
+    # the TrainedSdm table layer of the FULL model: 1 head of width 768, 4,096 slots, k=16, d_a 32
+    gen = torch.Generator().manual_seed(12)
+    q = torch.randn(B, T, 32, generator=gen).to(dev).to(torch.bfloat16)
+    tk1, tk2 = (torch.randn(1, 64, 16, generator=gen).to(dev) for _ in range(2))
+    tls = torch.full((1,), 2.0794, device=dev)
+    tv = torch.randn(1, 4096, 768, generator=gen).to(dev) * 0.02
+    tprm = core._params(dev, tk1, tk2, None, tls, None, None, None)
+    tws = core.CoreWorkspace()
+    tstate = {}
+
+    def tfwd():
+        sl, sc, wt = core.address(q, tk1, tk2, 16, tls, padded=True, params=tprm)
+        tstate["p"] = (sl, sc, wt)
+        core.table_read(sl, wt, tv, 16, out_dtype=torch.float32)
+
+    tfwd()
+    tdy = torch.randn(B, T, 768, generator=gen).to(dev)
+
+    def tbwd():
+        sl, sc, wt = tstate["p"]
+        core.table_backward(q, sl, wt, sc, tv, tdy, k=16, params=tprm, workspace=tws)
+
+    tf_ms = median_call_ms(tfwd, n=20, warm=3)
+    tb_ms = median_call_ms(tbwd, n=20, warm=3)
+    log(f"train: table layer forward {tf_ms * 1e3:.1f} us, backward {tb_ms * 1e3:.1f} us")
     return {"core_forward_train_ms": round(f_ms, 4), "core_backward_ms": round(b_ms, 4),
             "layer_step_ms": round(s_ms, 4), "layer_step_tokens_per_s": round(B * T / (s_ms * 1e-3), 1),
+            "table_forward_ms": round(tf_ms, 4), "table_backward_ms": round(tb_ms, 4),
             "workload": f"RunTimeSdm layer training step at B={B} T={T} d={D}, 12 heads, M=1,024, k=8, bf16 autocast; "
-                        "core = sdm_rt_forward_train / sdm_rt_backward on the bf16 projections"}
+                        "core = sdm_rt_forward_train / sdm_rt_backward on the bf16 projections; table = the "
+                        "TrainedSdm layer between wq and wo (1 head of 768, 4,096 slots, k=16): sdm_rt_address + "
+                        "sdm_rt_table_read, and sdm_rt_table_backward"}
 
 
 def main():

@@ -223,6 +223,27 @@ int sdm_rt_backward(const sdm_rt_dims* dims, const sdm_rt_params* params,
                     const void* dy, int64_t dy_row_stride, sdm_rt_dtype dy_dtype,
                     const sdm_rt_grads* grads, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace sdm_rt_table_backward needs (0 on invalid dims or a shape it does not cover). */
+size_t sdm_rt_table_backward_workspace_bytes(const sdm_rt_dims* dims);
+
+/* The backward of TrainedSdm's table layer between the query map and wo (track4_onesdm_models.py:438-455: pk_address
+ * of the query, softmax(exp(log_scale) * score), the embedding_bag read of the value tables), for picks held fixed:
+ *   q            [B*T rows] of H * d_a queries the picks came from (dtype in_dtype; no address bias)
+ *   slots, weights, scores   [B][H][T][pitch] as sdm_rt_address wrote them for q
+ *   values       [H][M][dh] value tables (dtype values_dtype); dims->head_dim = dh
+ *   dy           [B*T rows] of H * dh: the gradient of the read (sdm_rt_table_read's out), dtype dy_dtype
+ * writes d_q (float32 rows), d_values ([H][M][dh] float32, overwritten; each row summed over its picks in pick order:
+ * the picks are sorted by slot with a stable radix sort), d_keys1 / d_keys2 (both or neither) and d_log_scale ([H] or
+ * NULL).  Every sum runs in a fixed order, so the result is deterministic. */
+int sdm_rt_table_backward(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                          const void* q, int64_t q_row_stride, sdm_rt_dtype in_dtype,
+                          const int32_t* slots, const float* weights, const float* scores,
+                          const void* values, sdm_rt_dtype values_dtype,
+                          const void* dy, int64_t dy_row_stride, sdm_rt_dtype dy_dtype,
+                          float* d_q, int64_t d_q_row_stride, float* d_values,
+                          float* d_keys1, float* d_keys2, float* d_log_scale,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Description of the last failure on the calling thread ("" if none). */
 const char* sdm_rt_last_error(void);
 

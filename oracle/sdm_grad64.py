@@ -90,3 +90,14 @@ def core_from_picks(kz, qz, V, gate_logits, keys1, keys2, addr_b, log_scale, dec
     return read_from_weights(siw, ww, sir, wr, V, decay, n_sub * n_sub, reset, cfg.get("read_mode", "mean"),
                              cfg.get("read_eps", 1e-3), cfg.get("out_norm", True), onorm_w,
                              cfg.get("out_norm_eps", 1e-2))
+
+
+def table_from_picks(q, keys1, keys2, log_scale, values, si):
+    """TrainedSdm's read for fixed picks (OM:438-455): scores at the picks, softmax(e^log_scale sv), the weighted sum
+    of the picked value rows.  q (B, T, H, d_a); si (B, T, H, kk); values (H, M, dh) -> r (B, T, H, dh)."""
+    sv = pick_scores(q, None, keys1, keys2, si)
+    w = torch.softmax(sv * torch.exp(log_scale)[None, None, :, None], -1)
+    H = values.shape[0]
+    si = torch.as_tensor(si).to(torch.int64)
+    rows = values[torch.arange(H)[None, None, :, None], si]                    # (B, T, H, kk, dh)
+    return (w[..., None] * rows).sum(-2)

@@ -112,6 +112,15 @@ SIGNATURES = {
                                        ctypes.c_int, c_void_p, ctypes.POINTER(SdmRtSaved),
                                        c_void_p, c_i64, ctypes.c_int,
                                        ctypes.POINTER(SdmRtGrads), c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_table_backward_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
+    "sdm_rt_table_backward": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                             c_void_p, c_i64, ctypes.c_int,
+                                             c_void_p, c_void_p, c_void_p,
+                                             c_void_p, ctypes.c_int,
+                                             c_void_p, c_i64, ctypes.c_int,
+                                             c_void_p, c_i64, c_void_p,
+                                             c_void_p, c_void_p, c_void_p,
+                                             c_void_p, ctypes.c_size_t, c_void_p]),
     "sdm_rt_last_error": (ctypes.c_char_p, []),
 }
 

@@ -500,3 +500,75 @@ class SdmCoreFunction(torch.autograd.Function):
                 cast(g["log_scale"], ctx.dtypes[2], 7), d_decay,
                 cast(g["onorm_w"], ctx.dtypes[1], 9) if has_on else None,
                 cast(g["gate_bias"], ctx.dtypes[1], 10) if has_gb else None, None)
+
+
+def table_backward(q, slots, weights, scores, values, dy, *, k, params, workspace=None):
+    """Gradients of TrainedSdm's table read for fixed picks (sdm_rt_table_backward).
+
+    q [B, T, H * d_a]; slots, weights, scores [B, H, T, pitch] from address(q, ..., padded=True); values [H, M, dh];
+    dy [B, T, H * dh] the gradient of the read.  params: the (SdmRtParams, held) pair of keys1, keys2 and log_scale.
+    Returns a dict of float32 device tensors q, values, keys1, keys2, log_scale."""
+    lib = _lib.load()
+    keys1 = params[1][0]
+    B, T = q.shape[0], q.shape[1]
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    Hv, M, dh = values.shape
+    dims = make_dims(B, T, H, dh, d_a, n_sub, k, out_norm=False, write_gate=False)
+    qs = _rows(q, "q", B, T, H * d_a)
+    if dy.dtype not in _DT:
+        dy = dy.float()
+    if dy.dim() != 3 or dy.stride(2) != 1:
+        dy = dy.contiguous()
+    dys = _rows(dy, "dy", B, T, H * dh)
+    vals = values.detach().contiguous()
+    dev = q.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    g = dict(q=torch.empty(B, T, H * d_a, **f32), values=torch.empty(H, M, dh, **f32),
+             keys1=torch.empty(H, n_sub, half, **f32), keys2=torch.empty(H, n_sub, half, **f32),
+             log_scale=torch.empty(H, **f32))
+    nbytes = lib.sdm_rt_table_backward_workspace_bytes(ctypes.byref(dims))
+    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_table_backward(ctypes.byref(dims), ctypes.byref(params[0]), _ptr(q), qs, _DT[q.dtype],
+                                   _ptr(slots), _ptr(weights), _ptr(scores), _ptr(vals), _DT[vals.dtype], _ptr(dy),
+                                   dys, _DT[dy.dtype], _ptr(g["q"]), H * d_a, _ptr(g["values"]), _ptr(g["keys1"]),
+                                   _ptr(g["keys2"]), _ptr(g["log_scale"]), _ptr(ws), ws.numel(),
+                                   ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return g
+
+
+class TableSdmFunction(torch.autograd.Function):
+    """TrainedSdm's layer between the query map and wo as an autograd function: forward sdm_rt_address +
+    sdm_rt_table_read, backward sdm_rt_table_backward.
+
+    apply(q, keys1, keys2, log_scale, values, cfg) -> r float32 [B, T, H * dh]; q [B, T, H * d_a] float32 or
+    bfloat16; cfg: dict with k and optionally workspace.  After the call cfg["slots"] holds the picks
+    [B, H, T, pitch].  The picks carry no gradient (as topk in the reference)."""
+
+    @staticmethod
+    def forward(ctx, q, keys1, keys2, log_scale, values, cfg):
+        if q.device.type != "cuda":
+            raise RuntimeError("the table layer needs ROCm device tensors")
+        params = _params(q.device, keys1, keys2, None, log_scale, None, None, None)
+        slots, scores, weights = address(q, keys1, keys2, cfg["k"], log_scale, padded=True, params=params)
+        r = table_read(slots, weights, values, cfg["k"], out_dtype=torch.float32)
+        cfg["slots"] = slots
+        ctx.k = cfg["k"]
+        ctx.params = params
+        ctx.workspace = cfg.get("workspace")
+        ctx.dtypes = (q.dtype, keys1.dtype, log_scale.dtype, values.dtype)
+        ctx.save_for_backward(q, values, slots, scores, weights)
+        return r
+
+    @staticmethod
+    def backward(ctx, dr):
+        q, values, slots, scores, weights = ctx.saved_tensors
+        g = table_backward(q, slots, weights, scores, values, dr, k=ctx.k, params=ctx.params,
+                           workspace=ctx.workspace)
+        need = ctx.needs_input_grad
+        dq, dk, dl, dv = ctx.dtypes
+        return (g["q"].to(dq) if need[0] else None, g["keys1"].to(dk) if need[1] else None,
+                g["keys2"].to(dk) if need[2] else None, g["log_scale"].to(dl) if need[3] else None,
+                g["values"].to(dv) if need[4] else None, None)

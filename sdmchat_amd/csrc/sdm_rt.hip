@@ -20,7 +20,9 @@
 // lam = 0 (keep only the previous write) and lam = 1 (never fade) are exact.
 
 #include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>

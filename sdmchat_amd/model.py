@@ -9,8 +9,8 @@ run on the RMSNorm kernel; the dense maps are hipBLASLt GEMMs through torch.  Th
 separate subsystem and is not built here (archive=True raises).
 
 Training: with autograd recording the mixers run their differentiable path (RunTimeSdm's SdmCoreFunction, backward
-on the HIP kernels) and the norms the reference's torch ops, so ffn="mlp" (and "none") models train; the TrainedSdm
-table layer (ffn="sdm") is forward-only and raises under autograd.
+on the HIP kernels), the TrainedSdm layers theirs (TableSdmFunction, sdm_rt_table_backward) and the norms the
+reference's torch ops, so every arm (ffn="mlp", "sdm", "none") trains.
 """
 import math
 

@@ -5,7 +5,11 @@ A drop-in for the reference module: the same constructor, parameter names, shape
 ``Generator(9876 + seed)`` draws keys1 then keys2; values start at zero), so a reference state dict loads with
 ``strict=True``.  The forward runs the RMSNorm kernel, the query map as one GEMM, the product-key addressing kernel
 (sdm_rt_address: top-k of the n_sub^2 slots and the softmax weights) and the weighted table read (sdm_rt_table_read,
-the reference's embedding_bag), then the output map.  Forward only; there is no CPU or torch fallback.
+the reference's embedding_bag), then the output map.  There is no CPU or torch fallback.
+
+Training: with autograd recording the norm, the query map and wo run as the reference's torch ops (under the
+caller's autocast) and the layer between them through ``core.TableSdmFunction``, whose backward is the HIP
+``sdm_rt_table_backward`` (gradients of the query, the sub-keys, log_scale and the value tables).
 """
 import math
 
@@ -43,9 +47,6 @@ class TrainedSdm(nn.Module):
         nn.init.zeros_(self.values)
 
     def _check(self, x):
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            raise RuntimeError("TrainedSdm HIP path is forward-only: call it under torch.no_grad() or "
-                               "torch.inference_mode()")
         if x.device.type != "cuda":
             raise RuntimeError("TrainedSdm HIP path needs a ROCm device tensor")
         if x.dim() != 3 or x.shape[-1] != self.d:
@@ -85,8 +86,24 @@ class TrainedSdm(nn.Module):
         return (w[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk),
                 si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk).long())
 
+    def _training(self, x):
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _forward_train(self, x):
+        """The differentiable forward (track4_onesdm_models.py:438-455): q = wq(norm(x).float()).float(), the table
+        layer through TableSdmFunction, wo."""
+        B, T, _ = x.shape
+        q = self.wq(self.norm(x).float()).float()
+        cfg = dict(k=self.k)
+        r = core.TableSdmFunction.apply(q, self.keys1, self.keys2, self.log_scale, self.values, cfg)
+        kk = min(self.k, min(self.k, self.n_sub) ** 2)
+        self.last_si = cfg["slots"][..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
+        return self.wo(r).to(x.dtype)
+
     def forward(self, x):
         self._check(x)
+        if self._training(x):
+            return self._forward_train(x)
         B, T, _ = x.shape
         dt = self._compute_dtype(x)
         with torch.autocast("cuda", enabled=False):

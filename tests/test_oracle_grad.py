@@ -119,3 +119,43 @@ def test_fade_gradient_identity():
     lhs = lam.detach() * lam.grad
     np.testing.assert_allclose(lhs.numpy(), rhs.numpy(), rtol=1e-10, atol=1e-12)
     assert abs(lhs[2].item()) > 1e-3   # a non-trivial fade gradient is checked
+
+
+@pytest.mark.parametrize("n_sub,k", [(4, 3), (5, 6)])
+def test_table_gradients_equal_finite_differences(n_sub, k):
+    """TrainedSdm's read for fixed picks (sdm_grad64.table_from_picks): its value equals sdm_fp64's pk_address +
+    address_weights + table_read, and its autograd gradients (q, both sub-key sets, log_scale, the value tables)
+    equal central finite differences of that numpy forward, which recomputes the picks (checked not to move)."""
+    rng = np.random.default_rng(11 + n_sub)
+    B, T, H, d_a, dh = 1, 6, 2, 4, 3
+    c = dict(q=rng.standard_normal((B, T, H, d_a)), keys1=rng.standard_normal((H, n_sub, d_a // 2)),
+             keys2=rng.standard_normal((H, n_sub, d_a // 2)), log_scale=np.log(8.0) + 0.2 * rng.standard_normal(H),
+             values=rng.standard_normal((H, n_sub * n_sub, dh)))
+
+    def np_read(cc):
+        sv, si = O.pk_address(cc["q"].reshape(B * T, H, d_a), cc["keys1"], cc["keys2"], k)
+        w = O.address_weights(sv, cc["log_scale"])
+        return O.table_read(si, w, cc["values"]).reshape(B, T, H, dh), si
+
+    r_np, si = np_read(c)
+    kk = si.shape[-1]
+    t = {n: torch.tensor(v, requires_grad=True) for n, v in c.items()}
+    r = G.table_from_picks(t["q"], t["keys1"], t["keys2"], t["log_scale"], t["values"], si.reshape(B, T, H, kk))
+    np.testing.assert_allclose(r.detach().numpy(), r_np, rtol=0, atol=1e-12)
+    wgt = np.random.default_rng(5).standard_normal(r_np.shape)
+    (r * torch.tensor(wgt)).sum().backward()
+    h = 1e-6
+    for name, base in c.items():
+        grad = t[name].grad.numpy()
+        for idx in np.ndindex(base.shape):
+            vals = []
+            for sgn in (1.0, -1.0):
+                cc = dict(c)
+                x = np.array(base, np.float64)
+                x[idx] += sgn * h
+                cc[name] = x
+                rr, s2 = np_read(cc)
+                assert np.array_equal(s2, si), f"picks moved at {name}{idx}"
+                vals.append(float(np.sum(rr * wgt)))
+            fd = (vals[0] - vals[1]) / (2 * h)
+            assert abs(fd - grad[idx]) <= 1e-6 * max(1.0, abs(fd)), (name, idx, fd, grad[idx])
