@@ -1160,11 +1160,11 @@ constexpr int kScanThreads = 512;   // 64 positions x 8 lanes
 __host__ __device__ constexpr int pad4(int M) { return (M + 3) / 4 * 4; }
 
 // LDS of one scan workgroup: the slab A[M + 1][CW] and the write counts cnt[M + 1] (row M, which the plan's null
-// write records read, stays zero), the current chunk's variable plan part, its values s_v[64][CW] in float32, fade
-// powers pw[68] and the variable-part sizes of all n_chunks plans.
+// write records read, stays zero), two buffers (chunk parity) of a chunk's staged variable plan part and its values
+// s_v[64][CW] in float32, fade powers pw[68] and the variable-part sizes of all n_chunks plans.
 __host__ __device__ constexpr size_t scan_lds_bytes(int M, int KP, int CW, int n_chunks) {
-  return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + var_stage(KP) +
-         sizeof(float) * kChunk * CW + sizeof(float) * 68 + sizeof(int32_t) * pad4(n_chunks);
+  return sizeof(float) * (static_cast<size_t>(M + 1) * CW + pad4(M + 1)) + 2 * var_stage(KP) +
+         2 * sizeof(float) * kChunk * CW + sizeof(float) * 68 + sizeof(int32_t) * pad4(n_chunks);
 }
 
 // CPL consecutive values (CPL = 4, 2, 1) from LDS in one access; bfloat16 values are converted.
@@ -1320,9 +1320,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   const int M = a.M;
   float* A = lds;                                       // [M + 1][CW]
   float* cnt = A + static_cast<size_t>(M + 1) * CW;     // [M + 1]
-  unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M + 1));
-  float* s_v = reinterpret_cast<float*>(var + VS);
-  float* pw = s_v + kChunk * CW;
+  unsigned char* var = reinterpret_cast<unsigned char*>(cnt + pad4(M + 1));   // [2][VS], by chunk parity
+  float* s_v = reinterpret_cast<float*>(var + 2 * VS);                        // [2][64][CW], by chunk parity
+  float* pw = s_v + 2 * kChunk * CW;
   int32_t* s_sizes = reinterpret_cast<int32_t*>(pw + 68);   // read from LDS: a scalar load in the loop would hold up
                                                             // every LDS wait behind a memory round trip
 
@@ -1351,30 +1351,37 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   }
   float mu = 1.f;
 
+  // S1, stage: chunk c's variable plan part and values into the LDS buffers of its parity (a chunk is staged
+  // during the previous chunk's write phase, so it needs no barrier of its own)
+  auto stage = [&](int c, const ChunkRegs<KP, NV, VT, CPL>& r) {
+    unsigned char* vb = var + (c & 1) * VS;
+    float* sb = s_v + (c & 1) * kChunk * CW;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int piece = tid + k * kScanThreads;
+      if (piece < r.pieces) reinterpret_cast<uint4*>(vb)[piece] = r.var[k];
+    }
+    float vv[CPL];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) vv[k] = to_f32(r.v[k]);
+    lds_seg_store<CPL>(&sb[p * CW + CPL * l8], *reinterpret_cast<const Seg<CPL>*>(vv));
+  };
+
   // the next chunk's registers alternate between two sets (the loop below is unrolled by two), so nothing is copied
   ChunkRegs<KP, NV, VT, CPL> ra, rb;
   fetch_chunk<0>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
   fetch_chunk<1>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
   fetch_chunk<2>(ra, a, slab, b, h, col0, 0, sizes[0], tid, p, l8);
   int next_bytes = a.n_chunks > 1 ? sizes[1] : 0;
+  stage(0, ra);
   lds_barrier();
   const float lam_chunk = pw[kChunk];   // the fade of a full chunk, kept in a register
 
   auto chunk = [&](const int c, const ChunkRegs<KP, NV, VT, CPL>& nx, ChunkRegs<KP, NV, VT, CPL>& fut) {
     const int c0 = c * kChunk;
     const int L = min(kChunk, a.T - c0);
-    // S1: stage
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int piece = tid + k * kScanThreads;
-      if (piece < nx.pieces) reinterpret_cast<uint4*>(var)[piece] = nx.var[k];
-    }
-    {
-      float vv[CPL];
-#pragma unroll
-      for (int k = 0; k < CPL; ++k) vv[k] = to_f32(nx.v[k]);
-      lds_seg_store<CPL>(&s_v[p * CW + CPL * l8], *reinterpret_cast<const Seg<CPL>*>(vv));
-    }
+    const unsigned char* varc = var + (c & 1) * VS;   // this chunk's staged plan part and values
+    const float* s_vc = s_v + (c & 1) * kChunk * CW;
     // this chunk's records
     int m[KP];
     float w[KP];
@@ -1410,14 +1417,13 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       own_slot[k] = static_cast<int>(nx.own_slot[k]);
       own_wt[k] = nx.own_wt[k];
     }
-    lds_barrier();
     const bool more = c + 1 < a.n_chunks;
     if (more) {
       fetch_chunk<2>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
       fetch_chunk<0>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
       next_bytes = c + 2 < a.n_chunks ? s_sizes[c + 2] : 0;
     }
-    const uint32_t* hdr = reinterpret_cast<const uint32_t*>(var);
+    const uint32_t* hdr = reinterpret_cast<const uint32_t*>(varc);
     const int n_ri = hdr[0], n_ext = hdr[2];
     const bool chunk_reset = hdr[1] & 0x80000000u;
     // variable-part entries: from LDS within the staged bytes, else from the plan in global memory
@@ -1425,15 +1431,15 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     const int o_ri_c = 16 + 8 * n_ext, o_ri_q = 16 + 8 * n_ext + 4 * n_ri;
     auto ext_at = [&](int e) {
       const int o = 16 + 8 * e;
-      return o + 8 <= VS ? *reinterpret_cast<const uint2*>(var + o) : *reinterpret_cast<const uint2*>(gvar + o);
+      return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
     };
     auto ri_c_at = [&](int k) {
       const int o = o_ri_c + 4 * k;
-      return o + 4 <= VS ? *reinterpret_cast<const float*>(var + o) : *reinterpret_cast<const float*>(gvar + o);
+      return o + 4 <= VS ? *reinterpret_cast<const float*>(varc + o) : *reinterpret_cast<const float*>(gvar + o);
     };
     auto ri_q_at = [&](int k) {
       const int o = o_ri_q + k;
-      return static_cast<int>(o < VS ? var[o] : gvar[o]);
+      return static_cast<int>(o < VS ? varc[o] : gvar[o]);
     };
     // S2: read
     if (p < L) {
@@ -1447,7 +1453,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 #pragma unroll
       for (int i = 0; i < KP; ++i) x[i] = lds_seg<CPL>(&A[m[i] * CW + CPL * l8]);
 #pragma unroll
-      for (int t = 0; t < kInline; ++t) vi[t] = lds_seg<CPL>(&s_v[(t < n_in ? iq[t] : 0) * CW + CPL * l8]);
+      for (int t = 0; t < kInline; ++t) vi[t] = lds_seg<CPL>(&s_vc[(t < n_in ? iq[t] : 0) * CW + CPL * l8]);
       float acc[CPL];
 #pragma unroll
       for (int k = 0; k < CPL; ++k) acc[k] = 0.f;
@@ -1471,7 +1477,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         for (int j = 0; j < 4; ++j) {
           const int ej = min(e + j, ri_e - 1);
           cf[j] = e + j < ri_e ? ri_c_at(ej) : 0.f;
-          vq[j] = lds_seg<CPL>(&s_v[ri_q_at(ej) * CW + CPL * l8]);
+          vq[j] = lds_seg<CPL>(&s_vc[ri_q_at(ej) * CW + CPL * l8]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1520,7 +1526,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
           const uint32_t rx = wr[k0 + j].x;
           dc[j] = __uint_as_float(wr[k0 + j].y & 0x7fffffffu) * inv_mu;
           x[j] = lds_seg<CPL>(&A[(rx & 0xffffu) * CW + CPL * l8]);
-          vq[j] = lds_seg<CPL>(&s_v[((rx >> 16) & 63u) * CW + CPL * l8]);
+          vq[j] = lds_seg<CPL>(&s_vc[((rx >> 16) & 63u) * CW + CPL * l8]);
         }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
@@ -1532,7 +1538,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
             do {
               t = ext_at(e++);
               const float cf = __uint_as_float(t.x) * inv_mu;
-              const Seg<CPL> vx = lds_seg<CPL>(&s_v[(t.y & 63u) * CW + CPL * l8]);
+              const Seg<CPL> vx = lds_seg<CPL>(&s_vc[(t.y & 63u) * CW + CPL * l8]);
 #pragma unroll
               for (int k = 0; k < CPL; ++k) x[j].v[k] = fmaf(cf, vx.v[k], x[j].v[k]);
             } while (!(t.y & 0x80000000u));
@@ -1559,6 +1565,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         if (mc != M) cnt[mc] = cold + dcc;
       }
     }
+    if (more) stage(c + 1, fut);   // the other parity's buffers: free since the previous chunk's last barrier
     mu = mu_new;
     lds_barrier();
   };
