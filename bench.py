@@ -269,7 +269,8 @@ def main():
     ap.add_argument("--train-only", action="store_true", help="only the backward measurement (for profiler runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer's sharding is described in DESIGN.md",
+        print(f"bench.py measures one GPU only (asked for {a.gpus}); the mixer runs on one GPU here, so no figure at "
+              "several GPUs is produced",
               file=sys.stderr)
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 """CPU oracle for the run-time SDM mixer (RunTimeSdm) -- TEST INFRASTRUCTURE ONLY.
 
 Nothing in the product package imports this package.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import it, and there only as the checker (or, for ``cpu_baseline``, as the
+``cpu_baseline`` leg of ``bench.py`` may import it, and there only to check results (or, for ``cpu_baseline``, as the
 timed CPU restatement), never as a path that produces product results.
 
 Modules
@@ -11,6 +11,8 @@ Modules
 ``sdm_torch32`` torch float32 CPU restatement that follows the reference's op sequence (F.normalize, einsum, topk,
                dense chunk scatter and matmuls), so its addressing bits equal the reference's when run with the same
                torch build.  It is also the timed CPU baseline.
+``sdm_grad64`` float64 torch restatement of the core (and of TrainedSdm's table read) for fixed picks, differentiated
+               by torch autograd: the oracle of the backward kernels.
 
 Pinning (what each oracle function is checked against in ``tests/``):
   * ``sdm_torch32.pk_address`` -- bit-exact against golden vectors written by the reference's own ``pk_address``
@@ -21,4 +23,7 @@ Pinning (what each oracle function is checked against in ``tests/``):
     prefix sum), gate ~ 0 gives a zero read, and equality with ``sdm_torch32`` chunked form for chunk sizes
     1, 5, 7, 23, 64, 128 and T.
   * softmax / sigmoid / RMSNorm / out-norm -- textbook closed forms, checked on hand-computed values.
+  * ``sdm_grad64.core_from_picks`` / ``table_from_picks`` -- forward equal to ``sdm_fp64`` (token recurrence, table
+    read) to 1e-12; every autograd gradient equal to central finite differences of the ``sdm_fp64`` forward (picks
+    recomputed and checked not to move); the fade identity lam dL/dlam = sum_t t P_t - sum_s (s+1) Q_s.
 """
