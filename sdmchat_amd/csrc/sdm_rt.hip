@@ -904,13 +904,16 @@ __host__ __device__ constexpr int var_stage(int KP) {
 // static LDS of plan_kernel (picks, fade powers, totals)
 __host__ __device__ constexpr size_t plan_static_lds(int KP) { return 2 * kChunk * KP * (2 + 4) + 4 * (kChunk + 4) + 16; }
 
-// inclusive prefix sum over the 64 lanes of a wave
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(v, off, 64);
-    if (lane >= off) v += t;
-  }
+// inclusive prefix sum over the 64 lanes of a wave, by DPP: shifts by 1, 2, 4 and 8 lanes within each row of 16
+// (lanes shifted in from outside the row read 0), then the last lane of row 0 added to row 1 and of row 2 to row 3
+// (row_bcast:15), then lane 31 to rows 2 and 3 (row_bcast:31).  The whole wave must be active.
+__device__ __forceinline__ int wave_incl_scan(int v, int) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 
