@@ -946,8 +946,12 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   if constexpr (MODE == 0) stage_keys<HALF>(a.g, h, kn, tid, 128);
   for (int i = tid; i < M; i += 128) wmask[i] = 0ull;
   if (tid <= kChunk) {
-    float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
-    for (int e = 0; e < tid; ++e) v *= lam;
+    float v = 1.f, sq = lam;   // lam^tid by squaring (exact for lam = 0 and lam = 1)
+#pragma unroll
+    for (int bit = 0; bit < 7; ++bit) {
+      v = ((tid >> bit) & 1) ? v * sq : v;
+      sq *= sq;
+    }
     pw[tid] = v;
   }
   if constexpr (MODE == 0) __syncthreads();
