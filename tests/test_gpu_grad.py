@@ -136,6 +136,13 @@ def test_grad_sixteen_picks():
     check_case("k16", 14, 1, 100, 2, 16, 8, 8, 16, overlap=0.7)
 
 
+def test_grad_crowded_chunks_read_chains_past_the_staged_part():
+    """n_sub = 4 gives M = 16 locations and k = 16 picks them all: every position writes every slot, so each chunk of
+    both grad scans holds 64 * 16 - 16 = 1,008 later-writer chain entries, past the 384 a scan stages in LDS at
+    k = 16; the rest are read from the chain plan in global memory."""
+    check_case("crowded-k16", 21, 1, 200, 2, 16, 8, 4, 16, overlap=0.9)
+
+
 def test_grad_layer_shape_bf16():
     """The layer shape of the validation workload (H=12, dh=64, d_a=64, M=1024, k=8), bfloat16 projections."""
     check_case("layer-bf16", 15, 1, 256, 12, 64, 64, 32, 8, dtype=torch.bfloat16, overlap=0.8, reset_p=0.01)
