@@ -1292,7 +1292,7 @@ __device__ __forceinline__ void fetch_chunk(ChunkRegs<KP, NV, VT, CPL>& r, const
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int piece = tid + k * kScanThreads;
-      r.var[k] = piece < r.pieces ? vs[piece] : make_uint4(0u, 0u, 0u, 0u);
+      r.var[k] = vs[piece < r.pieces ? piece : 0];   // every lane loads (piece 0 stands in); staging skips the rest
     }
     const int row = min(c * kChunk + p, a.T - 1);
     const VT* vrow = static_cast<const VT*>(a.v) + (static_cast<int64_t>(b) * a.T + row) * a.v_stride +
@@ -1425,28 +1425,36 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       own_wt[k] = nx.own_wt[k];
     }
     const bool more = c + 1 < a.n_chunks;
-    if (more) {
-      fetch_chunk<2>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
-      fetch_chunk<0>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
-      next_bytes = c + 2 < a.n_chunks ? s_sizes[c + 2] : 0;
-    }
+    // the next chunk's loads, unconditional (the last chunk fetches itself again): with a fixed number of loads in
+    // flight every later wait for this chunk's registers is exact and does not wait for them
+    const int cn = more ? c + 1 : c;
+    fetch_chunk<2>(fut, a, slab, b, h, col0, cn, next_bytes, tid, p, l8);
+    fetch_chunk<0>(fut, a, slab, b, h, col0, cn, next_bytes, tid, p, l8);
+    if (more) next_bytes = c + 2 < a.n_chunks ? s_sizes[c + 2] : 0;
     const uint32_t* hdr = reinterpret_cast<const uint32_t*>(varc);
     const int n_ri = hdr[0], n_ext = hdr[2];
     const bool chunk_reset = hdr[1] & 0x80000000u;
     // variable-part entries: from LDS within the staged bytes, else from the plan in global memory
     const unsigned char* gvar = a.plans + (slab * a.n_chunks + c) * pg.stride() + pg.off_var();
     const int o_ri_c = 16 + 8 * n_ext, o_ri_q = 16 + 8 * n_ext + 4 * n_ri;
-    auto ext_at = [&](int e) {
+    // With st = std::true_type the whole part is staged and the entries come from LDS only.  The two code paths
+    // stay separate: a global load on a joined path makes every use wait for all vector-memory loads in flight,
+    // the next chunk's prefetched records included.
+    const bool all_staged = static_cast<int>(hdr[3]) <= VS;
+    auto ext_at = [&](int e, auto st) {
       const int o = 16 + 8 * e;
-      return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
+      if constexpr (decltype(st)::value) return *reinterpret_cast<const uint2*>(varc + o);
+      else return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
     };
-    auto ri_c_at = [&](int k) {
+    auto ri_c_at = [&](int k, auto st) {
       const int o = o_ri_c + 4 * k;
-      return o + 4 <= VS ? *reinterpret_cast<const float*>(varc + o) : *reinterpret_cast<const float*>(gvar + o);
+      if constexpr (decltype(st)::value) return *reinterpret_cast<const float*>(varc + o);
+      else return o + 4 <= VS ? *reinterpret_cast<const float*>(varc + o) : *reinterpret_cast<const float*>(gvar + o);
     };
-    auto ri_q_at = [&](int k) {
+    auto ri_q_at = [&](int k, auto st) {
       const int o = o_ri_q + k;
-      return static_cast<int>(o < VS ? varc[o] : gvar[o]);
+      if constexpr (decltype(st)::value) return static_cast<int>(varc[o]);
+      else return static_cast<int>(o < VS ? varc[o] : gvar[o]);
     };
     // S2: read
     if (p < L) {
@@ -1477,20 +1485,27 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
 #pragma unroll
         for (int k = 0; k < CPL; ++k) acc[k] = fmaf(cf, vi[t].v[k], acc[k]);
       }
-      for (int e = ri_b; e < ri_e; e += 4) {   // the rest, from the variable part, four at a time
-        float cf[4];
-        Seg<CPL> vq[4];
+      auto ri_loop = [&](auto st) {
+        for (int e = ri_b; e < ri_e; e += 4) {   // the rest, from the variable part, four at a time
+          float cf[4];
+          Seg<CPL> vq[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ej = min(e + j, ri_e - 1);
-          cf[j] = e + j < ri_e ? ri_c_at(ej) : 0.f;
-          vq[j] = lds_seg<CPL>(&s_vc[ri_q_at(ej) * CW + CPL * l8]);
+          for (int j = 0; j < 4; ++j) {
+            const int ej = min(e + j, ri_e - 1);
+            cf[j] = e + j < ri_e ? ri_c_at(ej, st) : 0.f;
+            vq[j] = lds_seg<CPL>(&s_vc[ri_q_at(ej, st) * CW + CPL * l8]);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) acc[k] = fmaf(cf[j], vq[j].v[k], acc[k]);
+          }
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int k = 0; k < CPL; ++k) acc[k] = fmaf(cf[j], vq[j].v[k], acc[k]);
-        }
+      };
+      if (all_staged) {
+        ri_loop(std::true_type{});
+      } else {
+        ri_loop(std::false_type{});
       }
       const float cn = sum8(cpart);
       if (a.read_mean) {
@@ -1504,7 +1519,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
                                static_cast<int64_t>(h) * a.dh + col0 + CPL * l8, acc);
     }
     lds_barrier();
-    if (more) fetch_chunk<1>(fut, a, slab, b, h, col0, c + 1, next_bytes, tid, p, l8);
+    fetch_chunk<1>(fut, a, slab, b, h, col0, cn, next_bytes, tid, p, l8);
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
     float fade = lam_chunk;
     if (L != kChunk) fade = pw[L];
@@ -1522,7 +1537,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
       lds_barrier();
     }
     // S3: write; group p applies records p + 64 k, NB at a time (distinct slots; null records write nothing)
-    {
+    auto write_phase = [&](auto st) {
       const float inv_mu = fast_rcp(mu_new);
 #pragma unroll
       for (int k0 = 0; k0 < KP; k0 += NB) {
@@ -1543,7 +1558,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
             int e = wr[k0 + j].x >> 22;
             uint2 t;
             do {
-              t = ext_at(e++);
+              t = ext_at(e++, st);
               const float cf = __uint_as_float(t.x) * inv_mu;
               const Seg<CPL> vx = lds_seg<CPL>(&s_vc[(t.y & 63u) * CW + CPL * l8]);
 #pragma unroll
@@ -1559,7 +1574,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
           int e = ow.x >> 22;
           uint2 t;
           do {
-            t = ext_at(e++);
+            t = ext_at(e++, st);
             dcc += __uint_as_float(t.x) * inv_mu;
           } while (!(t.y & 0x80000000u));
         }
@@ -1571,6 +1586,11 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         }
         if (mc != M) cnt[mc] = cold + dcc;
       }
+    };
+    if (all_staged) {
+      write_phase(std::true_type{});
+    } else {
+      write_phase(std::false_type{});
     }
     if (more) stage(c + 1, fut);   // the other parity's buffers: free since the previous chunk's last barrier
     mu = mu_new;
