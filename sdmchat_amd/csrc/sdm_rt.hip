@@ -1752,25 +1752,36 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   float* mem = a.mem + sl * a.M * a.dh;
   float* cnt = a.cnt + sl * a.M;
   const int kk = a.kk;
-  // every load that does not depend on the state first: the picks (pads: slot -1, weight 0) and the value row
+  // every load that does not depend on the state first, all issued together: the picks (pads: slot -1 read as
+  // row 0 with weight 0; the weights of picks past kk are masked after the load), the value row, the scale, the
+  // fade, the reset flag and the out-norm weights.  Loads stay unconditional (indexes clamped, null arrays read a
+  // stand-in word of the scales): a load under a branch would be waited for on its own.
   int rsl[KP], wsl[KP];
   float rwv[KP], wwv[KP];
 #pragma unroll
   for (int j = 0; j < KP; ++j) {
     rsl[j] = max(a.rslot[sl * KP + j], 0);
-    rwv[j] = a.rwt[sl * KP + j];
+    const float rw = a.rwt[sl * KP + j];
+    rwv[j] = j < kk ? rw : 0.f;
     wsl[j] = max(a.wslot[sl * KP + j], 0);
-    wwv[j] = a.wwt[sl * KP + j];
+    const float ww = a.wwt[sl * KP + j];
+    wwv[j] = j < kk ? ww : 0.f;
   }
   const VT* vrow = static_cast<const VT*>(a.v) + static_cast<int64_t>(b) * a.v_stride + static_cast<int64_t>(h) * a.dh;
-  float vv[kCols];
+  float vv[kCols], onw[kCols];
 #pragma unroll
   for (int q = 0; q < kCols; ++q) {
     const int c = lane + 64 * q;
-    vv[q] = c < a.dh ? to_f32(vrow[c]) : 0.f;
+    const int cc = min(c, a.dh - 1);
+    const float v0 = to_f32(vrow[cc]);
+    vv[q] = c < a.dh ? v0 : 0.f;
+    const float w0 = *(a.out_norm ? a.onorm_w + h * a.dh + cc : a.scale + sl);
+    onw[q] = a.out_norm ? w0 : 1.f;
   }
   float mu = a.scale[sl];
-  if (a.reset && a.reset[b]) {   // a document starts here: the memory is emptied before the read
+  const float lam = a.decay[h];
+  const uint8_t rst = *(a.reset ? a.reset + b : reinterpret_cast<const uint8_t*>(a.scale + sl));
+  if (a.reset && rst) {   // a document starts here: the memory is emptied before the read
     scale_slab(mem, cnt, a.M, a.dh, 0.f, lane);
     mu = 1.f;
     __threadfence_block();
@@ -1786,14 +1797,14 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
     if (c < a.dh) {
       float row[KP];
 #pragma unroll
-      for (int j = 0; j < KP; ++j) row[j] = j < kk ? mem[static_cast<int64_t>(rsl[j]) * a.dh + c] : 0.f;
+      for (int j = 0; j < KP; ++j) row[j] = mem[static_cast<int64_t>(rsl[j]) * a.dh + c];   // weight 0 past kk
 #pragma unroll
       for (int j = 0; j < KP; ++j) acc[q] = fmaf(rwv[j], row[j], acc[q]);
     }
   }
   float cr[KP];
 #pragma unroll
-  for (int j = 0; j < KP; ++j) cr[j] = j < kk ? cnt[rsl[j]] : 0.f;
+  for (int j = 0; j < KP; ++j) cr[j] = cnt[rsl[j]];
   float den = 0.f;
 #pragma unroll
   for (int j = 0; j < KP; ++j) den = fmaf(rwv[j], cr[j], den);
@@ -1809,9 +1820,14 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
     ss = fmaf(r[q], r[q], ss);
   }
   float on = 1.f;
-  if (a.out_norm) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if (a.out_norm) {   // the wave sum: rows of 16 lanes by DPP, then the four row sums
+    float s16 = sum8(ss);
+    s16 += dpp_f<0x140>(s16);   // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s16), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s16), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s16), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s16), 48));
+    ss = (r0 + r1) + (r2 + r3);
     on = rsqrtf(ss / static_cast<float>(a.dh) + a.out_norm_eps);
   }
 #pragma unroll
@@ -1819,14 +1835,14 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
     const int c = lane + 64 * q;
     if (c < a.dh) {
       float o = r[q];
-      if (a.out_norm) o = o * on * a.onorm_w[h * a.dh + c];
+      if (a.out_norm) o = o * on * onw[q];
       const int64_t at = static_cast<int64_t>(b) * a.r_stride + static_cast<int64_t>(h) * a.dh + c;
       if (a.out_bf16) static_cast<bf16_t*>(a.r_out)[at] = from_f32<bf16_t>(o);
       else static_cast<float*>(a.r_out)[at] = o;
     }
   }
   // fade (O(1) through the scale; rescale the slab when the scale gets small), then write (:294-298)
-  float mu2 = mu * a.decay[h];
+  float mu2 = mu * lam;
   if (!(mu2 >= kMuFloor)) {
     scale_slab(mem, cnt, a.M, a.dh, mu2, lane);
     mu2 = 1.f;
@@ -1840,7 +1856,7 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
     if (c < a.dh) {
       float old[KP];
 #pragma unroll
-      for (int j = 0; j < KP; ++j) old[j] = j < kk ? mem[static_cast<int64_t>(wsl[j]) * a.dh + c] : 0.f;
+      for (int j = 0; j < KP; ++j) old[j] = mem[static_cast<int64_t>(wsl[j]) * a.dh + c];   // stored only below kk
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
         if (j < kk) mem[static_cast<int64_t>(wsl[j]) * a.dh + c] = fmaf(wwv[j] * inv, vv[q], old[j]);
@@ -1850,7 +1866,7 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   if (lane == 0) {
     float oc[KP];
 #pragma unroll
-    for (int j = 0; j < KP; ++j) oc[j] = j < kk ? cnt[wsl[j]] : 0.f;
+    for (int j = 0; j < KP; ++j) oc[j] = cnt[wsl[j]];
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
       if (j < kk) cnt[wsl[j]] = oc[j] + wwv[j] * inv;
