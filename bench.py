@@ -110,7 +110,7 @@ def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
     kz, qz, V, g = m._project(xt, torch.bfloat16)
     kz, qz, V, g = kz[:, 0], qz[:, 0], V[:, 0], g[:, 0]
     st = m.decode_state(streams, dev)
-    prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, m.wg.bias)
+    prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, None)
     ws = core.CoreWorkspace()
     out = torch.empty(streams, D, dtype=torch.bfloat16, device=dev)
 
@@ -291,7 +291,7 @@ def main():
 
     with torch.no_grad():
         kz, qz, V, g = m._project(x, torch.bfloat16)
-        prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, m.wg.bias)
+        prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, None)
         ws = core.CoreWorkspace()
         r_out = torch.empty(B, T, D, dtype=torch.bfloat16, device=dev)
 

@@ -340,6 +340,30 @@ def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
     return out
 
 
+class RmsNormFunction(torch.autograd.Function):
+    """rms_norm as an autograd function: the forward on the RMSNorm kernel (the reference's rounding, SM:63-71), the
+    backward of y = x * rsqrt(mean(x^2) + eps) * w in float32 with the casts taken as identities, as autograd takes
+    the reference's ``.to(x.dtype)``.  apply(x, w, eps, out_dtype) -> y."""
+
+    @staticmethod
+    def forward(ctx, x, w, eps, out_dtype):
+        ctx.save_for_backward(x, w)
+        ctx.eps = eps
+        return rms_norm(x, w, eps, out_dtype=out_dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        xf = x.float()
+        r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + ctx.eps)
+        n = xf * r
+        g = dy.float()
+        gw = g * w.float()
+        dx = r * (gw - n * (gw * n).mean(-1, keepdim=True)) if ctx.needs_input_grad[0] else None
+        dw = (g * n).reshape(-1, n.shape[-1]).sum(0) if ctx.needs_input_grad[1] else None
+        return (None if dx is None else dx.to(x.dtype), None if dw is None else dw.to(w.dtype), None, None)
+
+
 # -- training: forward with saved tensors, backward, and the autograd Function -------------------------------------
 def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
     B, T = v.shape[0], v.shape[1]

@@ -102,24 +102,31 @@ class RunTimeSdm(nn.Module):
 
     # -- fused input projection ----------------------------------------------------------------------------------
     def _fused_weight(self, dtype):
-        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 256, a shape hipBLASLt runs well), cached until a
-        weight changes."""
+        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 256, a shape hipBLASLt runs well), the matching
+        bias (zero except wg.bias on the gate rows; None without the write gate) and wo, all in ``dtype``, cached
+        until one of these tensors changes (data pointer or in-place version)."""
         ws = (self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight)
-        key = (dtype, ws[0].device) + tuple((w.data_ptr(), w._version) for w in ws)
+        srcs = ws + (self.wg.bias, self.wo.weight)
+        key = (dtype, ws[0].device, self.write_gate) + tuple((t.data_ptr(), t._version) for t in srcs)
         if self._fused is not None and self._fused[0] == key:
-            return self._fused[1], self._fused[2]
+            return self._fused[1:]
         rows = sum(w.shape[0] for w in ws)
         padded = (rows + 255) // 256 * 256
         W = torch.zeros(padded, self.d, dtype=dtype, device=ws[0].device)
         W[:rows].copy_(torch.cat([w.detach() for w in ws], 0))
+        bias = None
+        if self.write_gate:   # the gate logit rounds once, as the reference's wg(hx) under autocast (OM:205)
+            bias = torch.zeros(padded, dtype=dtype, device=ws[0].device)
+            bias[rows - self.h:rows].copy_(self.wg.bias.detach())
         wo = self.wo.weight.detach().to(dtype)
-        self._fused = (key, W, wo)
-        return W, wo
+        self._fused = (key, W, bias, wo)
+        return W, bias, wo
 
     def _core_params(self, device):
-        """The core's float32 parameters, converted once per change of the module's tensors."""
+        """The core's float32 parameters, converted once per change of the module's tensors (no gate bias: it is
+        the fused projection's bias)."""
         return self._prm.get(device, self.keys1, self.keys2, self.addr_b, self.log_scale, self.decay,
-                             self.onorm_w if self.out_norm else None, self.wg.bias if self.write_gate else None,
+                             self.onorm_w if self.out_norm else None, None,
                              decay_source=self.decay_logit if self.learn_decay else self.decays_fixed)
 
     def _check(self, x, reset):
@@ -141,12 +148,13 @@ class RunTimeSdm(nn.Module):
 
     def _project(self, x, dt):
         """RMSNorm then one fused GEMM for wk, wq, wv, wg (prepare, track4_onesdm_models.py:197-206).  Returns views
-        kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer;
-        addr_b and the gate bias are added inside the core."""
+        kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer.
+        The gate bias is the GEMM's bias, so W_g hx + b rounds to dt once, as wg(hx) does; addr_b is added inside
+        the core."""
         H, d_a, d = self.h, self.d_a, self.d
         hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
-        W = self._fused_weight(dt)[0]
-        proj = torch.matmul(hx, W.t())                                 # [B, T, padded rows]
+        W, bias = self._fused_weight(dt)[:2]
+        proj = F.linear(hx, W, bias)                                   # [B, T, padded rows]
         o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
         g = proj[..., o_g:o_g + H] if self.write_gate else None
         return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
@@ -154,28 +162,36 @@ class RunTimeSdm(nn.Module):
     def _training(self, x):
         return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
 
-    def _forward_train(self, x, reset):
-        """The differentiable forward: the reference's prepare (:195-213) in torch ops up to the projections, the
-        core through SdmCoreFunction, finish's wo (:247).  Under autocast the projections and wo run in its dtype,
-        as in the reference."""
-        B, T, _ = x.shape
+    def _project_train(self, x):
+        """The differentiable prepare (:195-206) up to the projections: the input norm on the RMSNorm kernel
+        (core.RmsNormFunction, with its float32 backward) and the same padded fused GEMM with the gate bias as
+        inference, so both forwards compute the same values.  Under autocast the GEMM runs in its dtype, as in the
+        reference.  Returns kz, qz, V, g (None without the write gate)."""
         H, d_a, d = self.h, self.d_a, self.d
-        hx = self.norm(grad_scale(x, self.mem_in_grad)).float()
-        ws = [self.wk.weight, self.wq.weight, self.wv.weight]
-        bias = None
-        if self.write_gate:   # the gate bias inside the projection, so the logit rounds as wg(hx) does
-            ws.append(self.wg.weight)
-            bias = torch.cat([self.wg.bias.new_zeros(2 * H * d_a + d), self.wg.bias])
-        proj = F.linear(hx, torch.cat(ws, 0), bias)
+        hx = core.RmsNormFunction.apply(grad_scale(x, self.mem_in_grad), self.norm.w, self.norm.eps,
+                                        torch.promote_types(x.dtype, self.norm.w.dtype)).float()
+        W = torch.cat([self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight], 0)
+        rows = W.shape[0]
+        pad = (rows + 255) // 256 * 256 - rows
+        W = F.pad(W, (0, 0, 0, pad))
+        # the gate bias inside the projection, so the logit rounds once, as wg(hx) does
+        bias = F.pad(self.wg.bias, (rows - H, pad)) if self.write_gate else None
+        proj = F.linear(hx, W, bias)
         o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
-        kz, qz, V = proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g]
         g = proj[..., o_g:o_g + H] if self.write_gate else None
+        return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
+
+    def _forward_train(self, x, reset):
+        """The differentiable forward: _project_train, the core through SdmCoreFunction, finish's wo (:247)."""
+        B, T, _ = x.shape
+        H = self.h
+        kz, qz, V, g = self._project_train(x)
         cfg = dict(k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
                    out_norm_eps=self.out_norm_eps, reset=reset, workspace=self._ws)
         r = core.SdmCoreFunction.apply(kz, qz, V, g, self.keys1, self.keys2, self.addr_b, self.log_scale,
                                        self.decay(), self.onorm_w if self.out_norm else None, None, cfg)
         y = self.wo(r).to(x.dtype)
-        self._gate_src = (g.detach() if g is not None else None, None, (B, T, H), x.device)
+        self._gate_src = (g.detach().contiguous() if g is not None else None, None, (B, T, H), x.device)
         self._last_gate = None
         self.last_state = None
         return y
@@ -195,16 +211,17 @@ class RunTimeSdm(nn.Module):
         H = self.h
         with torch.autocast("cuda", enabled=False):
             kz, qz, V, g = self._project(x, dt)
-            wo = self._fused_weight(dt)[1]
+            wo = self._fused_weight(dt)[2]
             res = core.core_forward(
                 kz, qz, V, g, keys1=self.keys1, keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(),
                 addr_b=self.addr_b, onorm_w=self.onorm_w if self.out_norm else None,
-                gate_bias=self.wg.bias if self.write_gate else None, k=self.k, read_mode=self.read_mode,
+                gate_bias=None, k=self.k, read_mode=self.read_mode,
                 out_norm=self.out_norm, read_eps=self.read_eps, out_norm_eps=self.out_norm_eps, out_dtype=dt,
                 want_state=self.keep_state, workspace=self._ws, reset=reset, params=self._core_params(x.device))
             r, state = (res if self.keep_state else (res, None))
             y = torch.matmul(r, wo.t()).to(x.dtype)
-        self._gate_src = (g, self.wg.bias.detach() if self.write_gate else None, (B, T, H), x.device)
+        # the gate logits alone ([B, T, H]; a view would keep the whole projection buffer alive)
+        self._gate_src = (g.contiguous() if g is not None else None, None, (B, T, H), x.device)
         self._last_gate = None
         self.last_state = state
         return y
@@ -246,11 +263,11 @@ class RunTimeSdm(nn.Module):
         dt = self._compute_dtype(x2)
         with torch.autocast("cuda", enabled=False):
             kz, qz, V, g = self._project(x2.unsqueeze(1), dt)
-            wo = self._fused_weight(dt)[1]
+            wo = self._fused_weight(dt)[2]
             r = core.decode_step(
                 kz[:, 0], qz[:, 0], V[:, 0], None if g is None else g[:, 0], state, keys1=self.keys1,
                 keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(), addr_b=self.addr_b,
-                onorm_w=self.onorm_w if self.out_norm else None, gate_bias=self.wg.bias if self.write_gate else None,
+                onorm_w=self.onorm_w if self.out_norm else None, gate_bias=None,
                 k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
                 out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
                 params=self._core_params(x.device))

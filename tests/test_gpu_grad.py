@@ -211,10 +211,7 @@ def test_module_training_step_matches_the_oracle():
     (y * wgt).sum().backward()
     torch.cuda.synchronize()
     with torch.no_grad():   # the picks of the module's own projections (the same fused product)
-        hx = m.norm(x).float()
-        W = torch.cat([m.wk.weight, m.wq.weight, m.wv.weight, m.wg.weight], 0)
-        bias = torch.cat([m.wg.bias.new_zeros(2 * H * d_a + d), m.wg.bias])
-        proj = torch.nn.functional.linear(hx, W, bias)
+        proj = torch.cat(m._project_train(x)[:2], -1)
         kz, qz = proj[..., :H * d_a], proj[..., H * d_a:2 * H * d_a]
         siw, _, _ = core.address(kz, m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)
         sir, _, _ = core.address(qz, m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)
@@ -307,10 +304,7 @@ def test_onesdm_training_step_matches_the_oracle():
     picks = []
     with torch.no_grad():
         for i, m in enumerate(model.mems):
-            hx = m.norm(inputs[i]).float()
-            W = torch.cat([m.wk.weight, m.wq.weight, m.wv.weight, m.wg.weight], 0)
-            bias = torch.cat([m.wg.bias.new_zeros(2 * H * d_a + d), m.wg.bias])
-            proj = torch.nn.functional.linear(hx, W, bias)
+            proj = torch.cat(m._project_train(inputs[i])[:2], -1)
             sw = core.address(proj[..., :H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
             sr = core.address(proj[..., H * d_a:2 * H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
             picks.append((sw.permute(0, 2, 1, 3).long().cpu(), sr.permute(0, 2, 1, 3).long().cpu()))

@@ -8,8 +8,9 @@ import pytest
 import torch
 
 from oracle import sdm_fp64 as O
-from sdmchat_amd import RunTimeSdm, synthetic as S
-from tests._gpu_util import DELTA, assert_close, check_core, say
+from sdmchat_amd import RunTimeSdm, core, synthetic as S
+from tests._gpu_util import (DELTA, assert_close, check_picks, gpu_address, half_ulp_bf16, say,
+                              scan_from_picks)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,29 +48,120 @@ def test_module_fp32_end_to_end():
     assert float(m.last_gate.min()) >= 0 and float(m.last_gate.max()) <= 1
 
 
-def test_module_bf16_core_and_output_map():
-    """bf16 activations: the core on the module's own projections (picks against the oracle, read-out against the
-    fp64 recurrence on those picks), and y against the output map applied in float64 to the read-out (2e-3 plus half
-    a bf16 ulp for the bf16 outputs)."""
+def _bf16(a):
+    """float values rounded to bfloat16 (nearest even), as float64."""
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).double().numpy()
+
+
+def _autocast_norm(x, w):
+    """The reference's input norm before bf16 autocast's cast: bf16(bf16(x * rsqrt(mean x^2 + eps)) * w)
+    (RMSNorm, SM:69-71), the scale in float32."""
+    xf = np.asarray(x, np.float32)
+    r = (1.0 / np.sqrt(np.mean(xf.astype(np.float64) ** 2, -1, keepdims=True) + 1e-6)).astype(np.float32)
+    return _bf16(_bf16(xf * r) * np.asarray(w, np.float32))
+
+
+def _autocast_projections(hx, p):
+    """The reference's projections under bf16 autocast (OM:199-205), restated: bf16(hx . bf16(W)^T + bf16(b)) with
+    the sum in float64.  Returns, per projection, the value and the sum of the |terms| (its error scale)."""
+    out = {}
+    for n in ("wk", "wq", "wv", "wg"):
+        w = _bf16(p[f"{n}.weight"])
+        y = hx @ w.T
+        if n == "wg":
+            y = y + _bf16(p["wg.bias"])
+        out[n] = (_bf16(y), np.abs(hx) @ np.abs(w).T)
+    return out
+
+
+def test_module_bf16_end_to_end():
+    """bf16 x -> y at the bench shape (B=8, T=2048, d=768, H=12, M=1,024, k=8), every stage against an
+    independent restatement: the norm and the four projections against the reference's autocast roundings (at most
+    one bf16 ulp apart, on under 0.1% of the values: the GEMM sums in a different order); every pick against the
+    fp64 oracle (margin rule); then, for batch rows 0 and 7, the read-out of all 12 heads from the fp64 recurrence
+    and y = bf16(r) wo^T in float64 (OM:247 under autocast), within 2e-3 plus half a bf16 ulp.  The gate bias is
+    non-zero, so the gate logit's rounding (bf16(W_g hx + b), OM:205) is exercised."""
     cfg = S.layer_cfg()
     p = S.layer_params(cfg, seed=63)
-    x = torch.from_numpy(S.layer_input(2, 512, 768, seed=64)).cuda().to(torch.bfloat16)
+    rng = np.random.Generator(np.random.PCG64(630))
+    p["wg.bias"] = rng.uniform(-1.0, 1.0, 12).astype(np.float32)
+    p["onorm_w"] = rng.uniform(0.5, 1.5, (12, 64)).astype(np.float32)
+    x = _bf16(S.layer_input(8, 2048, 768, seed=64)).astype(np.float32)
     m = build(cfg, p)
-    say("module bf16")
+    say("module bf16 end to end, B=8 T=2048")
+    xd = torch.from_numpy(x).cuda().to(torch.bfloat16)
     with torch.no_grad():
-        kz, qz, V, g = m._project(x, torch.bfloat16)
-        y = m(x)
-    f = [t.float().cpu().numpy() for t in (kz, qz, V, g)]
+        y = m(xd).float().cpu().numpy()
+        kz, qz, V, g = (t.float().cpu().numpy() for t in m._project(xd, torch.bfloat16))
+        hx = core.rms_norm(xd, m.norm.w, m.norm.eps, out_dtype=torch.bfloat16).double().cpu().numpy()
+    rows = [0, 7]
+    # the norm: the kernel sums the squares in another order, so a value may round the other way (two bf16 ulps)
+    hx_ref = _autocast_norm(x[rows], p["norm.w"])
+    dn = np.abs(hx[rows] - hx_ref)
+    assert np.all(dn <= 4.0 * half_ulp_bf16(hx_ref)), "the input norm is more than two bf16 ulps off"
+    say(f"  norm: {float(np.mean(dn > 0)):.2e} of the values differ from the float64 scale")
+    assert float(np.mean(dn > 0)) < 1e-3
+    # the projections of the kernel's normalised rows against float64 sums rounded to bf16
+    ref = _autocast_projections(hx[rows], p)
+    for name, got in (("wk", kz), ("wq", qz), ("wv", V), ("wg", g)):
+        want, terms = ref[name]
+        d = np.abs(got[rows].astype(np.float64) - want)
+        # one bf16 ulp, plus the float32 accumulation error of a 768-term sum (768 * 2^-24 of the |terms|)
+        lim = 2.0 * half_ulp_bf16(want) + 768 * 2.0 ** -24 * terms
+        if not np.all(d <= lim):
+            i = np.unravel_index(np.argmax(d - lim), d.shape)
+            raise AssertionError(f"{name}: {int((d > lim).sum())} values past the bound; worst at {i}: got "
+                                 f"{got[rows][i]!r} want {want[i]!r} terms {terms[i]!r}")
+        frac = float(np.mean(d > 0))
+        say(f"  {name}: {frac:.2e} of the values differ from the float64 sum rounded to bf16")
+        assert frac < 2e-3, f"{name}: {frac:.2e} of the values differ"
     po = dict(keys1=p["keys1"], keys2=p["keys2"], addr_b=p["addr_b"], log_scale=p["log_scale"],
-              decay=p["decays_fixed"], onorm_w=p["onorm_w"], gate_bias=p["wg.bias"])
-    check_core(*f, po, 8, dtype=torch.bfloat16, tol=2e-3)
+              decay=p["decays_fixed"], onorm_w=p["onorm_w"], gate_bias=np.zeros(12, np.float32))
+    siw, _, ww = gpu_address(kz, po, 8, dtype=torch.bfloat16, gate=g)
+    sir, _, wr = gpu_address(qz, po, 8, dtype=torch.bfloat16)
+    flips = check_picks(kz, po, 8, siw, ww, g) + check_picks(qz, po, 8, sir, wr)
+    say("picks that differ from the fp64 oracle (near-ties):", flips)
+    wo = _bf16(p["wo.weight"])
+    for b in rows:
+        r, _ = scan_from_picks(siw[b:b + 1], ww[b:b + 1], sir[b:b + 1], wr[b:b + 1], V[b:b + 1], p["decays_fixed"],
+                               12, "mean", True, p["onorm_w"], 1024)
+        assert_close(y[b:b + 1], _bf16(r) @ wo.T, 2e-3, bf16_out=True, msg=f"y, batch row {b}")
+
+
+def test_module_bf16_eval_equals_training_forward():
+    """The inference forward and the differentiable forward (bf16 autocast, x requiring grad) of one module give the
+    same bits: the same norm kernel, the same fused projection with the gate bias, the same core and wo."""
+    cfg = S.layer_cfg()
+    p = S.layer_params(cfg, seed=67)
+    p["wg.bias"] = np.random.Generator(np.random.PCG64(670)).uniform(-1.0, 1.0, 12).astype(np.float32)
+    m = build(cfg, p)
+    x = torch.from_numpy(S.layer_input(2, 512, 768, seed=671)).cuda().to(torch.bfloat16)
+    say("module eval vs training forward")
     with torch.no_grad():
-        from sdmchat_amd import core
-        r = core.core_forward(kz, qz, V, g, keys1=m.keys1, keys2=m.keys2, log_scale=m.log_scale, decay=m.decay(),
-                              addr_b=m.addr_b, onorm_w=m.onorm_w, gate_bias=m.wg.bias, k=8)
-    wo = m.wo.weight.detach().to(torch.bfloat16).double().cpu().numpy()
-    want_y = r.double().cpu().numpy() @ wo.T
-    assert_close(y.float().cpu().numpy(), want_y, 2e-3, bf16_out=True, msg="y = r wo^T")
+        y_eval = m(x)
+    xg = x.clone().requires_grad_(True)
+    with torch.enable_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y_train = m(xg)
+    assert y_train.dtype == y_eval.dtype == torch.bfloat16
+    assert torch.equal(y_train.detach(), y_eval), float((y_train.detach().float() - y_eval.float()).abs().max())
+
+
+def test_module_output_map_cache_follows_in_place_changes():
+    """An in-place change of wo alone (no_grad) reaches the next bf16 forward: doubling wo doubles y exactly."""
+    cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8)
+    m = build(cfg, S.layer_params(cfg, seed=69))
+    x = torch.randn(2, 40, 64, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        y1 = m(x)
+        m.wo.weight.mul_(2.0)
+        y2 = m(x)
+        m.wg.bias.add_(0.75)          # the gate bias lives in the fused projection: it must follow too
+        y3 = m(x)
+        m.wg.bias.sub_(0.75)
+        y4 = m(x)
+    assert torch.equal(y2, 2 * y1)
+    assert not torch.equal(y3, y2)
+    assert torch.equal(y4, y2)
 
 
 def test_zero_output_map_gives_exact_zero():

@@ -103,10 +103,7 @@ def test_onesdm_trained_sdm_arm_training_step_matches_the_oracle():
     mp, sp = [], []
     with torch.no_grad():
         for i, m in enumerate(model.mems):
-            hx = m.norm(ins[("m", i)]).float()
-            W = torch.cat([m.wk.weight, m.wq.weight, m.wv.weight, m.wg.weight], 0)
-            bias = torch.cat([m.wg.bias.new_zeros(2 * H * d_a + d), m.wg.bias])
-            proj = torch.nn.functional.linear(hx, W, bias)
+            proj = torch.cat(m._project_train(ins[("m", i)])[:2], -1)
             sw = core.address(proj[..., :H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
             sr = core.address(proj[..., H * d_a:2 * H * d_a], m.keys1, m.keys2, k, m.log_scale, addr_b=m.addr_b)[0]
             mp.append((sw.permute(0, 2, 1, 3).long().cpu(), sr.permute(0, 2, 1, 3).long().cpu()))
