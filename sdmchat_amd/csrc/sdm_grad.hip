@@ -1,5 +1,5 @@
-// sdm_rt_grad.inc -- the backward of the run-time SDM core (included at the end of sdm_rt.hip: one translation unit,
-// so the helpers above are shared).
+// sdm_grad.hip -- the backward of the run-time SDM core (sdm_rt_forward_train, sdm_rt_backward) and of TrainedSdm's
+// table layer (sdm_rt_table_backward).
 //
 // The gradient of RunTimeSdm.forward (track4_onesdm_models.py:195-274, the part between the projections and wo) for
 // picks held fixed (topk and the slot ids carry no gradient).  With K[t][s] = lam^(t-1-s) sum_ij wr[t,i] ww[s,j]
@@ -19,7 +19,14 @@
 // lam * dL/dlam (the gradient with respect to log lam) needs no extra pass: sum_{t,s} (t-1-s) K[t][s] X[t][s]
 // = sum_t t P_t - sum_s (s+1) Q_s with P_t = sum_i wr[t,i] dwr[t,i] and Q_s = sum_j ww[s,j] dww[s,j].
 
-namespace {
+#include <hipcub/hipcub.hpp>
+
+#include "sdm_scan.h"
+
+namespace sdmrt {
+
+constexpr int kGradScanThreads = 512;   // grad scans: 64 positions x 8 lanes
+
 
 // ---------------------------------------------------------------------------------------------------------------
 // read-out backward: out-norm (finish :243-246) and mean read, per (token, head)
@@ -421,7 +428,7 @@ __device__ __forceinline__ unsigned long long group_or8(unsigned long long v) {
 //           write records g + 64 k: each written slot's kept writers' faded values / mu, added to the slot's row in
 //           one pass (one owner per row: no atomics), lane l8 the count of record l8 + 8 b
 template <int CW, int KP, bool REV, typename WT, typename RT>
-__global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a) {
+__global__ void __launch_bounds__(kGradScanThreads) grad_scan_kernel(GradScanArgs a) {
   constexpr int CPL = CW / 8;
   extern __shared__ __attribute__((aligned(16))) unsigned char glds[];
   const int M = a.M;
@@ -437,7 +444,7 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
   unsigned char* s_rm = glds + lay.rm;
   unsigned char* s_ext = glds + lay.ext;
   constexpr int XS = grad_ext_stage(KP);
-  constexpr int NX = (XS / 16 + kScanThreads - 1) / kScanThreads;   // staged chain pieces per thread
+  constexpr int NX = (XS / 16 + kGradScanThreads - 1) / kGradScanThreads;   // staged chain pieces per thread
 
   const int cg = blockIdx.x;
   const int h = blockIdx.y;
@@ -453,8 +460,8 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
   const float lam = a.decay[h];
   float* dot_out = a.dot_out + (static_cast<int64_t>(cg) * a.B * a.H + bh) * T * KP;
 
-  for (int i = tid; i < (M + 1) * CW; i += kScanThreads) A[i] = 0.f;
-  for (int i = tid; i <= M; i += kScanThreads) cnt[i] = 0.f;
+  for (int i = tid; i < (M + 1) * CW; i += kGradScanThreads) A[i] = 0.f;
+  for (int i = tid; i <= M; i += kGradScanThreads) cnt[i] = 0.f;
   if (tid <= kChunk) {
     float v = 1.f;   // lam^tid by repeated multiplication (exact for lam = 0 and lam = 1)
     for (int e = 0; e < tid; ++e) v *= lam;
@@ -523,7 +530,7 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
     const uint4* xs = reinterpret_cast<const uint4*>(cp + 16 + 8 * kChunk * KP);
 #pragma unroll
     for (int k = 0; k < NX; ++k) {
-      const int piece = tid + k * kScanThreads;
+      const int piece = tid + k * kGradScanThreads;
       x.xp[k] = piece < XS / 16 ? xs[piece] : make_uint4(0u, 0u, 0u, 0u);
     }
   };
@@ -552,7 +559,7 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
     if (l8 == 0) s_wc[g] = cur.wc;
 #pragma unroll
     for (int k = 0; k < NX; ++k) {
-      const int piece = tid + k * kScanThreads;
+      const int piece = tid + k * kGradScanThreads;
       if (piece < XS / 16) reinterpret_cast<uint4*>(s_ext)[piece] = cur.xp[k];
     }
     {
@@ -576,7 +583,7 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
 #pragma unroll
     for (int k = 0; k < CPL; ++k) rv[k] = valid ? to_f32(cur.rv[k]) : 0.f;
     const float rcf = cur.rcf;
-    for (int i = tid; i < M; i += kScanThreads) wmask[i] = 0ull;
+    for (int i = tid; i < M; i += kGradScanThreads) wmask[i] = 0ull;
     In nxt;
     const bool more = c + 1 < a.n_chunks;
     if (more) fetch(c + 1, nxt);   // in flight across the barriers below (they order LDS only)
@@ -699,13 +706,13 @@ __global__ void __launch_bounds__(kScanThreads) grad_scan_kernel(GradScanArgs a)
     // write: fade (an emptied slab for a chunk with a reset), then the kept writers of each slot
     float mu_new = mu * pw[L];
     if (rmask) {
-      for (int i = tid; i < M * CW; i += kScanThreads) A[i] = 0.f;
-      for (int i = tid; i < M; i += kScanThreads) cnt[i] = 0.f;
+      for (int i = tid; i < M * CW; i += kGradScanThreads) A[i] = 0.f;
+      for (int i = tid; i < M; i += kGradScanThreads) cnt[i] = 0.f;
       mu_new = 1.f;
       lds_barrier();
     } else if (!(mu_new >= kMuFloor)) {
-      for (int i = tid; i < M * CW; i += kScanThreads) A[i] *= mu_new;
-      for (int i = tid; i < M; i += kScanThreads) cnt[i] *= mu_new;
+      for (int i = tid; i < M * CW; i += kGradScanThreads) A[i] *= mu_new;
+      for (int i = tid; i < M; i += kGradScanThreads) cnt[i] *= mu_new;
       mu_new = 1.f;
       lds_barrier();
     }
@@ -1377,7 +1384,7 @@ int launch_grad_scan_t(const GradPlan& g, const GradScanArgs& a, hipStream_t st)
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
   if (attr != hipSuccess) return set_err(SDM_RT_ELAUNCH, "grad scan: cannot enable %zu bytes of LDS", kLdsBytes);
   dim3 grid(g.n_cg, g.p.H, g.p.B);
-  hipLaunchKernelGGL((grad_scan_kernel<CW, KP, REV, WT, RT>), grid, dim3(kScanThreads), lds, st, a);
+  hipLaunchKernelGGL((grad_scan_kernel<CW, KP, REV, WT, RT>), grid, dim3(kGradScanThreads), lds, st, a);
   return check_launch("grad scan");
 }
 
@@ -1477,7 +1484,9 @@ int make_table_plan(const sdm_rt_dims* d, TablePlan* g) {
   return SDM_RT_OK;
 }
 
-}  // namespace
+}  // namespace sdmrt
+
+using namespace sdmrt;
 
 // ---------------------------------------------------------------------------------------------------------------
 // C ABI of the backward
@@ -1529,61 +1538,26 @@ int sdm_rt_forward_train(const sdm_rt_dims* dims, const sdm_rt_params* params, c
   aa.slot_out2 = saved->slots_r;
   aa.w_out2 = saved->weights_r;
   aa.s_out2 = saved->scores_r;
-  rc = in_dtype == SDM_RT_BF16 ? by_half<AddressLaunch, bf16_t>(p.half, p, aa, st)
-                               : by_half<AddressLaunch, float>(p.half, p, aa, st);
+  rc = launch_address(p, aa, in_dtype, st);
   if (rc) return rc;
 
-  char* ws = static_cast<char*>(workspace);
-  int32_t* sizes = reinterpret_cast<int32_t*>(ws + p.off_sizes);
-  unsigned char* plans = reinterpret_cast<unsigned char*>(ws + p.off_plans);
-  PlanArgs pa{};
-  pa.g = addr_geom(p, params);
-  pa.kz = kz;
-  pa.kz_stride = kz_row_stride;
-  pa.qz = qz;
-  pa.qz_stride = qz_row_stride;
-  pa.gl = gl;
-  pa.g_stride = gate_row_stride;
-  pa.decay = params->decay;
-  pa.reset = reset;
-  pa.plans = plans;
-  pa.sizes = sizes;
-  pa.B = p.B;
-  pa.T = p.T;
-  pa.M = p.M;
-  pa.n_chunks = p.n_chunks;
-  rc = in_dtype == SDM_RT_BF16 ? by_half<PlanLaunch, bf16_t>(p.half, p, pa, st)
-                               : by_half<PlanLaunch, float>(p.half, p, pa, st);
-  if (rc) return rc;
-  ScanArgs s{};
-  s.plans = plans;
-  s.sizes = sizes;
-  s.v = v;
-  s.v_stride = v_row_stride;
-  s.decay = params->decay;
-  s.B = p.B;
-  s.T = p.T;
-  s.H = p.H;
-  s.dh = p.dh;
-  s.M = p.M;
-  s.n_chunks = p.n_chunks;
-  s.read_mean = dims->read_mean;
-  s.read_eps = dims->read_eps;
-  s.r_out = saved->read;
-  s.r_stride = wv;
-  s.den_out = dims->read_mean ? saved->den : nullptr;
-  if ((rc = launch_scan(p, s, in_dtype, SDM_RT_F32, st))) return rc;
-  const int64_t rows = static_cast<int64_t>(p.B) * p.T * p.H;
-  const unsigned blocks = static_cast<unsigned>((rows + 31) / 32);
-  const float* onw = dims->out_norm ? params->onorm_w : nullptr;
-  if (out_dtype == SDM_RT_BF16) {
-    hipLaunchKernelGGL((finish_kernel<bf16_t>), dim3(blocks), dim3(256), 0, st, saved->read, wv,
-                       static_cast<bf16_t*>(r_out), out_row_stride, onw, rows, p.H, p.dh, dims->out_norm_eps);
-  } else {
-    hipLaunchKernelGGL((finish_kernel<float>), dim3(blocks), dim3(256), 0, st, saved->read, wv,
-                       static_cast<float*>(r_out), out_row_stride, onw, rows, p.H, p.dh, dims->out_norm_eps);
-  }
-  return check_launch("finish");
+  CoreIO io{};
+  io.kz = kz;
+  io.kz_stride = kz_row_stride;
+  io.qz = qz;
+  io.qz_stride = qz_row_stride;
+  io.v = v;
+  io.v_stride = v_row_stride;
+  io.gate_logits = gl;
+  io.g_stride = gate_row_stride;
+  io.in_dtype = in_dtype;
+  io.reset = reset;
+  io.r_out = r_out;
+  io.r_stride = out_row_stride;
+  io.out_dtype = out_dtype;
+  io.read_out = saved->read;
+  io.den_out = dims->read_mean ? saved->den : nullptr;
+  return run_core(p, dims, params, io, workspace, st);
 }
 
 size_t sdm_rt_backward_workspace_bytes(const sdm_rt_dims* dims) {

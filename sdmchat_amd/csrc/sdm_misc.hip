@@ -1,0 +1,191 @@
+// sdm_misc.hip -- the input norm (sdm_rt_rms_norm), the table read of TrainedSdm (sdm_rt_table_read) and the
+// addressing entry point (sdm_rt_address).
+#include "sdm_common.h"
+
+namespace sdmrt {
+
+// rms_norm: one wave per row; lanes take 8 consecutive values at a time
+template <typename InT, typename OutT>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x, int64_t x_stride,
+                                                       OutT* __restrict__ out, int64_t out_stride,
+                                                       const float* __restrict__ w, int64_t rows, int d, float eps) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;   // whole waves
+  const InT* src = x + row * x_stride;
+  constexpr int kMax = 4;    // 8 * 64 * 4 = 2048 values per row in registers
+  float v[kMax][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMax; ++k) {
+    const int c = 8 * (lane + 64 * k);
+    if (c < d) {
+      load_vals<8, InT>(src + c, v[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  OutT* dst = out + row * out_stride;
+#pragma unroll
+  for (int k = 0; k < kMax; ++k) {
+    const int c = 8 * (lane + 64 * k);
+    if (c < d) {
+      float wv[8];
+      load_vals<8, float>(w + c, wv);
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = to_f32(from_f32<InT>(v[k][e] * r)) * wv[e];   // .to(x.dtype) * w
+      store_vals<8, OutT>(dst + c, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// table read: the weighted sum of the picked rows of per-head value tables (TrainedSdm.forward's embedding_bag,
+// track4_onesdm_models.py:448-455): out[n][h * dh + c] = sum_j w[n][h][j] * values[h][slot[n][h][j]][c] in float32,
+// picks in order.  One wave per (token, head); lane l takes columns 4l, 4l + 256, ... (dh a multiple of 4).
+template <int KP, typename VT, typename OutT>
+__global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restrict__ slots,
+                                                         const float* __restrict__ wts,
+                                                         const VT* __restrict__ values, OutT* __restrict__ out,
+                                                         int64_t out_stride, int B, int T, int H, int M, int dh,
+                                                         int kk) {
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave >= static_cast<int64_t>(B) * T * H) return;   // whole waves
+  const int64_t n = wave / H;
+  const int h = static_cast<int>(wave - n * H);
+  const int b = static_cast<int>(n / T);
+  const int t = static_cast<int>(n - static_cast<int64_t>(b) * T);
+  const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
+  int sl[KP];
+  float w[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    sl[j] = min(max(slots[pb + j], 0), M - 1);   // pads (-1) and stray ids stay inside the table
+    w[j] = j < kk ? wts[pb + j] : 0.f;
+  }
+  const VT* tab = values + static_cast<int64_t>(h) * M * dh;
+  for (int c0 = 4 * lane; c0 < dh; c0 += 256) {
+    float v[KP][4];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      if (j < kk) {
+        load_vals<4, VT>(tab + static_cast<int64_t>(sl[j]) * dh + c0, v[j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[j][e] = 0.f;
+      }
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(w[j], v[j][e], acc[e]);
+    }
+    store_vals<4, OutT>(out + n * out_stride + static_cast<int64_t>(h) * dh + c0, acc);
+  }
+}
+
+}  // namespace sdmrt
+
+using namespace sdmrt;
+
+extern "C" {
+
+int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, int64_t rows, int32_t d,
+                    const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                    void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (rows < 0 || d < 1) return set_err(SDM_RT_EINVAL, "rows must be >= 0 and d >= 1");
+  if (d % 8 != 0 || d > 2048) return set_err(SDM_RT_EUNSUPPORTED, "d = %d must be a multiple of 8 up to 2048", d);
+  if (rows == 0) return SDM_RT_OK;
+  if (!x || !w || !out) return set_err(SDM_RT_EINVAL, "x, w and out must not be NULL");
+  if (x_row_stride < d || out_row_stride < d) return set_err(SDM_RT_EINVAL, "row strides must be >= d");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+#define SDM_RT_NORM(IT, OT)                                                                                     \
+  hipLaunchKernelGGL((rms_norm_kernel<IT, OT>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x),      \
+                     x_row_stride, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  if (in_dtype == SDM_RT_BF16) {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(bf16_t, bf16_t);
+    else SDM_RT_NORM(bf16_t, float);
+  } else {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(float, bf16_t);
+    else SDM_RT_NORM(float, float);
+  }
+#undef SDM_RT_NORM
+  return check_launch("rms_norm");
+}
+int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* z, int64_t z_row_stride,
+                   const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype, int32_t* slot_out,
+                   float* score_out, float* weight_out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p, false);
+  if (rc) return rc;
+  if ((rc = check_params(params, false, false))) return rc;
+  if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
+  if (p.B == 0 || p.T == 0) return SDM_RT_OK;
+  if (!z || !slot_out) return set_err(SDM_RT_EINVAL, "z and slot_out must not be NULL");
+  if (z_row_stride < static_cast<int64_t>(p.H) * p.d_a)
+    return set_err(SDM_RT_EINVAL, "z_row_stride %lld < heads * addr_dim", (long long)z_row_stride);
+  if (gate_logits && gate_row_stride < p.H)
+    return set_err(SDM_RT_EINVAL, "gate_row_stride %lld < heads", (long long)gate_row_stride);
+  (void)workspace;   // the addressing alone needs no workspace
+  (void)workspace_bytes;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  AddrArgs a{};
+  a.g = addr_geom(p, params);
+  a.z = z;
+  a.z_stride = z_row_stride;
+  a.gl = gate_logits;
+  a.g_stride = gate_row_stride;
+  a.B = p.B;
+  a.T = p.T;
+  a.pitch = p.pitch;
+  a.slot_out = slot_out;
+  a.w_out = weight_out;
+  a.s_out = score_out;
+  return launch_address(p, a, in_dtype, st);
+}
+
+int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float* weights, const void* values,
+                      sdm_rt_dtype values_dtype, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                      void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p, false);
+  if (rc) return rc;
+  if ((rc = check_dtype(values_dtype, "values_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (p.dh < 4 || p.dh % 4 != 0) return set_err(SDM_RT_EUNSUPPORTED, "head_dim %d must be a positive multiple of 4", p.dh);
+  if (p.B == 0 || p.T == 0) return SDM_RT_OK;
+  if (!slots || !weights || !values || !out) return set_err(SDM_RT_EINVAL, "slots, weights, values and out must not be NULL");
+  if (out_row_stride < static_cast<int64_t>(p.H) * p.dh)
+    return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t waves = static_cast<int64_t>(p.B) * p.T * p.H;
+  const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+#define SDM_RT_TABLE(KP, VT, OT)                                                                                   \
+  hipLaunchKernelGGL((table_read_kernel<KP, VT, OT>), dim3(blocks), dim3(256), 0, st, slots, weights,             \
+                     static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, p.H, p.M, p.dh, \
+                     p.kk)
+#define SDM_RT_TABLE_KP(VT, OT) \
+  if (p.pitch == 8) SDM_RT_TABLE(8, VT, OT); else SDM_RT_TABLE(16, VT, OT)
+  if (values_dtype == SDM_RT_BF16) {
+    if (out_dtype == SDM_RT_BF16) { SDM_RT_TABLE_KP(bf16_t, bf16_t); } else { SDM_RT_TABLE_KP(bf16_t, float); }
+  } else {
+    if (out_dtype == SDM_RT_BF16) { SDM_RT_TABLE_KP(float, bf16_t); } else { SDM_RT_TABLE_KP(float, float); }
+  }
+#undef SDM_RT_TABLE_KP
+#undef SDM_RT_TABLE
+  return check_launch("table_read");
+}
+}  // extern "C"
