@@ -22,9 +22,11 @@ cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle
 dense chunk algorithm) on the same workload, all host cores, one warm call then best of three.
 
 decode: the decode step (sdm_rt_decode_step, one token for each of 64 streams, 12 heads, float32 state carried in
-place) timed as a HIP graph of 64 steps replayed 513 times, so the state runs through 32,832 positions; us_per_step
-= replay time / 64 (device time, no host launch cost), reported overall (median) and at positions 0, 1,024, 8,192
-and 32,768 to show that the cost of a step does not grow with the position.  --no-decode skips it.
+place) timed as a HIP graph of 64 steps replayed 513 times, so the state runs through 32,832 positions; before every
+replay the graph's input rows are refilled with the projections of fresh random tokens, so every step addresses new
+rows.  us_per_step = replay time / 64 (device time, no host launch cost), reported overall (median) and at positions
+0, 1,024, 8,192 and 32,768 to show that the cost of a step does not grow with the position, and again with head 0's
+fade set to 0 (us_per_step_head0_fade0).  --no-decode skips it.
 
 model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12 layers of d=768 with this mixer
 (12 heads, M=1,024, k=8): "swiglu" = each layer's per-token step a SwiGLU of hidden 2,048 (the survey's config 3),
@@ -99,45 +101,62 @@ def cpu_baseline():
 
 
 def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
-    """Device time of sdm_rt_decode_step for `streams` streams of the layer, by position (see the module doc)."""
+    """Device time of sdm_rt_decode_step for `streams` streams of the layer, by position (see the module doc): a HIP
+    graph of `graph_steps` steps over static input rows, refilled with fresh random tokens' projections before every
+    replay, so every step addresses new rows.  Measured with the layer's fades and again with head 0's fade set to
+    0 (its state holds only the last step's writes)."""
     import numpy as np
     import torch
 
     from sdmchat_amd import core
 
-    gen = torch.Generator(device="cpu").manual_seed(7)
-    xt = torch.randn(streams, 1, D, generator=gen).to(dev).to(torch.bfloat16)
-    kz, qz, V, g = m._project(xt, torch.bfloat16)
-    kz, qz, V, g = kz[:, 0], qz[:, 0], V[:, 0], g[:, 0]
-    st = m.decode_state(streams, dev)
-    prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, m.decay(), m.onorm_w, None)
-    ws = core.CoreWorkspace()
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def fresh():
+        x = torch.randn(graph_steps * streams, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+        return [t[:, 0].reshape(graph_steps, streams, -1) for t in m._project(x, torch.bfloat16)]
+
+    bufs = [t.clone() for t in fresh()]
     out = torch.empty(streams, D, dtype=torch.bfloat16, device=dev)
+    ws = core.CoreWorkspace()
+    res = {}
+    for name, zero_head in (("layer fades", False), ("head 0 fade 0", True)):
+        decay = m.decay().detach().clone()
+        if zero_head:
+            decay[0] = 0.0
+        prm = core._params(dev, m.keys1, m.keys2, m.addr_b, m.log_scale, decay, m.onorm_w, None)
+        st = m.decode_state(streams, dev)
 
-    def step():
-        core.decode_step(kz, qz, V, g, st, keys1=m.keys1, keys2=m.keys2, log_scale=m.log_scale, decay=m.decay(),
-                         k=K, out=out, workspace=ws, params=prm)
+        def step(t):
+            core.decode_step(bufs[0][t], bufs[1][t], bufs[2][t], bufs[3][t], st, keys1=m.keys1, keys2=m.keys2,
+                             log_scale=m.log_scale, decay=decay, k=K, out=out, workspace=ws, params=prm)
 
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(graph_steps):
-            step()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
-    for e0, e1 in evs:
-        e0.record()
-        graph.replay()
-        e1.record()
-    torch.cuda.synchronize()
-    us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
-    by_pos = {str(pos): round(float(us[pos // graph_steps]), 2) for pos in (0, 1024, 8192, 32768)}
-    log(f"decode: {np.median(us):.2f} us per step (median over {replays} replays), by position {by_pos}")
-    return {"workload": f"RunTimeSdm decode step: {streams} streams x {H} heads, one token each, float32 state",
-            "us_per_step": round(float(np.median(us)), 2), "us_per_step_by_position": by_pos,
-            "steps_timed": replays * graph_steps, "method": f"HIP graph of {graph_steps} steps, replay time / "
-            f"{graph_steps}"}
+        for t in range(3):
+            step(t)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for t in range(graph_steps):
+                step(t)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+        for e0, e1 in evs:
+            for b_, f_ in zip(bufs, fresh()):
+                b_.copy_(f_)
+            e0.record()
+            graph.replay()
+            e1.record()
+        torch.cuda.synchronize()
+        us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
+        by_pos = {str(pos): round(float(us[pos // graph_steps]), 2) for pos in (0, 1024, 8192, 32768)}
+        log(f"decode ({name}): {np.median(us):.2f} us per step (median over {replays} replays), by position {by_pos}")
+        res[name] = (round(float(np.median(us)), 2), by_pos)
+        del graph
+    return {"workload": f"RunTimeSdm decode step: {streams} streams x {H} heads, one fresh random token each per "
+                        f"step, float32 state", "us_per_step": res["layer fades"][0],
+            "us_per_step_by_position": res["layer fades"][1], "us_per_step_head0_fade0": res["head 0 fade 0"][0],
+            "steps_timed": replays * graph_steps,
+            "method": f"HIP graph of {graph_steps} steps, replay time / {graph_steps}; inputs refilled with new "
+                      "random tokens' projections between replays"}
 
 
 def model_bench(dev, vocab=32768, layers=12, mlp_f=2048):

@@ -122,7 +122,8 @@ size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);
 
 /* One decode step: one token for each of B = dims->batch streams (dims->seq_len must be 1), with the recurrence of
  * RunTimeSdm.forward_sequential (track4_onesdm_models.py:276-300): optional reset, read, then faded write.  The
- * reference keeps no state across calls (it only exposes last_state, :299); this entry point carries it.
+ * reference keeps no state across calls (it only exposes last_state, :299); this entry point carries it.  Shapes
+ * whose addressing runs on the matrix cores (addr_dim 16, 32 or 64 and n_sub <= 32) take one kernel launch.
  *   kz, qz, v, gate_logits   one row per stream, as in sdm_rt_forward
  *   reset        [B] uint8 or NULL: 1 empties that stream's memory before it reads (a BOS, :287-289)
  *   state_mem    [B][H][M][dh] float32, state_cnt [B][H][M] float32, state_scale [B][H] float32, read and
@@ -130,14 +131,18 @@ size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);
  *                state_scale * state_cnt.  A new stream starts from mem = cnt = 0, scale = 1; a state from
  *                sdm_rt_forward (state_out_*) continues with scale = 1.  Keeping the scale apart makes the fade
  *                O(1) per step: the cost of a step does not grow with the position (the slab is rescaled once
- *                when the scale falls below 2^-60, and on every step of a head whose decay is 0).
+ *                when the scale falls below 2^-60).
+ *   state_last   [B][H][pitch] int32 (pitch = sdm_rt_pick_pitch(dims)) or NULL, updated in place: the slots of
+ *                the last step's writes where that step left nothing else (decay 0), else -2 in entry 0.  With it
+ *                a head of decay 0 zeroes only those rows instead of its whole slab.  A new stream starts with
+ *                every entry -1 (an empty slab), a state from sdm_rt_forward with -2 (unknown).
  *   r_out        one row per stream of H * dh read-outs (after the mean read and the output norm, before wo),
  *                dtype out_dtype */
 int sdm_rt_decode_step(const sdm_rt_dims* dims, const sdm_rt_params* params,
                        const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
                        const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
                        sdm_rt_dtype in_dtype, const uint8_t* reset,
-                       float* state_mem, float* state_cnt, float* state_scale,
+                       float* state_mem, float* state_cnt, float* state_scale, int32_t* state_last,
                        void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
 

@@ -237,32 +237,53 @@ def table_read(slots, weights, values, k, out_dtype=torch.float32, out=None):
 class DecodeState:
     """State of B decode streams: the true memory is ``scale * mem`` and the true counts ``scale * cnt``
     (mem [B, H, M, dh], cnt [B, H, M], scale [B, H], float32, on the device).  Keeping the scale apart lets a decode
-    step fade the whole state in O(1)."""
+    step fade the whole state in O(1).  ``last`` [B, H, pitch] int32 (or None) holds the slots of the last step's
+    writes where that step left nothing else (a head of decay 0), so the next step zeroes only those rows: -1 marks
+    an unused entry, -2 in entry 0 a slab whose other rows are unknown."""
 
-    def __init__(self, mem, cnt, scale):
+    def __init__(self, mem, cnt, scale, last=None):
         B, H, M, dh = mem.shape
         if tuple(cnt.shape) != (B, H, M) or tuple(scale.shape) != (B, H):
             raise ValueError("DecodeState needs mem [B, H, M, dh], cnt [B, H, M] and scale [B, H]")
         for t in (mem, cnt, scale):
             if t.dtype != torch.float32 or not t.is_contiguous() or t.device != mem.device:
                 raise ValueError("DecodeState tensors must be contiguous float32 on one device")
-        self.mem, self.cnt, self.scale = mem, cnt, scale
+        if last is not None and (last.dtype != torch.int32 or last.dim() != 3 or tuple(last.shape[:2]) != (B, H)
+                                 or not last.is_contiguous() or last.device != mem.device):
+            raise ValueError("DecodeState.last must be contiguous int32 [B, H, pitch] on the state's device")
+        self.mem, self.cnt, self.scale, self.last = mem, cnt, scale, last
 
     @classmethod
-    def empty(cls, B, H, M, dh, device):
+    def empty(cls, B, H, M, dh, device, pitch=None):
+        last = None if pitch is None else torch.full((B, H, pitch), -1, dtype=torch.int32, device=device)
         return cls(torch.zeros(B, H, M, dh, device=device), torch.zeros(B, H, M, device=device),
-                   torch.ones(B, H, device=device))
+                   torch.ones(B, H, device=device), last)
 
     @classmethod
-    def from_state(cls, mem, cnt):
+    def from_state(cls, mem, cnt, pitch=None):
         """Continue from a true state, e.g. the (mem, cnt) of core_forward(..., want_state=True)."""
         mem = mem.detach().to(torch.float32).contiguous().clone()
         cnt = cnt.detach().to(torch.float32).contiguous().clone()
-        return cls(mem, cnt, torch.ones(mem.shape[:2], device=mem.device))
+        last = None
+        if pitch is not None:
+            last = torch.full(mem.shape[:2] + (pitch,), -1, dtype=torch.int32, device=mem.device)
+            last[..., 0] = -2
+        return cls(mem, cnt, torch.ones(mem.shape[:2], device=mem.device), last)
 
     def state(self):
         """The true (mem, cnt), as forward's last_state holds them (a format conversion, not a decode step)."""
         return self.mem * self.scale[..., None, None], self.cnt * self.scale[..., None]
+
+    def nbytes(self):
+        """Device bytes the state holds."""
+        return sum(t.numel() * t.element_size() for t in (self.mem, self.cnt, self.scale, self.last) if t is not None)
+
+
+def pick_pitch(k, n_sub):
+    """Entries per address of the pick arrays (sdm_rt_pick_pitch): the kept picks rounded up to 8."""
+    c1 = min(k, n_sub)
+    kk = min(k, c1 * c1)
+    return (kk + 7) // 8 * 8
 
 
 def decode_step(kz, qz, v, gate_logits, state, *, keys1, keys2, log_scale, decay, addr_b=None, onorm_w=None,
@@ -291,6 +312,8 @@ def decode_step(kz, qz, v, gate_logits, state, *, keys1, keys2, log_scale, decay
     gs = 0 if gate_logits is None else _rows2(gate_logits, "gate_logits", B, H)
     if tuple(state.mem.shape) != (B, H, M, dh):
         raise ValueError(f"state holds {tuple(state.mem.shape)}, expected [B={B}, H={H}, M={M}, dh={dh}]")
+    if state.last is not None and state.last.shape[2] != pick_pitch(k, n_sub):
+        raise ValueError(f"state.last has pitch {state.last.shape[2]}, expected {pick_pitch(k, n_sub)}")
     dev = v.device
     if params is None:
         params = _params(dev, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)
@@ -309,7 +332,7 @@ def decode_step(kz, qz, v, gate_logits, state, *, keys1, keys2, log_scale, decay
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = lib.sdm_rt_decode_step(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
                                 _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(state.mem), _ptr(state.cnt),
-                                _ptr(state.scale), _ptr(out), ostride, _DT[out_dtype], _ptr(ws), ws.numel(),
+                                _ptr(state.scale), _ptr(state.last), _ptr(out), ostride, _DT[out_dtype], _ptr(ws), ws.numel(),
                                 ctypes.c_void_p(stream))
     _lib.check(rc, lib)
     return out

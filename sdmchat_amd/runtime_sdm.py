@@ -246,7 +246,7 @@ class RunTimeSdm(nn.Module):
     def decode_state(self, batch, device=None):
         """An empty state for ``batch`` decode streams (a core.DecodeState)."""
         device = device if device is not None else self.keys1.device
-        return core.DecodeState.empty(batch, self.h, self.M, self.dh, device)
+        return core.DecodeState.empty(batch, self.h, self.M, self.dh, device, core.pick_pitch(self.k, self.n_sub))
 
     def step(self, x, state, reset=None):
         """One token for each of B streams: x [B, d] (or [B, 1, d]) -> y of the same shape, with the recurrence of

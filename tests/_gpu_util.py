@@ -220,16 +220,17 @@ def check_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, tol=1e-5
 
 
 def gpu_decode(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, read_mode="mean", out_norm=True,
-               reset=None, state=None):
+               reset=None, state=None, last=True):
     """Run sdm_rt_decode_step once per position (B streams, T steps); returns r (numpy float32, (B, T, H*dh)) and
-    the final DecodeState.  reset: (B, T) bool or None; state: a DecodeState to continue from, or None (empty)."""
+    the final DecodeState.  reset: (B, T) bool or None; state: a DecodeState to continue from, or None (empty, with
+    the last-write slots when ``last``)."""
     B, T = V.shape[0], V.shape[1]
     H, n_sub, half = p["keys1"].shape
     dh = V.shape[2] // H
     tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
     kz_d, qz_d, V_d, g_d = (to_dev(x, dtype) for x in (kz, qz, V, g))
     if state is None:
-        state = core.DecodeState.empty(B, H, n_sub * n_sub, dh, "cuda")
+        state = core.DecodeState.empty(B, H, n_sub * n_sub, dh, "cuda", core.pick_pitch(k, n_sub) if last else None)
     rs = None if reset is None else torch.from_numpy(np.asarray(reset, bool)).cuda()
     ws = core.CoreWorkspace()
     outs = []

@@ -33,11 +33,14 @@ def _oracle_read(kz, qz, V, g, p, k, reset=None, read_mode="mean", out_norm=True
     return r.transpose(0, 2, 1, 3).reshape(B, T, H * dh), mem, cnt
 
 
-def test_decode_matches_oracle_and_forward_fp32():
+@pytest.mark.parametrize("d_a,last", [(16, True), (16, False), (12, True)])
+def test_decode_matches_oracle_and_forward_fp32(d_a, last):
+    """d_a 16: one launch (addressing on the matrix cores); d_a 12: an addressing launch, then the step.  last:
+    with and without the last-write slots (a head of decay 0 zeroes those rows, or its whole slab)."""
     decays = (0.0, 1.0, 0.5, 0.97)
-    kz, qz, V, g, p = core_inputs(3, 150, 4, 16, 16, 8, seed=71, decays=decays, addr_bias=0.3)
-    say("decode fp32", V.shape)
-    r_dec, st = gpu_decode(kz, qz, V, g, p, 8)
+    kz, qz, V, g, p = core_inputs(3, 150, 4, 16, d_a, 8, seed=71, decays=decays, addr_bias=0.3)
+    say("decode fp32", V.shape, d_a, last)
+    r_dec, st = gpu_decode(kz, qz, V, g, p, 8, last=last)
     r64, m64, c64 = _oracle_read(kz, qz, V, g, p, 8)
     np.testing.assert_allclose(r_dec, r64, atol=1e-5, rtol=1e-5)
     mem, cnt = (t.cpu().numpy() for t in st.state())
@@ -79,6 +82,21 @@ def test_decode_resets():
     np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
 
 
+def test_decode_zero_fade_with_resets():
+    """Heads of decay 0 (only the last step's writes remain: those rows are zeroed, not the slab) across resets."""
+    kz, qz, V, g, p = core_inputs(3, 80, 4, 16, 16, 8, seed=81, decays=(0.0, 0.0, 1.0, 0.5))
+    reset = np.zeros((3, 80), bool)
+    reset[0, 0] = reset[0, 33] = reset[1, 1] = reset[2, 79] = True
+    r_dec, st = gpu_decode(kz, qz, V, g, p, 8, reset=reset)
+    r64, m64, c64 = _oracle_read(kz, qz, V, g, p, 8, reset=reset)
+    np.testing.assert_allclose(r_dec, r64, atol=1e-5, rtol=1e-5)
+    mem, cnt = (t.cpu().numpy() for t in st.state())
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+    last = st.last.cpu().numpy()
+    assert (last[:, :2, 0] >= 0).all() and (last[:, 2:, 0] == -2).all()   # decay-0 heads keep their write slots
+
+
 def test_decode_small_fades_rescale_the_state():
     """Fades 0 and 0.05-0.3 push the state scale below 2^-60 within a few dozen steps (every step for 0)."""
     kz, qz, V, g, p = core_inputs(2, 120, 4, 16, 16, 8, seed=75, decays=(0.0, 0.05, 0.3, 1.0))
@@ -95,7 +113,7 @@ def test_decode_continues_a_forward_state():
     r_all, (m_all, c_all) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
     cut = 100
     _, (m1, c1) = gpu_core(kz[:, :cut], qz[:, :cut], V[:, :cut], g[:, :cut], p, 8, want_state=True)
-    st = core.DecodeState.from_state(torch.from_numpy(m1).cuda(), torch.from_numpy(c1).cuda())
+    st = core.DecodeState.from_state(torch.from_numpy(m1).cuda(), torch.from_numpy(c1).cuda(), core.pick_pitch(8, 16))
     r2, st = gpu_decode(kz[:, cut:], qz[:, cut:], V[:, cut:], g[:, cut:], p, 8, state=st)
     np.testing.assert_allclose(r2, r_all[:, cut:], atol=1e-5, rtol=1e-5)
     mem, cnt = (t.cpu().numpy() for t in st.state())
@@ -134,9 +152,9 @@ def test_decode_graph_replays_match_eager():
         core.decode_step(kz_d, qz_d, V_d, g_d, st, keys1=tp["keys1"], keys2=tp["keys2"], log_scale=tp["log_scale"],
                          decay=tp["decay"], k=8, out=out, workspace=ws, params=prm)
 
-    eager, ge = core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda")
-    graphed, gg = core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda")
-    step(core.DecodeState.empty(4, 4, 64, 16, "cuda"), torch.empty(4, 64, device="cuda"))   # sizes the workspace
+    eager, ge = core.DecodeState.empty(4, 4, 64, 16, "cuda", 8), torch.empty(4, 64, device="cuda")
+    graphed, gg = core.DecodeState.empty(4, 4, 64, 16, "cuda", 8), torch.empty(4, 64, device="cuda")
+    step(core.DecodeState.empty(4, 4, 64, 16, "cuda", 8), torch.empty(4, 64, device="cuda"))   # sizes the workspace
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -151,5 +169,5 @@ def test_decode_graph_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(gg, ge), f"replay {rep}: read-out differs"
         assert torch.equal(graphed.mem, eager.mem) and torch.equal(graphed.cnt, eager.cnt)
-        assert torch.equal(graphed.scale, eager.scale)
+        assert torch.equal(graphed.scale, eager.scale) and torch.equal(graphed.last, eager.last)
         del junk
