@@ -112,7 +112,7 @@ def test_decode_step_validation():
 
     def call(d, state=fake, ws_bytes=need):
         return lib.sdm_rt_decode_step(ctypes.byref(d), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12,
-                                      I, None, state, state, state, fake, 768, F, fake, ws_bytes, None)
+                                      I, None, state, state, state, None, fake, 768, F, fake, ws_bytes, None)
     assert call(_dims(B=4, T=2)) == -1 and b"seq_len must be 1" in lib.sdm_rt_last_error()
     assert call(dims, state=None) == -1 and b"state" in lib.sdm_rt_last_error()
     assert call(dims, ws_bytes=need - 1) == -2 and b"workspace" in lib.sdm_rt_last_error()
