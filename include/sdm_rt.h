@@ -117,6 +117,22 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params,
                    float* state_out_mem, float* state_out_cnt,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* sdm_rt_forward without a workspace argument: the same kernels run on a scratch array that the library holds on
+ * each device it runs on (a fixed sdm_rt_noalloc_scratch_bytes() = 128 MiB, kept until the process ends), so the
+ * call allocates no device memory.  It has no counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops).  A call whose workspace (sdm_rt_workspace_bytes) exceeds the
+ * scratch returns SDM_RT_ENOSPACE without launching anything.  All calls on one device share its scratch: calls that
+ * overlap on one device (on different streams, or from different threads) race and must be serialised by the
+ * caller.  Arguments as sdm_rt_forward. */
+size_t sdm_rt_noalloc_scratch_bytes(void);
+int sdm_rt_forward_noalloc(const sdm_rt_dims* dims, const sdm_rt_params* params,
+                           const void* kz, int64_t kz_row_stride, const void* qz, int64_t qz_row_stride,
+                           const void* v, int64_t v_row_stride, const void* gate_logits, int64_t gate_row_stride,
+                           sdm_rt_dtype in_dtype, const uint8_t* reset,
+                           void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                           const float* state_in_mem, const float* state_in_cnt,
+                           float* state_out_mem, float* state_out_cnt, void* stream);
+
 /* Bytes of workspace sdm_rt_decode_step needs (the picks of one token per stream; 0 on invalid dims). */
 size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);
 

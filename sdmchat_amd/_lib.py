@@ -90,6 +90,13 @@ SIGNATURES = {
                                       c_void_p, c_i64, ctypes.c_int,
                                       c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, ctypes.c_size_t, c_void_p]),
+    "sdm_rt_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "sdm_rt_forward_noalloc": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
+                                              c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                                              ctypes.c_int, c_void_p,
+                                              c_void_p, c_i64, ctypes.c_int,
+                                              c_void_p, c_void_p, c_void_p, c_void_p,
+                                              c_void_p]),
     "sdm_rt_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
     "sdm_rt_decode_step": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
                                           c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,

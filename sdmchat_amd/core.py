@@ -137,14 +137,16 @@ class CoreWorkspace:
 
 def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr_b=None, onorm_w=None,
                  gate_bias=None, k, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2,
-                 out_dtype=None, out=None, state_in=None, want_state=False, workspace=None, params=None, reset=None):
+                 out_dtype=None, out=None, state_in=None, want_state=False, workspace=None, params=None, reset=None,
+                 no_alloc=False):
     """The SDM core between the projections and the output map (RunTimeSdm.forward minus wk/wq/wv/wg and wo).
 
     kz, qz [B, T, H * d_a]; v [B, T, H * dh]; gate_logits [B, T, H] or None (no write gate); all share one dtype,
     each with its own uniform row stride.  Returns r [B, T, H * dh] (out_dtype, default v's dtype) and, when want_state, the final
     (mem [B, H, M, dh], cnt [B, H, M]) float32 state.  ``params`` may carry a prepared (SdmRtParams, held) pair.
     reset [B, T] bool or None: where set, the memory is emptied before that position reads (forward(x, reset),
-    track4_onesdm_models.py:229-233)."""
+    track4_onesdm_models.py:229-233).  no_alloc: run on the library's fixed scratch (sdm_rt_forward_noalloc) instead
+    of a workspace."""
     lib = _lib.load()
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape
@@ -183,12 +185,19 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
         if tuple(reset.shape) != (B, T):
             raise ValueError(f"reset must be [B={B}, T={T}]")
         rs = reset.to(device=dev, dtype=torch.uint8).contiguous()
-    nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))  # 0 for invalid dims: the call below reports why
-    ws = (workspace or CoreWorkspace()).get(nbytes, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
-                            _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(out), ostride, _DT[out_dtype], _ptr(mem_in), _ptr(cnt_in),
-                            _ptr(mem_out), _ptr(cnt_out), _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+    if no_alloc:
+        rc = lib.sdm_rt_forward_noalloc(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v),
+                                        vs, _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(out), ostride,
+                                        _DT[out_dtype], _ptr(mem_in), _ptr(cnt_in), _ptr(mem_out), _ptr(cnt_out),
+                                        ctypes.c_void_p(stream))
+    else:
+        nbytes = lib.sdm_rt_workspace_bytes(ctypes.byref(dims))  # 0 for invalid dims: the call below reports why
+        ws = (workspace or CoreWorkspace()).get(nbytes, dev)
+        rc = lib.sdm_rt_forward(ctypes.byref(dims), ctypes.byref(prm), _ptr(kz), ks, _ptr(qz), qs, _ptr(v), vs,
+                                _ptr(gate_logits), gs, _DT[dt], _ptr(rs), _ptr(out), ostride, _DT[out_dtype],
+                                _ptr(mem_in), _ptr(cnt_in), _ptr(mem_out), _ptr(cnt_out), _ptr(ws), ws.numel(),
+                                ctypes.c_void_p(stream))
     _lib.check(rc, lib)
     if want_state:
         return out, (mem_out, cnt_out)

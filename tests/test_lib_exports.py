@@ -119,6 +119,22 @@ def test_decode_step_validation():
     assert call(_dims(B=0, T=1)) == 0
 
 
+def test_forward_noalloc_rejects_calls_beyond_its_scratch():
+    """sdm_rt_forward_noalloc runs on a fixed 128 MiB scratch; a call whose workspace is larger fails on the host,
+    before any device call."""
+    lib = _lib.load()
+    cap = lib.sdm_rt_noalloc_scratch_bytes()
+    assert cap == 128 << 20
+    big = _dims(B=32, T=2048)
+    assert lib.sdm_rt_workspace_bytes(ctypes.byref(big)) > cap
+    prm = _lib.SdmRtParams(*([ctypes.c_void_p(256)] * 7))
+    fake = ctypes.c_void_p(256)
+    F = _lib.SDM_RT_F32
+    rc = lib.sdm_rt_forward_noalloc(ctypes.byref(big), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12,
+                                    F, None, fake, 768, F, None, None, None, None, None)
+    assert rc == -2 and b"scratch" in lib.sdm_rt_last_error()
+
+
 def test_backward_validation():
     """sdm_rt_forward_train / sdm_rt_backward check their arguments on the host before any launch."""
     lib = _lib.load()
