@@ -12,6 +12,18 @@ from numpy PCG64 seeds and stored next to the outputs, so the fixture is self-co
 Output: tests/golden/pk_address_golden.npz with, per case NAME, arrays NAME.z (N, H, d_a) float32,
 NAME.keys1 / NAME.keys2 (H, n_sub, d_a/2) float32, NAME.k (scalar), NAME.sv (N, H, kk) float32 and NAME.si
 (N, H, kk) int16 as returned by the reference (descending order).
+
+``python tests/golden/make_golden.py runtime`` writes tests/golden/runtime_sdm_golden.npz from the reference's
+``pk_address``, ``RunTimeSdm`` (:151-300) and ``OneSdmLM`` (:471-555), on the inputs of golden_inputs.py (numpy
+PCG64; only seeds and a checksum of each input are stored, the tests regenerate the inputs):
+  addr.*     the reference's picks (si int16, sv float32) of the 24,576 layer-workload addresses
+             (golden_inputs.layer_addresses: 2,048 tokens x 12 heads, bf16-rounded projections)
+  config1.*, edge.*   RunTimeSdm.forward in float32 on the CPU (no autocast): y, and the picks of prepare
+             (siw, sir int16 [B, H, T, kk]); config1 = B1 T256 d768 H12 M1024 k8, edge = d32 H4 n_sub 6 k4 chunk 7
+             with fades 0 and 1.  Seeds are searched (with the oracle, fp64) for inputs whose every addressing has
+             a top-k margin above 2e-6, so the picks are the same in any correct float32 or float64 evaluation.
+  model_mlp.*, model_sdm.*   the logits of a tiny OneSdmLM of each arm (golden_inputs.MODEL_KW, reset at BOS), with
+             the same margin search.
 """
 import os
 import sys
@@ -90,5 +102,94 @@ def main():
     print("wrote", OUT, os.path.getsize(OUT), "bytes")
 
 
+def _layer_margin(kw, p, x):
+    """The smallest fp64 top-k margin of both addressings of a layer (the oracle's restatement of prepare)."""
+    from oracle import sdm_fp64 as O
+    B, T, d = x.shape
+    H, d_a, k = kw["heads"], kw["d_a"], kw["k"]
+    hx = O.rms_norm(x.astype(np.float64), p["norm.w"].astype(np.float64))
+    m = np.inf
+    for wn in ("wk.weight", "wq.weight"):
+        z = (hx @ p[wn].astype(np.float64).T).reshape(B * T, H, d_a) + p["addr_b"]
+        m = min(m, float(O.topk_margin(z, p["keys1"], p["keys2"], k).min()))
+    return m
+
+
+def runtime_main():
+    sys.path.insert(0, REF_DIR)
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+    import track4_onesdm_models as ref  # noqa: E402  (reference checkout, this container only)
+    from oracle import sdm_fp64 as O  # noqa: E402
+    from tests.golden import golden_inputs as G  # noqa: E402
+
+    torch.set_num_threads(4)
+    blob = {}
+    # 1. the layer workload's addressing
+    z, k1, k2 = G.layer_addresses()
+    with torch.no_grad():
+        sv, si = ref.pk_address(torch.from_numpy(z), torch.from_numpy(k1), torch.from_numpy(k2), 8)
+    blob["addr.seed"] = np.int64(21)
+    blob["addr.digest"] = G.digest(z)
+    blob["addr.k"] = np.int64(8)
+    blob["addr.si"] = si.numpy().astype(np.int16)
+    blob["addr.sv"] = sv.numpy().astype(np.float32)
+    print("addr", z.shape, "->", tuple(si.shape), flush=True)
+    # 2. RunTimeSdm.forward at config 1 and the edge shape
+    for name, seed0 in (("config1", 100), ("edge", 200)):
+        for seed in range(seed0, seed0 + 60):
+            kw, p, x = G.layer_case(name, seed)
+            if _layer_margin(kw, p, x) > 2e-6:
+                break
+        else:
+            raise RuntimeError(f"{name}: no seed with clean margins")
+        m = ref.RunTimeSdm(kw["d"], heads=kw["heads"], n_sub=kw["n_sub"], d_a=kw["d_a"], k=kw["k"],
+                           decays=kw["decays"], chunk=kw["chunk"])
+        m.load_state_dict({n: torch.from_numpy(v) for n, v in p.items()}, strict=True)
+        m.eval()
+        with torch.no_grad():
+            xt = torch.from_numpy(x)
+            y = m(xt)
+            siw, _, sir, _, _ = m.prepare(xt)
+        blob[f"{name}.seed"] = np.int64(seed)
+        blob[f"{name}.digest"] = G.digest(x)
+        blob[f"{name}.y"] = y.numpy().astype(np.float32)
+        blob[f"{name}.siw"] = siw.numpy().astype(np.int16)
+        blob[f"{name}.sir"] = sir.numpy().astype(np.int16)
+        print(name, "seed", seed, "y", tuple(y.shape), flush=True)
+    # 3. tiny OneSdmLM logits of both arms
+    for ffn in ("mlp", "sdm"):
+        kw = dict(G.MODEL_KW)
+        V = kw.pop("V")
+        for seed in range(300, 360):
+            torch.manual_seed(seed)
+            mdl = ref.OneSdmLM(V, ffn=ffn, seed=seed, **kw)
+            shapes = {n: tuple(t.shape) for n, t in mdl.state_dict().items()}
+            p = G.model_params(shapes, seed)
+            idx = G.model_tokens(seed)
+            cfg = dict(layers=kw["layers"], heads=kw["heads"], d_a=kw["d_a"], k=kw["k"], ffn=ffn,
+                       reset_at_bos=True, bos_id=kw["bos_id"], sdm_heads=kw["sdm_heads"], sdm_d_a=kw["sdm_d_a"],
+                       sdm_k=kw["sdm_k"])
+            margins = []
+            O.model_forward(idx, {n: v.astype(np.float64) for n, v in p.items()}, cfg, margins)
+            if min(margins) > 2e-6:
+                break
+        else:
+            raise RuntimeError(f"model {ffn}: no seed with clean margins")
+        mdl.load_state_dict({n: torch.from_numpy(v) for n, v in p.items()}, strict=True)
+        mdl.eval()
+        with torch.no_grad():
+            logits = mdl(torch.from_numpy(idx))
+        blob[f"model_{ffn}.seed"] = np.int64(seed)
+        blob[f"model_{ffn}.idx"] = idx.astype(np.int16)
+        blob[f"model_{ffn}.logits"] = logits.numpy().astype(np.float32)
+        print("model", ffn, "seed", seed, "logits", tuple(logits.shape), flush=True)
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "runtime_sdm_golden.npz")
+    np.savez_compressed(out, **blob)
+    print("wrote", out, os.path.getsize(out), "bytes")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["runtime"]:
+        runtime_main()
+    else:
+        main()

@@ -8,7 +8,11 @@ import torch
 
 from oracle import sdm_fp64 as O
 from sdmchat_amd import TrainedSdm, core
-from tests._gpu_util import DELTA, assert_close, say
+from tests._gpu_util import assert_close, say
+
+# the kernel addresses its own float32 queries (the oracle its float64 ones): picks may differ where the fp64 top-k
+# margin is within the queries' float32 error
+Q_DELTA = 1e-6
 
 pytestmark = pytest.mark.gpu
 
@@ -63,7 +67,7 @@ def test_trained_sdm_layer_matches_oracle(d, n_sub, heads, d_a, k):
     si_k, w_k = si_k.cpu().numpy(), w_k.cpu().numpy()
     same = np.all(np.sort(si_k, -1) == np.sort(parts["si"], -1), -1)
     margin = O.topk_margin(parts["q"], p["keys1"], p["keys2"], k)
-    assert np.all(same | (margin < DELTA)), "picks differ away from near-ties"
+    assert np.all(same | (margin < Q_DELTA)), "picks differ away from near-ties"
     # the layer on the kernel's own picks and weights
     B, T = x.shape[:2]
     r = O.table_read(si_k, w_k, p["values"]).reshape(B, T, d)
