@@ -53,6 +53,31 @@ def pk_address(z, keys1, keys2, k):
     return sv, si
 
 
+def adopt_picks(z, keys1, keys2, sv, si, forced, tol, log=None):
+    """Where another implementation's ordered picks ``forced`` (N, H, kk) differ from the oracle's si, check that
+    each difference is a tie within ``tol`` (the two slots' fp64 scores at that position) and take the forced
+    picks, with their fp64 scores.  Comparing a whole model with the HIP path needs this: its float32 inputs to a
+    layer differ from the oracle's float64 ones by rounding, so near ties may resolve the other way.  Appends the
+    number of adopted addresses to ``log``."""
+    forced = np.asarray(forced).astype(np.int64)
+    diff = si != forced
+    rows = diff.any(-1)                  # (N, H)
+    if rows.any():
+        tok = np.flatnonzero(rows.any(-1))   # tokens with a differing head
+        g = full_grid(np.asarray(z, np.float64)[tok], keys1, keys2)
+        s_own = np.take_along_axis(g, si[tok], -1)
+        s_got = np.take_along_axis(g, forced[tok], -1)
+        gap = np.abs(s_own - s_got)[diff[tok]]
+        if not np.all(gap < tol):
+            raise AssertionError(f"picks differ away from a tie: fp64 score gap {float(gap.max()):.3e} >= {tol:.1e}")
+        si = np.where(rows[..., None], forced, si)
+        sv = np.array(sv)
+        sv[tok] = np.where(rows[tok][..., None], s_got, sv[tok])
+    if log is not None:
+        log.append(int(rows.sum()))
+    return sv, si
+
+
 def full_grid(z, keys1, keys2):
     """Every location's score (s1[i] + s2[j]) / 2 at flat index i * n_sub + j: (N, H, n_sub^2)."""
     s1, s2 = half_scores(z, keys1, keys2)
@@ -76,6 +101,23 @@ def topk_margin(z, keys1, keys2, k):
     g = full_grid(z, keys1, keys2)
     if g.shape[-1] <= kk:
         return np.full(g.shape[:-1], np.inf)
+    part = -np.sort(-g, axis=-1)
+    return part[..., kk - 1] - part[..., kk]
+
+
+def topk_margin_pruned(z, keys1, keys2, k):
+    """topk_margin without the whole grid: the (kk+1) best locations all lie in the grid of each half's kk+1 best
+    sub-keys (a location ranked r in its half is beaten by r locations of its column), so that grid decides the
+    margin exactly."""
+    n_sub = keys1.shape[1]
+    kk = min(k, min(k, n_sub) ** 2)
+    if n_sub * n_sub <= kk:
+        return np.full(np.asarray(z).shape[:-1], np.inf)
+    s1, s2 = half_scores(z, keys1, keys2)
+    c = min(kk + 1, n_sub)
+    v1 = -np.sort(-s1, axis=-1)[..., :c]
+    v2 = -np.sort(-s2, axis=-1)[..., :c]
+    g = ((v1[..., :, None] + v2[..., None, :]) * 0.5).reshape(*v1.shape[:-1], c * c)
     part = -np.sort(-g, axis=-1)
     return part[..., kk - 1] - part[..., kk]
 
@@ -173,17 +215,24 @@ def finish(num, den, read_mode="mean", read_eps=1e-3, out_norm=True, onorm_w=Non
     return r
 
 
-def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False, reset=None):
+def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False, reset=None, forced=None):
     """The SDM core between the projections and the output map.
 
     kz, qz (B, T, H, d_a) already include addr_b; V (B, T, H, dh); gate_logits (B, T, H) or None (gate off).
     p: dict with keys1, keys2, log_scale, decay, onorm_w.  cfg: dict with k, read_mode, read_eps, out_norm,
-    out_norm_eps.  Returns r (B, T, H, dh) in float64."""
+    out_norm_eps (and adopt_tol, adopt_log for ``forced``).  forced: None or another implementation's (siw, sir)
+    picks (N, H, kk), taken at ties (adopt_picks).  Returns r (B, T, H, dh) in float64."""
     B, T, H, d_a = kz.shape
     k = cfg["k"]
     N = B * T
-    svw, siw = pk_address(np.asarray(kz, np.float64).reshape(N, H, d_a), p["keys1"], p["keys2"], k)
-    svr, sir = pk_address(np.asarray(qz, np.float64).reshape(N, H, d_a), p["keys1"], p["keys2"], k)
+    zw = np.asarray(kz, np.float64).reshape(N, H, d_a)
+    zr = np.asarray(qz, np.float64).reshape(N, H, d_a)
+    svw, siw = pk_address(zw, p["keys1"], p["keys2"], k)
+    svr, sir = pk_address(zr, p["keys1"], p["keys2"], k)
+    if forced is not None:
+        tol, log = cfg.get("adopt_tol", 1e-5), cfg.get("adopt_log")
+        svw, siw = adopt_picks(zw, p["keys1"], p["keys2"], svw, siw, forced[0], tol, log)
+        svr, sir = adopt_picks(zr, p["keys1"], p["keys2"], svr, sir, forced[1], tol, log)
     gate = None if gate_logits is None else sigmoid(np.asarray(gate_logits, np.float64).reshape(N, H))
     ww = address_weights(svw, p["log_scale"], gate)
     wr = address_weights(svr, p["log_scale"], None)
@@ -203,7 +252,7 @@ def core_forward(kz, qz, V, gate_logits, p, cfg, return_parts=False, reset=None)
     return r
 
 
-def layer_forward(x, p, cfg, reset=None):
+def layer_forward(x, p, cfg, reset=None, forced=None):
     """Whole RunTimeSdm.forward in float64 (OM:195-213 prepare, OM:249-274 forward, OM:243-247 finish).
 
     x (B, T, d); p holds the module's parameters under their state_dict names ('norm.w', 'wk.weight', ...,
@@ -220,7 +269,7 @@ def layer_forward(x, p, cfg, reset=None):
     g = (hx @ p["wg.weight"].T + p["wg.bias"]) if cfg.get("write_gate", True) else None
     core_p = dict(keys1=p["keys1"], keys2=p["keys2"], log_scale=p["log_scale"], decay=p["decay"],
                   onorm_w=p.get("onorm_w"))
-    r = core_forward(kz, qz, V, g, core_p, cfg, reset=reset)
+    r = core_forward(kz, qz, V, g, core_p, cfg, reset=reset, forced=forced)
     return r.reshape(B, T, d) @ p["wo.weight"].T
 
 
@@ -233,7 +282,7 @@ def table_read(si, w, values):
     return np.einsum("nhk,nhkd->nhd", np.asarray(w, np.float64), rows)
 
 
-def trained_sdm_forward(x, p, cfg, return_parts=False):
+def trained_sdm_forward(x, p, cfg, return_parts=False, forced=None):
     """TrainedSdm.forward (OM:414-457) in float64: RMSNorm, the query map, pk_address, softmax(exp(log_scale) *
     score), the weighted sum of the picked value rows, the output map.  p: norm.w, wq.weight, keys1, keys2, values,
     log_scale, wo.weight.  cfg: heads, d_a, k."""
@@ -242,6 +291,9 @@ def trained_sdm_forward(x, p, cfg, return_parts=False):
     hx = rms_norm(np.asarray(x, np.float64), p["norm.w"])
     q = (hx @ np.asarray(p["wq.weight"], np.float64).T).reshape(B * T, H, d_a)
     sv, si = pk_address(q, p["keys1"], p["keys2"], k)
+    if forced is not None:
+        sv, si = adopt_picks(q, p["keys1"], p["keys2"], sv, si, forced, cfg.get("adopt_tol", 1e-5),
+                             cfg.get("adopt_log"))
     w = address_weights(sv, p["log_scale"])
     r = table_read(si, w, p["values"]).reshape(B, T, d)
     y = r @ np.asarray(p["wo.weight"], np.float64).T
@@ -259,13 +311,15 @@ def swiglu(x, gate_w, up_w, down_w):
     return (silu(x @ gate_w.T) * (x @ up_w.T)) @ down_w.T
 
 
-def model_forward(idx, p, cfg, margins=None):
+def model_forward(idx, p, cfg, margins=None, forced=None):
     """OneSdmLM.forward (OM:471-555, archive off) in float64: embedding, per layer x + RunTimeSdm(x, reset) and
     x + SwiGLU(RMSNorm x) (ffn 'mlp') or x + TrainedSdm(x) (ffn 'sdm'), final RMSNorm, tied head.
 
     idx (B, T) int; p: the model's state dict as float64 arrays; cfg: layers, heads, d_a, k, ffn, mem, tie,
     reset_at_bos, bos_id, sdm_heads, sdm_d_a, sdm_k and the mixer options of core_forward.  When ``margins`` is a
-    list, the smallest fp64 top-k margin of every addressing is appended to it.  Returns logits (B, T, V)."""
+    list, the smallest fp64 top-k margin of every addressing is appended to it.  forced: None or a dict of another
+    implementation's picks, {("mem", i): (siw, sir), ("sdm", i): si} as (N, H, kk) arrays, taken at ties
+    (adopt_picks, cfg["adopt_tol"]; the adopted counts go to cfg["adopt_log"]).  Returns logits (B, T, V)."""
     E = p["emb.weight"]
     x = E[np.asarray(idx)]
     B, T, d = x.shape
@@ -281,15 +335,17 @@ def model_forward(idx, p, cfg, margins=None):
                 for wn in ("wk.weight", "wq.weight"):
                     z = (hx @ lp[wn].T).reshape(B * T, H, d_a) + lp["addr_b"]
                     margins.append(float(topk_margin(z, lp["keys1"], lp["keys2"], cfg["k"]).min()))
-            x = x + layer_forward(x, lp, cfg, reset)
+            x = x + layer_forward(x, lp, cfg, reset, None if forced is None else forced[("mem", i)])
         if cfg.get("ffn", "mlp") == "mlp":
             x = x + swiglu(rms_norm(x, p[f"mnorms.{i}.w"]), p[f"mlps.{i}.gate.weight"], p[f"mlps.{i}.up.weight"],
                            p[f"mlps.{i}.down.weight"])
         elif cfg["ffn"] == "sdm":
             pre = f"sdms.{i}."
             sp = {n[len(pre):]: v for n, v in p.items() if n.startswith(pre)}
-            scfg = dict(heads=cfg["sdm_heads"], d_a=cfg["sdm_d_a"], k=cfg["sdm_k"])
-            y, parts = trained_sdm_forward(x, sp, scfg, return_parts=True)
+            scfg = dict(heads=cfg["sdm_heads"], d_a=cfg["sdm_d_a"], k=cfg["sdm_k"], adopt_tol=cfg.get("adopt_tol", 1e-5),
+                        adopt_log=cfg.get("adopt_log"))
+            y, parts = trained_sdm_forward(x, sp, scfg, return_parts=True,
+                                           forced=None if forced is None else forced[("sdm", i)])
             if margins is not None:
                 margins.append(float(topk_margin(parts["q"], sp["keys1"], sp["keys2"], scfg["k"]).min()))
             x = x + y

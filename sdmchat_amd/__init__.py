@@ -9,4 +9,4 @@
 """
 from .runtime_sdm import RMSNorm, RunTimeSdm  # noqa: F401
 from .trained_sdm import TrainedSdm  # noqa: F401
-from .model import OneSdmLM  # noqa: F401
+from .model import DecodeGraph, ModelDecodeState, OneSdmLM, decode_state_bytes  # noqa: F401

@@ -56,6 +56,31 @@ def matched_sdm_n_sub(d, mlp_f, heads, d_a):
     return min(range(2, 4097), key=lambda n: abs(trained_sdm_params(d, n, heads, d_a) - target))
 
 
+class ModelDecodeState:
+    """The decode state of B streams of a OneSdmLM: per layer the mixer's core.DecodeState (None where the mixer is
+    disabled) and the number of tokens each stream has consumed.  Everything else in the model acts per token."""
+
+    def __init__(self, layers, pos=0):
+        self.layers = list(layers)
+        self.pos = pos
+
+    def nbytes(self):
+        """Device bytes the state holds."""
+        return sum(st.nbytes() for st in self.layers if st is not None)
+
+
+def decode_state_bytes(model, T):
+    """Bytes kept to continue decoding after T tokens (float32), excluding the weights (track4_onesdm_models.py:
+    641-652): per layer with a mixer, each head's M locations of dh values plus one write count.  It does not grow
+    with T.  (ModelDecodeState.nbytes adds the per-head scales and last-write slots this build also keeps.)"""
+    if not isinstance(model, OneSdmLM):
+        raise ValueError(f"decode_state_bytes: {type(model).__name__} is not a OneSdmLM")
+    if not model.has_mem:
+        return 0
+    m = model.mems[0]
+    return model.n_layers * m.h * m.M * (m.dh + 1) * 4
+
+
 class OneSdmLM(nn.Module):
     """Embedding, layers of [x + RunTimeSdm(x); x + FFN(x)], final RMSNorm, tied (or separate) head."""
 
@@ -135,3 +160,78 @@ class OneSdmLM(nn.Module):
 
     def forward(self, idx, sequential=False):
         return self.project(self.hidden(idx, sequential))
+
+    # -- decoding ----------------------------------------------------------------------------------------------------
+    def decode_state(self, batch, device=None):
+        """An empty decode state for ``batch`` streams."""
+        return ModelDecodeState([m.decode_state(batch, device) if m.enabled else None for m in self.mems])
+
+    def prefill(self, idx):
+        """forward(idx) over a prompt, also returning the decode state after its last token: (logits [B, T, V],
+        ModelDecodeState), so step() continues the streams (inference only)."""
+        keep = [m.keep_state for m in self.mems]
+        try:
+            for m in self.mems:
+                m.keep_state = True
+            logits = self.forward(idx)
+            layers = []
+            for m in self.mems:
+                if m.enabled:
+                    mem, cnt = m.last_state
+                    layers.append(core.DecodeState.from_state(mem, cnt, core.pick_pitch(m.k, m.n_sub)))
+                else:
+                    layers.append(None)
+        finally:
+            for m, k in zip(self.mems, keep):
+                m.keep_state = k
+        return logits, ModelDecodeState(layers, idx.shape[1])
+
+    def step(self, idx_t, state):
+        """One token for each of B streams: idx_t [B] int64 -> logits [B, V], the last position of
+        forward(idx, sequential=True) (track4_onesdm_models.py:534-555), with every mixer's memory carried in
+        ``state`` (a ModelDecodeState, updated in place).  Inference only."""
+        x = self.enfold(idx_t)
+        reset = (idx_t == self.bos_id) if self.reset_at_bos else None
+        for i in range(self.n_layers):
+            m = self.mems[i]
+            if m.enabled:
+                x = x + m.step(x, state.layers[i], reset)
+            if self.ffn == "mlp":
+                x = x + self.mlps[i](_norm(x, self.mnorms[i]))
+            elif self.ffn == "sdm":
+                x = x + self.sdms[i](x[:, None])[:, 0]   # per token
+        state.pos += 1
+        return self.project(_norm(x, self.nf))
+
+
+class DecodeGraph:
+    """OneSdmLM.step for a fixed set of B streams captured in a HIP graph: ``step(tokens)`` copies the tokens into
+    the graph's input, replays it and returns the graph's logits tensor (overwritten by the next step).  ``steps``
+    consecutive steps can be captured in one graph (``run(tokens [steps, B])``).  The state is the caller's
+    ModelDecodeState, updated in place; capture first runs two steps on a scratch state of the same shapes, so that
+    every workspace and parameter cache exists before capture and nothing allocates inside the graph."""
+
+    def __init__(self, model, state, steps=1):
+        dev = model.emb.weight.device
+        B = next(st.mem.shape[0] for st in state.layers if st is not None)
+        self.model, self.state, self.steps = model, state, steps
+        self.tokens = torch.zeros(steps, B, dtype=torch.long, device=dev)
+        with torch.no_grad():
+            scratch = model.decode_state(B, dev)
+            for _ in range(2):
+                model.step(self.tokens[0], scratch)
+            torch.cuda.synchronize(dev)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                outs = [model.step(self.tokens[t], state) for t in range(steps)]
+                self.logits = torch.stack(outs) if steps > 1 else outs[0]
+        state.pos -= steps   # capture ran no step
+
+    def run(self, tokens):
+        """tokens [steps, B] (or [B] for one step) -> logits [steps, B, V] (or [B, V])."""
+        self.tokens.copy_(tokens.reshape(self.tokens.shape))
+        self.graph.replay()
+        self.state.pos += self.steps
+        return self.logits
+
+    step = run

@@ -65,6 +65,8 @@ class RunTimeSdm(nn.Module):
         self.out_norm_eps = out_norm_eps
         self.enabled = True
         self.keep_state = False   # set True to fill last_state (costs one state write per call)
+        self.keep_picks = False   # set True to fill last_picks and last_addresses (an extra addressing per call)
+        self.last_picks = self.last_addresses = None
         self.norm = RMSNorm(d)
         self.wk = nn.Linear(d, heads * d_a, bias=False)
         self.wq = nn.Linear(d, heads * d_a, bias=False)
@@ -220,6 +222,12 @@ class RunTimeSdm(nn.Module):
                 want_state=self.keep_state, workspace=self._ws, reset=reset, params=self._core_params(x.device))
             r, state = (res if self.keep_state else (res, None))
             y = torch.matmul(r, wo.t()).to(x.dtype)
+            if self.keep_picks:   # the same addressing kernels as the core's, on the same projections
+                prm = self._core_params(x.device)
+                self.last_addresses = (kz, qz)   # before addr_b
+                self.last_picks = tuple(
+                    core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
+                                 params=prm)[0] for z in (kz, qz))
         # the gate logits alone ([B, T, H]; a view would keep the whole projection buffer alive)
         self._gate_src = (g.contiguous() if g is not None else None, None, (B, T, H), x.device)
         self._last_gate = None

@@ -56,3 +56,38 @@ def layer_params(cfg, seed=0, decay_range=(0.9, 0.999), decays=None):
 def layer_input(B, T, d, seed=1):
     rng = np.random.Generator(np.random.PCG64(seed))
     return rng.standard_normal((B, T, d)).astype(np.float32)
+
+
+# The whole-model workloads: the PARTIAL arm (SwiGLU of hidden 2,048 after each mixer) and the FULL arm (a TrainedSdm
+# of 4,096 slots, one head of width 768, k 16), 12 layers of d 768, vocabulary 32,768.
+MODEL_FULL = dict(V=32768, d=768, layers=12, mlp_f=2048, heads=12, n_sub=32, d_a=64, k=8)
+ARMS = {"swiglu": dict(ffn="mlp"), "trained_sdm": dict(ffn="sdm", sdm_n_sub=64, sdm_heads=1, sdm_k=16)}
+
+
+def full_model(arm, seed=5, **over):
+    """A OneSdmLM of the whole-model workload with seeded weights (CPU, float32): the reference's initialisation
+    (torch.manual_seed(seed)) with the zero-start maps (the mixers' wo and wg, the TrainedSdm output maps and value
+    tables) filled with N(0, 0.02), so every layer carries signal; fades U(0.9, 0.999) per head."""
+    import torch
+
+    from .model import OneSdmLM
+
+    kw = dict(MODEL_FULL)
+    kw.update(ARMS[arm])
+    kw.update(over)
+    V = kw.pop("V")
+    kw.setdefault("decays", tuple(float(v) for v in np.random.Generator(np.random.PCG64(3)).uniform(0.9, 0.999,
+                                                                                                     kw["heads"])))
+    torch.manual_seed(seed)
+    m = OneSdmLM(V, **kw)
+    gen = torch.Generator().manual_seed(seed + 6)
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            if n.endswith(("wo.weight", "wg.weight", "values")):
+                p.normal_(0.0, 0.02, generator=gen)
+    return m
+
+
+def model_tokens(B, T, V=32768, seed=11):
+    """Seeded uniform token ids (B, T) int64."""
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, V, size=(B, T)).astype(np.int64)

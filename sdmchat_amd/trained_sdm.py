@@ -39,6 +39,8 @@ class TrainedSdm(nn.Module):
         self.log_scale = nn.Parameter(torch.full((heads,), math.log(scale)), requires_grad=learn_scale)
         self.wo = nn.Linear(d, d, bias=False)
         self.last_si = None
+        self.keep_picks = False   # set True to keep the last forward's queries in last_q
+        self.last_q = None
         self._cast = None
         self._prm = core.ParamCache()
 
@@ -73,6 +75,8 @@ class TrainedSdm(nn.Module):
         """RMSNorm, the query map and the addressing: slots, scores, weights [B, H, T, pitch]."""
         hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
         q = torch.matmul(hx, self._weights(dt)[0].t())
+        if self.keep_picks:
+            self.last_q = q
         prm = self._prm.get(x.device, self.keys1, self.keys2, None, self.log_scale, None, None, None)
         return core.address(q, self.keys1, self.keys2, self.k, self.log_scale, padded=True, params=prm)
 

@@ -111,14 +111,16 @@ def test_bench_shape_bf16():
     say("bench-shape picks that differ from the oracle (all at near-ties):", flips)
 
 
-@pytest.mark.parametrize("T", [64, 150])
-def test_resets_match_the_oracle(T):
+@pytest.mark.parametrize("T,H,dh,d_a,n_sub", [(64, 4, 16, 16, 8), (150, 4, 16, 16, 8), (150, 12, 64, 64, 32)])
+def test_resets_match_the_oracle(T, H, dh, d_a, n_sub):
     """BOS resets (forward(x, reset), OM:229-233): the memory is emptied before the position reads.  Resets at chunk
-    starts, inside chunks, twice in one chunk, at the last position, and a row without any; fades 0, 0.5, 0.97, 1."""
+    starts, inside chunks, twice in one chunk, at the last position, and a row without any; fades 0, 0.5, 0.97, 1
+    (and the layer shape's: two column groups per slab sharing the out-norm)."""
     from oracle import sdm_fp64 as O
     from tests._gpu_util import assert_close, gpu_address
-    B, H, dh = 3, 4, 16
-    kz, qz, V, g, p = core_inputs(B, T, H, dh, 16, 8, seed=90 + T, decays=(0.0, 0.5, 0.97, 1.0))
+    B = 3
+    decays = (0.0, 0.5, 0.97, 1.0) * (H // 4)
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, d_a, n_sub, seed=90 + T, decays=decays)
     reset = np.zeros((B, T), bool)
     reset[0, [0, 20, 31, T - 1]] = True
     reset[1, [1, 63]] = True
@@ -130,7 +132,8 @@ def test_resets_match_the_oracle(T):
     Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
     num, den, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
                                            wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
-                                           (np.zeros((B, H, 64, dh)), np.zeros((B, H, 64))), reset=reset)
+                                           (np.zeros((B, H, n_sub ** 2, dh)), np.zeros((B, H, n_sub ** 2))),
+                                           reset=reset)
     r64 = O.finish(num, den, "mean", 1e-3, True, p["onorm_w"].astype(np.float64), 1e-2)
     assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 1e-5, msg="read-out with resets")
     np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)

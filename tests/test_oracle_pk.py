@@ -99,3 +99,39 @@ def test_weights_closed_form():
     np.testing.assert_allclose(O.rms_norm(x, np.ones(2), eps=0.0), x / np.sqrt(12.5), rtol=1e-15)
     np.testing.assert_allclose(O.normalize_rows(np.array([3.0, 4.0])), [0.6, 0.8], rtol=1e-15)
     np.testing.assert_allclose(O.normalize_rows(np.zeros(3)), np.zeros(3))
+
+
+def test_adopt_picks_takes_ties_and_rejects_the_rest():
+    """adopt_picks (used when a whole model is compared with the HIP path) swaps in another implementation's picks
+    only where the two slots' fp64 scores agree within the tolerance."""
+    rng = np.random.Generator(np.random.PCG64(5))
+    k1 = rng.standard_normal((1, 6, 3))
+    k2 = rng.standard_normal((1, 6, 3))
+    k2[0, 3] = k2[0, 2]   # sub-keys 2 and 3 of the second half are equal: slots i*6+2 and i*6+3 tie exactly
+    z = rng.standard_normal((4, 1, 6))
+    sv, si = O.pk_address(z, k1, k2, 4)
+    tied = si.copy()
+    for n in range(4):   # swap a 2 <-> 3 partner where the pick list holds exactly one of them
+        for j in range(4):
+            s = si[n, 0, j]
+            if s % 6 in (2, 3) and (s ^ 1) not in si[n, 0]:
+                tied[n, 0, j] = s ^ 1
+                break
+    log = []
+    sv2, si2 = O.adopt_picks(z, k1, k2, sv, si, tied, 1e-12, log)
+    np.testing.assert_array_equal(si2, tied)
+    np.testing.assert_allclose(sv2, sv, atol=1e-15)
+    assert log == [int((tied != si).any(-1).sum())]
+    wrong = si.copy()
+    wrong[0, 0, 0] = int(np.setdiff1d(np.arange(36), si[0, 0])[-1])   # a far worse slot
+    with pytest.raises(AssertionError):
+        O.adopt_picks(z, k1, k2, sv, si, wrong, 1e-6)
+
+
+@pytest.mark.parametrize("H,n_sub,half,k", [(3, 32, 16, 8), (2, 64, 16, 16), (2, 6, 4, 5), (1, 2, 3, 8)])
+def test_pruned_margin_equals_full_grid_margin(H, n_sub, half, k):
+    rng = np.random.Generator(np.random.PCG64(6))
+    z = rng.standard_normal((50, H, 2 * half))
+    k1 = rng.standard_normal((H, n_sub, half))
+    k2 = rng.standard_normal((H, n_sub, half))
+    np.testing.assert_array_equal(O.topk_margin_pruned(z, k1, k2, k), O.topk_margin(z, k1, k2, k))
