@@ -159,26 +159,25 @@ def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
                       "random tokens' projections between replays"}
 
 
-def model_bench(dev, vocab=32768, layers=12, mlp_f=2048):
-    """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms (see the module doc)."""
-    import numpy as np
+def model_bench(dev):
+    """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms, and the bf16 logits' agreement with
+    float32 (see the module doc)."""
     import torch
 
-    from sdmchat_amd import OneSdmLM
+    from sdmchat_amd import synthetic as S
 
     out = {}
-    gen = torch.Generator().manual_seed(11)
-    idx = torch.randint(0, vocab, (B, T), generator=gen).to(dev)
-    decays = tuple(float(v) for v in np.random.Generator(np.random.PCG64(3)).uniform(0.9, 0.999, H))
-    for name, kw in (("swiglu", dict(ffn="mlp")),
-                     ("trained_sdm", dict(ffn="sdm", sdm_n_sub=64, sdm_heads=1, sdm_k=16))):
-        torch.manual_seed(5)
-        m = OneSdmLM(vocab, d=D, layers=layers, mlp_f=mlp_f, heads=H, n_sub=N_SUB, d_a=D_A, k=K, decays=decays, **kw)
-        with torch.no_grad():
-            for n, p in m.named_parameters():
-                if n.endswith(("wo.weight", "wg.weight", "values")):
-                    p.normal_(0.0, 0.02, generator=gen)
-        m = m.to(dev).to(torch.bfloat16).eval()
+    idx = torch.from_numpy(S.model_tokens(B, T, seed=11)).to(dev)
+    agree = {}
+    for name in ("swiglu", "trained_sdm"):
+        m = S.full_model(name).to(dev).eval()
+        with torch.no_grad():   # bf16 logits against float32 ones on the same weights (B=1, T=512)
+            ref = m(idx[:1, :512]).float()
+            m = m.to(torch.bfloat16)
+            low = m(idx[:1, :512]).float()
+        agree[name] = {"max_abs_err_over_scale": round(float((low - ref).abs().max() / ref.abs().max()), 5),
+                       "top1_agreement": round(float((low.argmax(-1) == ref.argmax(-1)).float().mean()), 4)}
+        del ref, low
         with torch.no_grad():
             for _ in range(2):
                 m(idx)
@@ -193,13 +192,53 @@ def model_bench(dev, vocab=32768, layers=12, mlp_f=2048):
                 ts.append(e0.elapsed_time(e1))
         ms = sorted(ts)[2]
         out[name] = {"ms": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
-        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
+        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s; bf16 vs fp32 "
+            f"{agree[name]}")
         del m
         torch.cuda.empty_cache()
-    out["workload"] = (f"OneSdmLM forward (logits): B={B} T={T}, vocabulary {vocab}, {layers} layers, d={D}, mixer "
-                       f"{H} heads M={N_SUB * N_SUB} k={K}; swiglu: hidden {mlp_f}; trained_sdm: 4,096 slots, 1 head, "
-                       f"k=16; bf16")
+    mf = S.MODEL_FULL
+    out["logit_agreement"] = dict(agree, workload="the same model in bfloat16 and in float32, B=1, T=512: max "
+                                  "|logit difference| / max |float32 logit|, and the fraction of positions whose "
+                                  "top logit agrees")
+    out["workload"] = (f"OneSdmLM forward (logits): B={B} T={T}, vocabulary {mf['V']}, {mf['layers']} layers, "
+                       f"d={mf['d']}, mixer {mf['heads']} heads M={mf['n_sub'] ** 2} k={mf['k']}; swiglu: hidden "
+                       f"{mf['mlp_f']}; trained_sdm: 4,096 slots, 1 head, k=16; bf16")
     return out
+
+
+def decode_model_bench(dev, streams=64, graph_steps=64, total=32768):
+    """The FULL model (the trained_sdm arm) decoding `streams` streams, one fresh random token per stream per step,
+    through `total` positions (see the module doc)."""
+    import numpy as np
+    import torch
+
+    from sdmchat_amd import DecodeGraph, synthetic as S
+
+    m = S.full_model("trained_sdm").to(dev).to(torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(13)
+    replays = total // graph_steps + 1
+    with torch.no_grad():
+        st = m.decode_state(streams, dev)
+        g = DecodeGraph(m, st, steps=graph_steps)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+        t0 = time.perf_counter()
+        for e0, e1 in evs:
+            toks = torch.randint(0, m.V, (graph_steps, streams), generator=gen, device=dev)
+            e0.record()
+            g.run(toks)
+            e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
+    by_pos = {str(p): round(float(us[p // graph_steps]), 1) for p in (0, 1024, 8192, 32768) if p <= total}
+    steps = replays * graph_steps
+    log(f"decode (FULL model): {np.median(us):.1f} us per step, {streams * 1e6 / np.median(us):.0f} tokens/s, by "
+        f"position {by_pos}; {steps} steps in {wall:.1f} s")
+    return {"workload": f"FULL OneSdmLM (trained_sdm arm) decode: {streams} streams, one fresh random token per "
+                        f"stream per step, {steps} steps, bf16, float32 state ({st.nbytes() / 2 ** 30:.2f} GiB)",
+            "us_per_step": round(float(np.median(us)), 1), "tokens_per_s": round(streams * 1e6 / float(np.median(us)), 1),
+            "us_per_step_by_position": by_pos, "wall_s": round(wall, 2),
+            "method": f"HIP graph of {graph_steps} steps (DecodeGraph), replay time / {graph_steps}"}
 
 
 def train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms):
@@ -283,6 +322,9 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model measurement")
+    ap.add_argument("--no-decode-model", action="store_true", help="skip the whole-model decode measurement")
+    ap.add_argument("--decode-model-only", action="store_true", help="only the whole-model decode (profiler runs)")
+    ap.add_argument("--decode-model-steps", type=int, default=32768, help="positions the whole-model decode runs")
     ap.add_argument("--model-only", action="store_true", help="only the whole-model measurement (for profiler runs)")
     ap.add_argument("--no-train", action="store_true", help="skip the backward measurement")
     ap.add_argument("--train-only", action="store_true", help="only the backward measurement (for profiler runs)")
@@ -300,6 +342,9 @@ def main():
     dev = torch.device("cuda:0")
     if a.model_only:
         print(json.dumps({"model": model_bench(dev)}), flush=True)
+        return
+    if a.decode_model_only:
+        print(json.dumps({"decode_model": decode_model_bench(dev, total=a.decode_model_steps)}), flush=True)
         return
     cfg = S.layer_cfg(d=D, heads=H, n_sub=N_SUB, d_a=D_A, k=K)
     params = S.layer_params(cfg, seed=0)
@@ -365,6 +410,7 @@ def main():
         decode = None if a.no_decode else decode_bench(m, dev)
         train = None if a.no_train else train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms)
         model = None if a.no_model else model_bench(dev)
+        decode_model = None if a.no_decode_model else decode_model_bench(dev, total=a.decode_model_steps)
 
     ms_per_step = wall * 1e3 / a.steps
     tokens = B * T
@@ -400,6 +446,8 @@ def main():
         rec["decode"] = decode
     if model is not None:
         rec["model"] = model
+    if decode_model is not None:
+        rec["decode_model"] = decode_model
     if train is not None:
         rec["train"] = train
     if not a.no_cpu:

@@ -6,8 +6,9 @@
 namespace sdmrt {
 
 // sdm_rt_address: one thread per (token, head).  Grid: x = token tiles of 64, y = head.  MODE 1 and 2: the tile is
-// addressed by the wave on the matrix cores (address_wave; 2 = no masked candidate), MODE 0: per thread with the
-// sub-keys staged in LDS (address_one).
+// addressed by the wave on the matrix cores (address_wave; 2 = no masked candidate), MODE 3 and 4 likewise with 64
+// sub-keys per half (two sub-key tiles; 4 = no masked candidate), MODE 0: per thread with the sub-keys staged in
+// LDS (address_one).
 template <int HALF, int CAP, typename InT, int MODE>
 __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   extern __shared__ float kn[];   // [2][n_sub][HALF] (per-thread path)
@@ -28,7 +29,8 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
   int slot[CAP];
   float w[CAP], sc[CAP];
   if constexpr (MODE > 0) {
-    address_wave<HALF, CAP, InT, MODE == 2>(a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
+    address_wave<HALF, CAP, InT, MODE == 2 || MODE == 4, (MODE >= 3 ? 64 : 32)>(
+        a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
                                      static_cast<int>(min<int64_t>(64, N - n0)), gate, slot, w, sc);
     if (n >= N) return;
   } else {
@@ -67,6 +69,12 @@ struct AddressLaunch {
         if (full_grid(p)) go<8, 2>(p, a, st);
         else if (p.cap == 8) go<8, 1>(p, a, st);
         else go<16, 1>(p, a, st);
+        return check_launch("address");
+      }
+      if (use_mf64(p)) {   // 64 sub-keys per half: no masked candidate when n_sub = 64 and c1 = kk = CAP
+        const bool full = p.n_sub == 64 && p.c1 == p.cap && p.kk == p.cap;
+        if (p.cap == 8) full ? go<8, 4>(p, a, st) : go<8, 3>(p, a, st);
+        else full ? go<16, 4>(p, a, st) : go<16, 3>(p, a, st);
         return check_launch("address");
       }
     }

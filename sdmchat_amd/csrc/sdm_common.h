@@ -388,10 +388,23 @@ __host__ __device__ constexpr int n_pairs(int cap) {
 //   14..17: 15 - ra, 10..13: 15 - rb, 5..9: 31 - i1, 0..4: 31 - i2
 // so plain double order is (mean score descending, then (ra, rb) ascending), and the field names the slot.  Keys
 // of invalid candidates get the high word 0x00100000: a normal double below every real key.
-template <int FS>
+// With 64 sub-keys per half (NS = 64) the index fields are 6 bits wide and every field sits one place higher per
+// extra index bit: a half key clears its low 21 bits (scores closer than 2^-29 tie), half 2's index is at bits 1..6
+// and half 1's at 7..12, the ranks at 13..16 and 17..20; a grid key's low 20 bits hold 16..19: 15 - ra,
+// 12..15: 15 - rb, 6..11: 63 - i1, 0..5: 63 - i2.  KeyLayout<NS> gives the positions for either.
+template <int NS>
+struct KeyLayout {
+  static_assert(NS == 32 || NS == 64, "32 or 64 sub-keys per half");
+  static constexpr int IB = NS == 64 ? 6 : 5;       // index field width
+  static constexpr int FS2 = 1, FS1 = 1 + IB;       // index fields of a half key (second half, first half)
+  static constexpr int RS2 = 1 + 2 * IB, RS1 = 5 + 2 * IB;   // rank fields of a ranked half key
+  static constexpr uint32_t kClear = ~((1u << (2 * IB + 9)) - 1u);   // the value part of a half key's low word
+  static constexpr unsigned long long kGridFields = (1ull << (2 * IB + 8)) - 1ull;
+};
+template <int FS, int NS = 32>
 __device__ __forceinline__ double half_key(float a, double inv, int i) {   // s = a * inv
   const unsigned long long b = __double_as_longlong(fma(static_cast<double>(a), inv, 6.0));
-  const uint32_t lo = (static_cast<uint32_t>(b) & 0xfff80000u) | (static_cast<uint32_t>(31 - i) << FS);
+  const uint32_t lo = (static_cast<uint32_t>(b) & KeyLayout<NS>::kClear) | (static_cast<uint32_t>(NS - 1 - i) << FS);
   return __longlong_as_double((b & 0xffffffff00000000ull) | lo);
 }
 __device__ __forceinline__ double key_or(double k, uint32_t bits) {
@@ -400,9 +413,10 @@ __device__ __forceinline__ double key_or(double k, uint32_t bits) {
 __device__ __forceinline__ double key_invalid(double k) {
   return __longlong_as_double((0x00100000ull << 32) | (__double_as_longlong(k) & 0xffffffffull));
 }
-// the mean score of a grid key, to within 2^-32
+// the mean score of a grid key, to within 2^-32 (2^-30 with 64 sub-keys)
+template <int NS = 32>
 __device__ __forceinline__ float grid_score(double k) {
-  const double v = __longlong_as_double(__double_as_longlong(k) & ~0x3ffffull);
+  const double v = __longlong_as_double(__double_as_longlong(k) & ~KeyLayout<NS>::kGridFields);
   return static_cast<float>(fma(v, 0.5, -6.0));
 }
 
@@ -482,12 +496,13 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 // of both address rows
 template <int HALF, typename InT, bool FULL>
 __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf, const InT* z0, int64_t zstride,
-                                                int rows, floatx16 (&acc)[2], float (&inv)[2]) {
+                                                int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0) {
   constexpr int S = HALF / 2;
   const int l = threadIdx.x & 63;
   const int kb = l >> 5, jl = l & 31;
+  const int kr = kofs + jl;   // this lane's sub-key row (kofs: the sub-key tile, 0 or 32)
   float ka[S], zb[2][S], ab[S];
-  load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + kb * S, ka);
+  load_vals<S, float>(g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + kb * S, ka);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int row = min(32 * t + jl, rows - 1);
@@ -504,7 +519,7 @@ __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf
 #pragma unroll
     for (int s = 0; s < S; ++s) ks = fmaf(ka[s], ka[s], ks);
     const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-    const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
+    const float kinv = (FULL || kr < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
 #pragma unroll
     for (int s = 0; s < S; ++s) ka[s] *= kinv;
   }
@@ -532,7 +547,7 @@ __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf
 // 32..63 feed zeros).
 template <int HALF, bool FULL>
 __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
-                                                 int rows, floatx16 (&acc)[2], float (&inv)[2]) {
+                                                 int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0) {
   static_assert(HALF % 8 == 0, "bfloat16 scoring feeds 8 dims per lane");
   constexpr int Q = (HALF + 15) / 16;
   const int l = threadIdx.x & 63;
@@ -541,7 +556,8 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
   const int d0 = hf * HALF + 8 * kb;   // first dim of the address this lane feeds
   float ka[Q][8], ab[Q][8];
   uint4 zr[2][Q];
-  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(jl, g.n_sub - 1)) * HALF + 8 * kb;
+  const int kr = kofs + jl;   // this lane's sub-key row (kofs: the sub-key tile, 0 or 32)
+  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + 8 * kb;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
 #pragma unroll
@@ -570,7 +586,7 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
 #pragma unroll
       for (int e = 0; e < 8; ++e) ks = fmaf(ka[q][e], ka[q][e], ks);
     const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-    const float kinv = (FULL || jl < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
+    const float kinv = (FULL || kr < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
@@ -633,42 +649,55 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
 
 // Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
 // clamped; their lanes' outputs are unspecified): the selection of address_one on offset keys, scores within 2^-31
-// of float rounding.  FULL: n_sub = 32 and c1 = kk = CAP (no candidate is masked).  All 64 lanes of the wave must
-// call it.
-template <int HALF, int CAP, typename InT, bool FULL>
+// of float rounding (2^-29 with NS = 64).  NS: 32 sub-keys per half (n_sub <= 32) or 64 (n_sub <= 64: two sub-key
+// tiles scored in turn, each tile's CAP best merged into the half's).  FULL: n_sub = NS and c1 = kk = CAP (no
+// candidate is masked).  All 64 lanes of the wave must call it.
+template <int HALF, int CAP, typename InT, bool FULL, int NS = 32>
 __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
                                              float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
+  using KL = KeyLayout<NS>;
   const int kb = (threadIdx.x & 63) >> 5;
   double hk[2][CAP];   // ranked half keys
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    floatx16 acc[2];
-    float inv[2];
-    if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv);
-    else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv);
-    // after the swap below lane l holds every score of address row l
-    const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
-    double c[32];
+    double best[CAP];   // the half's CAP best keys so far, descending
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]), false,
-                                                       false);
-      const int i0 = 8 * (r / 4) + (r % 4);
-      if (hf == 0) {
-        c[r] = half_key<6>(__uint_as_float(sw[0]), dinv, i0);
-        c[16 + r] = half_key<6>(__uint_as_float(sw[1]), dinv, i0 + 4);
-      } else {
-        c[r] = half_key<1>(__uint_as_float(sw[0]), dinv, i0);
-        c[16 + r] = half_key<1>(__uint_as_float(sw[1]), dinv, i0 + 4);
+    for (int tile = 0; tile < NS / 32; ++tile) {   // sub-keys 32 tile ... 32 tile + 31
+      floatx16 acc[2];
+      float inv[2];
+      if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
+      else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
+      // after the swap below lane l holds every score of address row l
+      const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
+      double c[32];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]),
+                                                         false, false);
+        const int i0 = 32 * tile + 8 * (r / 4) + (r % 4);
+        if (hf == 0) {
+          c[r] = half_key<KL::FS1, NS>(__uint_as_float(sw[0]), dinv, i0);
+          c[16 + r] = half_key<KL::FS1, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+        } else {
+          c[r] = half_key<KL::FS2, NS>(__uint_as_float(sw[0]), dinv, i0);
+          c[16 + r] = half_key<KL::FS2, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+        }
+        if (!FULL) {   // sub-keys past n_sub are never picked
+          if (i0 >= g.n_sub) c[r] = key_invalid(c[r]);
+          if (i0 + 4 >= g.n_sub) c[16 + r] = key_invalid(c[16 + r]);
+        }
       }
-      if (!FULL) {   // sub-keys past n_sub are never picked
-        if (i0 >= g.n_sub) c[r] = key_invalid(c[r]);
-        if (i0 + 4 >= g.n_sub) c[16 + r] = key_invalid(c[16 + r]);
+      top_k_desc<CAP, 32>(c);
+      if (tile == 0) {
+#pragma unroll
+        for (int r = 0; r < CAP; ++r) best[r] = c[r];
+      } else {
+        merge_top_desc<CAP>(best, c);
       }
     }
-    top_k_desc<CAP, 32>(c);
 #pragma unroll
-    for (int r = 0; r < CAP; ++r) hk[hf][r] = key_or(c[r], static_cast<uint32_t>(15 - r) << (hf == 0 ? 15 : 11));
+    for (int r = 0; r < CAP; ++r)
+      hk[hf][r] = key_or(best[r], static_cast<uint32_t>(15 - r) << (hf == 0 ? KL::RS1 : KL::RS2));
   }
   // combine over the dominance-pruned grid (see address_one)
   auto cell = [&](int ra, int rb) {
@@ -713,12 +742,13 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
   int si[CAP];
 #pragma unroll
   for (int p = 0; p < CAP; ++p) {
-    cv[p] = grid_score(pc[p]);
+    cv[p] = grid_score<NS>(pc[p]);
     const uint32_t f = static_cast<uint32_t>(__double_as_longlong(pc[p]));
-    if (FULL) {
-      si[p] = 1023 - static_cast<int>(f & 1023u);   // (31 - i1) * 32 + (31 - i2) = 1023 - slot
+    if (FULL) {   // (NS - 1 - i1) * NS + (NS - 1 - i2) = NS^2 - 1 - slot
+      si[p] = NS * NS - 1 - static_cast<int>(f & static_cast<uint32_t>(NS * NS - 1));
     } else {
-      const int i1 = 31 - static_cast<int>((f >> 5) & 31u), i2 = 31 - static_cast<int>(f & 31u);
+      const int i1 = NS - 1 - static_cast<int>((f >> KL::IB) & static_cast<uint32_t>(NS - 1));
+      const int i2 = NS - 1 - static_cast<int>(f & static_cast<uint32_t>(NS - 1));
       si[p] = min(i1 * g.n_sub + i2, g.n_sub * g.n_sub - 1);
     }
   }
@@ -995,6 +1025,8 @@ int by_half(int half, Args&&... args) {
 // the matrix-core addressing covers half widths 8, 16, 32 and up to 32 sub-keys per half
 constexpr bool mf_half(int half) { return half == 8 || half == 16 || half == 32; }
 inline bool use_mf(const Plan& p) { return mf_half(p.half) && p.n_sub <= 32; }
+// the addressing entry point also takes 64 sub-keys per half on the matrix cores (two sub-key tiles)
+inline bool use_mf64(const Plan& p) { return mf_half(p.half) && p.n_sub > 32 && p.n_sub <= 64; }
 // no masked candidate: 32 sub-keys per half and 8 picks from the top 8 of each half
 inline bool full_grid(const Plan& p) { return use_mf(p) && p.n_sub == 32 && p.c1 == 8 && p.kk == 8; }
 

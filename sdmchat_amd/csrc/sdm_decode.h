@@ -313,11 +313,12 @@ __device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale,
                                              float gate, int& slot, float& w) {
   const int lane = threadIdx.x & 63;
   const int hf = lane >> 5, i = lane & 31;
-  double c = hf == 0 ? half_key<6>(sc[i], static_cast<double>(inv[0]), i)
-                     : half_key<1>(sc[32 + i], static_cast<double>(inv[1]), i);
+  using KL = KeyLayout<32>;
+  double c = hf == 0 ? half_key<KL::FS1>(sc[i], static_cast<double>(inv[0]), i)
+                     : half_key<KL::FS2>(sc[32 + i], static_cast<double>(inv[1]), i);
   if (!FULL && i >= g.n_sub) c = key_invalid(c);   // sub-keys past n_sub are never picked
   c = __longlong_as_double(static_cast<long long>(sort_lanes_desc<32>(static_cast<unsigned long long>(__double_as_longlong(c)), lane)));
-  const double hk = i < 16 ? key_or(c, static_cast<uint32_t>(15 - i) << (hf == 0 ? 15 : 11)) : c;   // ranked
+  const double hk = i < 16 ? key_or(c, static_cast<uint32_t>(15 - i) << (hf == 0 ? KL::RS1 : KL::RS2)) : c;   // ranked
   // grid pair of this lane: pairs (ra, rb) with (ra + 1)(rb + 1) <= CAP, row by row
   int x = lane, ra = -1, rb = 0;
 #pragma unroll

@@ -46,18 +46,18 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x
 // ---------------------------------------------------------------------------------------------------------------
 // table read: the weighted sum of the picked rows of per-head value tables (TrainedSdm.forward's embedding_bag,
 // track4_onesdm_models.py:448-455): out[n][h * dh + c] = sum_j w[n][h][j] * values[h][slot[n][h][j]][c] in float32,
-// picks in order.  One wave per (token, head); lane l takes columns 4l, 4l + 256, ... (dh a multiple of 4).
+// picks in order.  One workgroup of 256 threads per (token, head); thread i takes columns 4i ... 4i + 3 of every
+// 1,024 (dh a multiple of 4), with the loads of all picks issued before any use: one round trip for the picks, one
+// for the rows.
 template <int KP, typename VT, typename OutT>
 __global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restrict__ slots,
                                                          const float* __restrict__ wts,
                                                          const VT* __restrict__ values, OutT* __restrict__ out,
                                                          int64_t out_stride, int B, int T, int H, int M, int dh,
                                                          int kk) {
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wave >= static_cast<int64_t>(B) * T * H) return;   // whole waves
-  const int64_t n = wave / H;
-  const int h = static_cast<int>(wave - n * H);
+  const int64_t item = blockIdx.x;   // (token, head)
+  const int64_t n = item / H;
+  const int h = static_cast<int>(item - n * H);
   const int b = static_cast<int>(n / T);
   const int t = static_cast<int>(n - static_cast<int64_t>(b) * T);
   const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
@@ -69,17 +69,10 @@ __global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restri
     w[j] = j < kk ? wts[pb + j] : 0.f;
   }
   const VT* tab = values + static_cast<int64_t>(h) * M * dh;
-  for (int c0 = 4 * lane; c0 < dh; c0 += 256) {
+  for (int c0 = 4 * static_cast<int>(threadIdx.x); c0 < dh; c0 += 1024) {
     float v[KP][4];
 #pragma unroll
-    for (int j = 0; j < KP; ++j) {
-      if (j < kk) {
-        load_vals<4, VT>(tab + static_cast<int64_t>(sl[j]) * dh + c0, v[j]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[j][e] = 0.f;
-      }
-    }
+    for (int j = 0; j < KP; ++j) load_vals<4, VT>(tab + static_cast<int64_t>(sl[j]) * dh + c0, v[j]);   // weight 0 past kk
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
@@ -171,8 +164,7 @@ int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float
   if (out_row_stride < static_cast<int64_t>(p.H) * p.dh)
     return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t waves = static_cast<int64_t>(p.B) * p.T * p.H;
-  const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+  const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(p.B) * p.T * p.H);
 #define SDM_RT_TABLE(KP, VT, OT)                                                                                   \
   hipLaunchKernelGGL((table_read_kernel<KP, VT, OT>), dim3(blocks), dim3(256), 0, st, slots, weights,             \
                      static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, p.H, p.M, p.dh, \

@@ -87,3 +87,30 @@ def test_full_bench_shape_picks():
     diff = pick_diffs(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), si, gsi)
     say("addresses whose picks differ from the oracle's (all at ties):", int(diff.sum()), "of", diff.size)
     np.testing.assert_allclose(_as_tokens(scores), sv, atol=3e-7)
+
+
+@pytest.mark.parametrize("n_sub,k,H,half", [(64, 16, 1, 16), (64, 8, 2, 16), (48, 12, 2, 16), (40, 16, 3, 8),
+                                            (64, 16, 2, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_64_subkey_addressing_matches_oracle(n_sub, k, H, half, dtype):
+    """More than 32 sub-keys per half (the TrainedSdm table of the FULL model: 64, k 16) on the matrix cores, two
+    sub-key tiles per half: picks in the oracle's order up to ties, scores and weights."""
+    rng = np.random.Generator(np.random.PCG64(60 + n_sub + k))
+    B, T, d_a = 2, 150, 2 * half
+    z = bf16_round(rng.standard_normal((B, T, H * d_a)))
+    p = dict(keys1=rng.standard_normal((H, n_sub, half)).astype(np.float32),
+             keys2=rng.standard_normal((H, n_sub, half)).astype(np.float32),
+             addr_b=(rng.standard_normal((H, d_a)) * 0.3).astype(np.float32),
+             log_scale=rng.uniform(1.5, 2.5, H).astype(np.float32), decay=np.zeros(H, np.float32),
+             onorm_w=np.ones((H, 8), np.float32), gate_bias=np.zeros(H, np.float32))
+    say("64-sub-key addressing", n_sub, k, H, half, dtype)
+    slots, scores, weights = gpu_address(z, p, k, dtype=dtype)
+    zz = z.astype(np.float64).reshape(B * T, H, d_a) + p["addr_b"]
+    k1, k2 = p["keys1"].astype(np.float64), p["keys2"].astype(np.float64)
+    sv, si = O.pk_address(zz, k1, k2, k)
+    gsi = _as_tokens(slots)
+    same = ~pick_diffs(zz, k1, k2, si, gsi)
+    say(f"  {int((~same).sum())} of {same.size} addresses differ from the oracle's picks (all at ties)")
+    np.testing.assert_allclose(_as_tokens(scores), sv, atol=1e-6)
+    w = O.address_weights(sv, p["log_scale"].astype(np.float64))
+    np.testing.assert_allclose(_as_tokens(weights)[same], w[same], atol=2e-6, rtol=2e-6)
