@@ -7,19 +7,21 @@ per head, k=8, bf16 activations and weights, float32 memory state, synthetic see
 step is one module forward (fused RMSNorm, fused input projection GEMM, SDM core, output map) over the 16,384
 tokens, with inputs already resident in HBM; value = 16,384 * K / the wall time of K steps.  Prints one JSON line.
 
-roofline: the SDM core (sdm_rt_forward: plan_kernel, scan_kernel, finish_kernel, from the projection outputs to
-the read-out before wo) is HBM-bound.  Its algorithmic traffic is 6,168 B per token (kz, qz, V in bf16 =
+roofline: the SDM core (sdm_rt_forward: plan_kernel and scan_kernel, from the projection outputs to the read-out
+before wo) is HBM-bound.  Its algorithmic traffic is 6,168 B per token (kz, qz, V in bf16 =
 3 x 1,536 B, gate logits 24 B, read-out 1,536 B) plus 104,544 B of parameters per call: 101,161,056 B at this
 shape.  achieved = that / the core's median call time (5 warm calls, then the median of 50, each bracketed by HIP
 events on the stream the kernels run on).  traffic = measured HBM bytes per call (rocprofv3 FETCH_SIZE +
-WRITE_SIZE summed over the three kernels, scaled by the same counters' reading for a device copy of known size),
+WRITE_SIZE summed over the core's kernels, scaled by the same counters' reading for a device copy of known size),
 read from profiles/sdm_core_traffic_b8_t2048.txt when present (null otherwise).
 
 module: the whole layer is MFMA-bound (79.6 GFLOP per call against 55.2 MB): module.frac = max(bytes / 8 TB/s,
 FLOPs / 2.5 PFLOP/s) / module time.  copy_gbs: a 1 GiB device-to-device copy, for context.
 
 cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle/sdm_torch32.py, the reference's
-dense chunk algorithm) on the same workload, all host cores, one warm call then best of three.
+dense chunk algorithm) on the same workload, all host cores, one warm call then best of three; also at config 1
+(B=1, T=256), with the CPU model.  In the same leg the oracle checks the whole models: model.logit_agreement is the
+float32 GPU logits of both full-width models (B=1, T=64) against the fp64 oracle (oracle.sdm_fp64.model_forward).
 
 decode: the decode step (sdm_rt_decode_step, one token for each of 64 streams, 12 heads, float32 state carried in
 place) timed as a HIP graph of 64 steps replayed 513 times, so the state runs through 32,832 positions; before every
@@ -33,6 +35,12 @@ model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12
 "trained_sdm" = a TrainedSdm of 4,096 slots, one head of width 768, k=16 (config 4); bf16 weights and activations,
 synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm.
 --no-model skips it.
+
+decode_model: the FULL model (the trained_sdm arm above) decoding 64 independent streams, one fresh random token
+per stream per step, through 32,832 positions (the survey's config 5), bf16 weights, float32 state carried in
+place; steps run as HIP graphs of 64 (DecodeGraph), the tokens refilled between replays; us_per_step = replay time
+/ 64, reported overall (median), as tokens/s (64 / us_per_step) and at positions 0, 1,024, 8,192 and 32,768.
+--no-decode-model skips it; --decode-model-steps N shortens it.
 
 train: the backward -- the core's training forward (sdm_rt_forward_train: the forward plus the saved picks, weights,
 scores, read and denominators) and backward (sdm_rt_backward) on the layer's bf16 projections, median of 20 calls,
@@ -75,8 +83,20 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline():
-    import numpy as np
+    """The float32 CPU restatement of the reference forward at the bench shape (and at config 1, B1 T256), all host
+    cores, one warm call then best of three."""
     import torch
 
     from oracle import sdm_torch32 as R
@@ -86,18 +106,69 @@ def cpu_baseline():
     torch.set_num_threads(threads)
     cfg = S.layer_cfg(d=D, heads=H, n_sub=N_SUB, d_a=D_A, k=K)
     p = {n: torch.from_numpy(v) for n, v in S.layer_params(cfg, seed=0).items()}
-    x = torch.from_numpy(S.layer_input(B, T, D, seed=1))
-    best = float("inf")
-    with torch.no_grad():
-        R.forward(x, p, cfg)
-        for _ in range(3):
-            t0 = time.perf_counter()
+
+    def best_of_3(x):
+        best = float("inf")
+        with torch.no_grad():
             R.forward(x, p, cfg)
-            best = min(best, time.perf_counter() - t0)
-    del np
+            for _ in range(3):
+                t0 = time.perf_counter()
+                R.forward(x, p, cfg)
+                best = min(best, time.perf_counter() - t0)
+        return best
+
+    best = best_of_3(torch.from_numpy(S.layer_input(B, T, D, seed=1)))
+    best1 = best_of_3(torch.from_numpy(S.layer_input(1, 256, D, seed=1)))
     return {"value": round(B * T / best, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": _cpu_model(), "config1_tokens_per_s": round(256 / best1, 1),
             "sample": f"full workload B={B} T={T} in float32 (chunk 128), torch {torch.__version__} on the host CPU, "
-                      f"1 warm call then best of 3 ({best:.2f} s per call)"}
+                      f"1 warm call then best of 3 ({best:.2f} s per call); config 1 (B=1, T=256) likewise "
+                      f"({best1 * 1e3:.1f} ms per call)"}
+
+
+def logit_agreement(dev, T_agree=64):
+    """The whole models' float32 logits on the GPU against the fp64 oracle (oracle.sdm_fp64.model_forward) at full
+    width, B=1, T=T_agree: the oracle takes the GPU's picks where two slots' fp64 scores are within 1e-5 (float32
+    rounding of the layers' inputs may resolve such near ties the other way)."""
+    import numpy as np
+    import torch
+
+    from oracle import sdm_fp64 as O
+    from sdmchat_amd import synthetic as S
+
+    out = {}
+    idx = S.model_tokens(1, T_agree, seed=41)
+    for name in ("swiglu", "trained_sdm"):
+        m = S.full_model(name)
+        p = {n: v.detach().double().numpy() for n, v in m.state_dict().items()}
+        m = m.to(dev).eval()
+        for mm in m.mems:
+            mm.keep_picks = True
+        with torch.no_grad():
+            got = m(torch.from_numpy(idx).to(dev)).double().cpu().numpy()
+        forced = {}
+        for i, mm in enumerate(m.mems):
+            kk = min(mm.k, min(mm.k, mm.n_sub) ** 2)
+            forced[("mem", i)] = tuple(s_[..., :kk].permute(0, 2, 1, 3).reshape(T_agree, mm.h, kk).cpu().numpy()
+                                       for s_ in mm.last_picks)
+        for i, sd in enumerate(getattr(m, "sdms", [])):
+            forced[("sdm", i)] = sd.last_si.cpu().numpy()
+        cfg = dict(layers=m.n_layers, heads=m.mems[0].h, d_a=m.mems[0].d_a, k=m.mems[0].k, ffn=m.ffn,
+                   adopt_tol=1e-5, adopt_log=[])
+        if m.ffn == "sdm":
+            cfg.update(sdm_heads=m.sdms[0].h, sdm_d_a=m.sdms[0].d_a, sdm_k=m.sdms[0].k)
+        want = O.model_forward(idx, p, cfg, forced=forced)
+        scale = np.abs(want).max()
+        out[name] = {"max_abs_err_over_scale": float(f"{np.abs(got - want).max() / scale:.3g}"),
+                     "top1_agreement": round(float((got.argmax(-1) == want.argmax(-1)).mean()), 4),
+                     "ties_taken": int(sum(cfg["adopt_log"]))}
+        log(f"logit agreement {name}: {out[name]}")
+        del m
+        torch.cuda.empty_cache()
+    out["workload"] = (f"float32 GPU logits of the full-width models (d 768, 12 layers, vocabulary 32,768) against "
+                       f"the fp64 oracle, B=1, T={T_agree}; ties_taken: addresses where the oracle took the GPU's "
+                       "pick (fp64 score gap < 1e-5)")
+    return out
 
 
 def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
@@ -160,24 +231,15 @@ def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
 
 
 def model_bench(dev):
-    """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms, and the bf16 logits' agreement with
-    float32 (see the module doc)."""
+    """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms (see the module doc)."""
     import torch
 
     from sdmchat_amd import synthetic as S
 
     out = {}
     idx = torch.from_numpy(S.model_tokens(B, T, seed=11)).to(dev)
-    agree = {}
     for name in ("swiglu", "trained_sdm"):
-        m = S.full_model(name).to(dev).eval()
-        with torch.no_grad():   # bf16 logits against float32 ones on the same weights (B=1, T=512)
-            ref = m(idx[:1, :512]).float()
-            m = m.to(torch.bfloat16)
-            low = m(idx[:1, :512]).float()
-        agree[name] = {"max_abs_err_over_scale": round(float((low - ref).abs().max() / ref.abs().max()), 5),
-                       "top1_agreement": round(float((low.argmax(-1) == ref.argmax(-1)).float().mean()), 4)}
-        del ref, low
+        m = S.full_model(name).to(dev).to(torch.bfloat16).eval()
         with torch.no_grad():
             for _ in range(2):
                 m(idx)
@@ -192,14 +254,10 @@ def model_bench(dev):
                 ts.append(e0.elapsed_time(e1))
         ms = sorted(ts)[2]
         out[name] = {"ms": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
-        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s; bf16 vs fp32 "
-            f"{agree[name]}")
+        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
         del m
         torch.cuda.empty_cache()
     mf = S.MODEL_FULL
-    out["logit_agreement"] = dict(agree, workload="the same model in bfloat16 and in float32, B=1, T=512: max "
-                                  "|logit difference| / max |float32 logit|, and the fraction of positions whose "
-                                  "top logit agrees")
     out["workload"] = (f"OneSdmLM forward (logits): B={B} T={T}, vocabulary {mf['V']}, {mf['layers']} layers, "
                        f"d={mf['d']}, mixer {mf['heads']} heads M={mf['n_sub'] ** 2} k={mf['k']}; swiglu: hidden "
                        f"{mf['mlp_f']}; trained_sdm: 4,096 slots, 1 head, k=16; bf16")
@@ -453,6 +511,8 @@ def main():
     if not a.no_cpu:
         log("cpu baseline ...")
         rec["cpu_baseline"] = cpu_baseline()
+        if model is not None:   # the oracle as the checker of the whole model's logits
+            rec["model"]["logit_agreement"] = logit_agreement(dev)
     print(json.dumps(rec), flush=True)
 
 
