@@ -218,7 +218,8 @@ def decode_bench(m, dev, streams=64, graph_steps=64, replays=513):
             e1.record()
         torch.cuda.synchronize()
         us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
-        by_pos = {str(pos): round(float(us[pos // graph_steps]), 2) for pos in (0, 1024, 8192, 32768)}
+        by_pos = {str(pos): round(float(us[pos // graph_steps]), 2) for pos in (0, 1024, 8192, 32768)
+              if pos // graph_steps < replays}
         log(f"decode ({name}): {np.median(us):.2f} us per step (median over {replays} replays), by position {by_pos}")
         res[name] = (round(float(np.median(us)), 2), by_pos)
         del graph
@@ -379,6 +380,7 @@ def main():
     ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
+    ap.add_argument("--decode-replays", type=int, default=513, help="graph replays of the decode-step measurement")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model measurement")
     ap.add_argument("--no-decode-model", action="store_true", help="skip the whole-model decode measurement")
     ap.add_argument("--decode-model-only", action="store_true", help="only the whole-model decode (profiler runs)")
@@ -465,7 +467,7 @@ def main():
         big2 = torch.empty_like(big)
         copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
         del big, big2
-        decode = None if a.no_decode else decode_bench(m, dev)
+        decode = None if a.no_decode else decode_bench(m, dev, replays=a.decode_replays)
         train = None if a.no_train else train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms)
         model = None if a.no_model else model_bench(dev)
         decode_model = None if a.no_decode_model else decode_model_bench(dev, total=a.decode_model_steps)
