@@ -182,6 +182,24 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
                     const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                     void* stream);
 
+/* The residual add before an RMSNorm, fused with it (OneSdmLM.residual, track4_onesdm_models.py:540-546:
+ * x = x + layer(x), then the next layer's RMSNorm, track4_sdmllm_models.py:63-71): sum = cast_in(x + y), written to
+ * sum_out (it may be x itself), and out = the RMSNorm of sum as sdm_rt_rms_norm computes it.
+ *   x, y     [rows] of d values, dtype in_dtype, row strides in elements
+ *   sum_out  [rows] of d values, dtype in_dtype
+ *   out      [rows] of d values, dtype out_dtype */
+int sdm_rt_add_rms_norm(const void* x, int64_t x_row_stride, const void* y, int64_t y_row_stride,
+                        sdm_rt_dtype in_dtype, int64_t rows, int32_t d, const float* w, float eps,
+                        void* sum_out, int64_t sum_row_stride, void* out, int64_t out_row_stride,
+                        sdm_rt_dtype out_dtype, void* stream);
+
+/* SwiGLU's gate (track4_sdmllm_models.py:89-97: silu(gate(x)) * up(x)) on the output of one fused [gate | up]
+ * projection: out[r][c] = cast(cast(silu(g)) * u), g = gate_up[r][c], u = gate_up[r][f + c], silu(g) =
+ * g / (1 + exp(-g)) in float32, each product rounded as torch rounds it.
+ *   gate_up  [rows] of 2 f values, dtype, row stride >= 2 f;  out  [rows] of f values, dtype; f a multiple of 8 */
+int sdm_rt_silu_mul(const void* gate_up, int64_t gate_up_row_stride, sdm_rt_dtype dtype, int64_t rows, int32_t f,
+                    void* out, int64_t out_row_stride, void* stream);
+
 /* ---- training: forward with saved tensors, and the backward ------------------------------------------------
  * The reference trains RunTimeSdm through torch autograd of its chunked dense forward (RunTimeSdm.forward under
  * torch.utils.checkpoint, track4_onesdm_models.py:259-268).  These two entry points replace that autograd for the

@@ -108,6 +108,11 @@ SIGNATURES = {
                                          c_void_p, c_i64, ctypes.c_int, c_void_p]),
     "sdm_rt_rms_norm": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p,
                                        ctypes.c_float, c_void_p, c_i64, ctypes.c_int, c_void_p]),
+    "sdm_rt_add_rms_norm": (ctypes.c_int, [c_void_p, c_i64, c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32,
+                                           c_void_p, ctypes.c_float, c_void_p, c_i64, c_void_p, c_i64, ctypes.c_int,
+                                           c_void_p]),
+    "sdm_rt_silu_mul": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p, c_i64,
+                                       c_void_p]),
     "sdm_rt_forward_train": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
                                             c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
                                             ctypes.c_int, c_void_p,

@@ -397,6 +397,47 @@ class RmsNormFunction(torch.autograd.Function):
 
 
 # -- training: forward with saved tensors, backward, and the autograd Function -------------------------------------
+
+def add_rms_norm(x, y, w, eps=1e-6, out_dtype=None, inplace=True):
+    """The residual add and the next RMSNorm in one kernel: s = x + y (in x's dtype; written into x when
+    ``inplace``), returns (s, rms_norm(s, w, eps, out_dtype)) (OneSdmLM.residual's x + layer(x), then a norm)."""
+    if x.device.type != "cuda":
+        raise RuntimeError("add_rms_norm needs a ROCm device tensor")
+    if x.dtype not in _DT or y.dtype != x.dtype or x.shape != y.shape:
+        raise ValueError("add_rms_norm: x and y must have one shape and dtype (float32 or bfloat16)")
+    d = x.shape[-1]
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("add_rms_norm: x and y must be contiguous")
+    s = x if inplace else torch.empty_like(x)
+    out_dtype = out_dtype or x.dtype
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    wf = w.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    lib = _lib.load()
+    rows = x.numel() // d
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.sdm_rt_add_rms_norm(_ptr(x), d, _ptr(y), d, _DT[x.dtype], rows, d, _ptr(wf), float(eps), _ptr(s), d,
+                                 _ptr(out), d, _DT[out_dtype], ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return s, out
+
+
+def silu_mul(gate_up):
+    """SwiGLU's silu(g) * u on a fused [gate | up] projection [..., 2 f], with torch's roundings."""
+    if gate_up.device.type != "cuda" or gate_up.dtype not in _DT:
+        raise ValueError("silu_mul needs a float32 or bfloat16 ROCm tensor")
+    f2 = gate_up.shape[-1]
+    g2 = gate_up.reshape(-1, f2)
+    if g2.stride(1) != 1:
+        g2 = g2.contiguous()
+    out = torch.empty(gate_up.shape[:-1] + (f2 // 2,), dtype=gate_up.dtype, device=gate_up.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(gate_up.device).cuda_stream
+    rc = lib.sdm_rt_silu_mul(_ptr(g2), g2.stride(0), _DT[gate_up.dtype], g2.shape[0], f2 // 2, _ptr(out), f2 // 2,
+                             ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return out
+
+
 def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape

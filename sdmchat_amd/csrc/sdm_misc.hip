@@ -1,14 +1,18 @@
-// sdm_misc.hip -- the input norm (sdm_rt_rms_norm), the table read of TrainedSdm (sdm_rt_table_read) and the
-// addressing entry point (sdm_rt_address).
+// sdm_misc.hip -- the input norm (sdm_rt_rms_norm, and with the residual add before it sdm_rt_add_rms_norm),
+// SwiGLU's gate (sdm_rt_silu_mul), the table read of TrainedSdm (sdm_rt_table_read) and the addressing entry point
+// (sdm_rt_address).
 #include "sdm_common.h"
 
 namespace sdmrt {
 
-// rms_norm: one wave per row; lanes take 8 consecutive values at a time
-template <typename InT, typename OutT>
-__global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x, int64_t x_stride,
-                                                       OutT* __restrict__ out, int64_t out_stride,
-                                                       const float* __restrict__ w, int64_t rows, int d, float eps) {
+// rms_norm: one wave per row; lanes take 8 consecutive values at a time.  ADD: the row is x + y rounded to the input
+// type (a residual add), which is also written to sum (in place over x is allowed: each value is read and written
+// by the same lane).
+template <typename InT, typename OutT, bool ADD>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const InT* x, int64_t x_stride, const InT* y, int64_t y_stride,
+                                                       InT* sum, int64_t sum_stride, OutT* __restrict__ out,
+                                                       int64_t out_stride, const float* __restrict__ w, int64_t rows,
+                                                       int d, float eps) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;   // whole waves
@@ -21,6 +25,13 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x
     const int c = 8 * (lane + 64 * k);
     if (c < d) {
       load_vals<8, InT>(src + c, v[k]);
+      if constexpr (ADD) {
+        float u[8];
+        load_vals<8, InT>(y + row * y_stride + c, u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = to_f32(from_f32<InT>(v[k][e] + u[e]));   // x + y in the input type
+        store_vals<8, InT>(sum + row * sum_stride + c, v[k]);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
     }
@@ -41,6 +52,27 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* __restrict__ x
       store_vals<8, OutT>(dst + c, o);
     }
   }
+}
+
+// SwiGLU's gate: out = silu(g) * u with g, u the two halves of a row of the fused [gate | up] projection, each
+// product rounded as torch rounds silu(g) and then the product (x / (1 + exp(-x)) in float32, then the cast)
+template <typename T>
+__global__ void __launch_bounds__(256) silu_mul_kernel(const T* __restrict__ gu, int64_t gu_stride, T* __restrict__ out,
+                                                       int64_t out_stride, int64_t rows, int f) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;   // 8 values per thread
+  const int64_t per_row = f;
+  const int64_t row = i / per_row;
+  const int c = static_cast<int>(i - row * per_row);
+  if (row >= rows) return;
+  float g[8], u[8], o[8];
+  load_vals<8, T>(gu + row * gu_stride + c, g);
+  load_vals<8, T>(gu + row * gu_stride + f + c, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float s = to_f32(from_f32<T>(g[e] / (1.f + expf(-g[e]))));
+    o[e] = s * u[e];
+  }
+  store_vals<8, T>(out + row * out_stride + c, o);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -104,8 +136,8 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
 #define SDM_RT_NORM(IT, OT)                                                                                     \
-  hipLaunchKernelGGL((rms_norm_kernel<IT, OT>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x),      \
-                     x_row_stride, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  hipLaunchKernelGGL((rms_norm_kernel<IT, OT, false>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x), \
+                     x_row_stride, nullptr, 0, nullptr, 0, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
   if (in_dtype == SDM_RT_BF16) {
     if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(bf16_t, bf16_t);
     else SDM_RT_NORM(bf16_t, float);
@@ -115,6 +147,60 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
   }
 #undef SDM_RT_NORM
   return check_launch("rms_norm");
+}
+
+int sdm_rt_add_rms_norm(const void* x, int64_t x_row_stride, const void* y, int64_t y_row_stride,
+                        sdm_rt_dtype in_dtype, int64_t rows, int32_t d, const float* w, float eps, void* sum_out,
+                        int64_t sum_row_stride, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
+                        void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype(in_dtype, "in_dtype"))) return rc;
+  if ((rc = check_dtype(out_dtype, "out_dtype"))) return rc;
+  if (rows < 0 || d < 1) return set_err(SDM_RT_EINVAL, "rows must be >= 0 and d >= 1");
+  if (d % 8 != 0 || d > 2048) return set_err(SDM_RT_EUNSUPPORTED, "d = %d must be a multiple of 8 up to 2048", d);
+  if (rows == 0) return SDM_RT_OK;
+  if (!x || !y || !w || !sum_out || !out) return set_err(SDM_RT_EINVAL, "x, y, w, sum_out and out must not be NULL");
+  if (x_row_stride < d || y_row_stride < d || sum_row_stride < d || out_row_stride < d)
+    return set_err(SDM_RT_EINVAL, "row strides must be >= d");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+#define SDM_RT_ADD_NORM(IT, OT)                                                                                   \
+  hipLaunchKernelGGL((rms_norm_kernel<IT, OT, true>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x),   \
+                     x_row_stride, static_cast<const IT*>(y), y_row_stride, static_cast<IT*>(sum_out),              \
+                     sum_row_stride, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  if (in_dtype == SDM_RT_BF16) {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_ADD_NORM(bf16_t, bf16_t);
+    else SDM_RT_ADD_NORM(bf16_t, float);
+  } else {
+    if (out_dtype == SDM_RT_BF16) SDM_RT_ADD_NORM(float, bf16_t);
+    else SDM_RT_ADD_NORM(float, float);
+  }
+#undef SDM_RT_ADD_NORM
+  return check_launch("add_rms_norm");
+}
+
+int sdm_rt_silu_mul(const void* gate_up, int64_t gate_up_row_stride, sdm_rt_dtype dtype, int64_t rows, int32_t f,
+                    void* out, int64_t out_row_stride, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype(dtype, "dtype"))) return rc;
+  if (rows < 0 || f < 1) return set_err(SDM_RT_EINVAL, "rows must be >= 0 and f >= 1");
+  if (f % 8 != 0) return set_err(SDM_RT_EUNSUPPORTED, "f = %d must be a multiple of 8", f);
+  if (rows == 0) return SDM_RT_OK;
+  if (!gate_up || !out) return set_err(SDM_RT_EINVAL, "gate_up and out must not be NULL");
+  if (gate_up_row_stride < 2 * static_cast<int64_t>(f) || out_row_stride < f)
+    return set_err(SDM_RT_EINVAL, "gate_up_row_stride must be >= 2 f and out_row_stride >= f");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t threads = rows * (f / 8);
+  const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
+  if (dtype == SDM_RT_BF16)
+    hipLaunchKernelGGL((silu_mul_kernel<bf16_t>), dim3(blocks), dim3(256), 0, st, static_cast<const bf16_t*>(gate_up),
+                       gate_up_row_stride, static_cast<bf16_t*>(out), out_row_stride, rows, f);
+  else
+    hipLaunchKernelGGL((silu_mul_kernel<float>), dim3(blocks), dim3(256), 0, st, static_cast<const float*>(gate_up),
+                       gate_up_row_stride, static_cast<float*>(out), out_row_stride, rows, f);
+  return check_launch("silu_mul");
 }
 int sdm_rt_address(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* z, int64_t z_row_stride,
                    const void* gate_logits, int64_t gate_row_stride, sdm_rt_dtype in_dtype, int32_t* slot_out,

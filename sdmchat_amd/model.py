@@ -33,16 +33,29 @@ def _norm(x, norm):
 
 
 class SwiGLU(nn.Module):
-    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97), on dense GEMMs."""
+    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97).  Inference runs gate and up as one GEMM on their
+    stacked weights and silu(g) * u as one kernel (core.silu_mul, torch's roundings); with autograd recording, the
+    reference's ops."""
 
     def __init__(self, d, f):
         super().__init__()
         self.gate = nn.Linear(d, f, bias=False)
         self.up = nn.Linear(d, f, bias=False)
         self.down = nn.Linear(f, d, bias=False)
+        self._gu = None
+
+    def _gate_up(self):
+        """[gate; up] stacked, cached until either changes."""
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in (self.gate.weight, self.up.weight))
+        if self._gu is None or self._gu[0] != key:
+            self._gu = (key, torch.cat([self.gate.weight.detach(), self.up.weight.detach()], 0))
+        return self._gu[1]
 
     def forward(self, x):
-        return self.down(F.silu(self.gate(x)) * self.up(x))
+        if (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))) \
+                or x.device.type != "cuda" or torch.is_autocast_enabled("cuda"):
+            return self.down(F.silu(self.gate(x)) * self.up(x))
+        return self.down(core.silu_mul(F.linear(x, self._gate_up())))
 
 
 def trained_sdm_params(d, n_sub, heads, d_a):
@@ -139,6 +152,54 @@ class OneSdmLM(nn.Module):
     def unfold(self, x):
         return self.project(_norm(x, self.nf))
 
+    def _inference(self):
+        return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())) \
+            and not torch.is_autocast_enabled("cuda")
+
+    def _stages(self):
+        """The model's per-layer stages in order, each (kind, layer index, its input norm's weight and eps)."""
+        out = []
+        for i in range(self.n_layers):
+            m = self.mems[i]
+            if m.enabled:
+                out.append(("mem", i, m.norm))
+            if self.ffn == "mlp":
+                out.append(("mlp", i, self.mnorms[i]))
+            elif self.ffn == "sdm":
+                out.append(("sdm", i, self.sdms[i].norm))
+        return out
+
+    def _norm_dtype(self, kind, i, x):
+        """The dtype a stage's input norm produces: the mixer's and TrainedSdm's compute dtype, or the RMSNorm
+        module's promoted dtype (the SwiGLU norms and nf)."""
+        if kind == "mem":
+            return self.mems[i]._compute_dtype(x)
+        if kind == "sdm":
+            return self.sdms[i]._compute_dtype(x)
+        norm = self.mnorms[i] if kind == "mlp" else self.nf
+        return torch.promote_types(x.dtype, norm.w.dtype)
+
+    def _run(self, x, apply):
+        """Inference: the residual stream through every stage with each residual add fused into the next stage's
+        input norm (core.add_rms_norm: one kernel for x = x + y and its RMSNorm, the same roundings as the add and
+        the norm apart).  apply(kind, i, x, hx) gives a stage's output.  Returns nf(x)."""
+        stages = self._stages()
+        if not stages:
+            return _norm(x, self.nf)
+        kind, i, norm = stages[0]
+        x = x.contiguous().clone()   # the residual stream, updated in place
+        hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
+        for n, (kind, i, norm) in enumerate(stages):
+            y = apply(kind, i, x, hx)
+            nxt = stages[n + 1] if n + 1 < len(stages) else ("nf", 0, self.nf)
+            if y.dtype != x.dtype:   # a stage wider than the stream: the add promotes, as x + y does
+                x = (x + y).contiguous()
+                hx = core.rms_norm(x, nxt[2].w, nxt[2].eps, out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
+                continue
+            x, hx = core.add_rms_norm(x, y.contiguous(), nxt[2].w, nxt[2].eps,
+                                      out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
+        return hx
+
     def residual(self, idx, sequential=False):
         """The residual stream after the last layer (track4_onesdm_models.py:534-548).  ``sequential`` selects the
         token recurrence, which the HIP mixer computes in one pass either way."""
@@ -156,6 +217,16 @@ class OneSdmLM(nn.Module):
 
     def hidden(self, idx, sequential=False):
         """The final normalised state the tied head reads (logits = hidden @ E^T)."""
+        if self._inference() and idx.is_cuda:
+            reset = (idx == self.bos_id) if self.reset_at_bos else None
+
+            def apply(kind, i, x, hx):
+                if kind == "mem":
+                    return self.mems[i](x, reset, hx=hx)
+                if kind == "mlp":
+                    return self.mlps[i](hx)
+                return self.sdms[i](x, hx=hx)
+            return self._run(self.enfold(idx), apply)
         return _norm(self.residual(idx, sequential), self.nf)
 
     def forward(self, idx, sequential=False):
@@ -190,18 +261,17 @@ class OneSdmLM(nn.Module):
         """One token for each of B streams: idx_t [B] int64 -> logits [B, V], the last position of
         forward(idx, sequential=True) (track4_onesdm_models.py:534-555), with every mixer's memory carried in
         ``state`` (a ModelDecodeState, updated in place).  Inference only."""
-        x = self.enfold(idx_t)
         reset = (idx_t == self.bos_id) if self.reset_at_bos else None
-        for i in range(self.n_layers):
-            m = self.mems[i]
-            if m.enabled:
-                x = x + m.step(x, state.layers[i], reset)
-            if self.ffn == "mlp":
-                x = x + self.mlps[i](_norm(x, self.mnorms[i]))
-            elif self.ffn == "sdm":
-                x = x + self.sdms[i](x[:, None])[:, 0]   # per token
+
+        def apply(kind, i, x, hx):
+            if kind == "mem":
+                return self.mems[i].step(x, state.layers[i], reset, hx=hx)
+            if kind == "mlp":
+                return self.mlps[i](hx)
+            return self.sdms[i](x[:, None], hx=hx[:, None])[:, 0]   # per token
+        h = self._run(self.enfold(idx_t), apply)
         state.pos += 1
-        return self.project(_norm(x, self.nf))
+        return self.project(h)
 
 
 class DecodeGraph:

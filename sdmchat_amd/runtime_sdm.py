@@ -148,13 +148,14 @@ class RunTimeSdm(nn.Module):
             return torch.float32
         raise ValueError(f"unsupported input dtype {x.dtype}")
 
-    def _project(self, x, dt):
+    def _project(self, x, dt, hx=None):
         """RMSNorm then one fused GEMM for wk, wq, wv, wg (prepare, track4_onesdm_models.py:197-206).  Returns views
         kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer.
         The gate bias is the GEMM's bias, so W_g hx + b rounds to dt once, as wg(hx) does; addr_b is added inside
-        the core."""
+        the core.  hx: the normed input when the caller computed it (in dt, as the norm below gives it)."""
         H, d_a, d = self.h, self.d_a, self.d
-        hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
+        if hx is None:
+            hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
         W, bias = self._fused_weight(dt)[:2]
         proj = F.linear(hx, W, bias)                                   # [B, T, padded rows]
         o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
@@ -198,11 +199,12 @@ class RunTimeSdm(nn.Module):
         self.last_state = None
         return y
 
-    def forward(self, x, reset=None):
+    def forward(self, x, reset=None, hx=None):
         """x [B, T, d] -> y [B, T, d] in x.dtype; every call starts from an empty memory
         (track4_onesdm_models.py:249-274).  reset [B, T] bool: where True the memory is emptied before that position
         reads (a BOS starts a new document, :229-233).  With ``keep_state`` set, ``last_state`` receives (mem, cnt)
-        (inference only).  With autograd recording the forward is differentiable (SdmCoreFunction)."""
+        (inference only).  With autograd recording the forward is differentiable (SdmCoreFunction).  hx: the input
+        norm rms_norm(x) in the compute dtype, when the caller has it (inference only)."""
         B, T, _ = x.shape
         if not self.enabled:
             return torch.zeros_like(x)
@@ -212,7 +214,7 @@ class RunTimeSdm(nn.Module):
         dt = self._compute_dtype(x)
         H = self.h
         with torch.autocast("cuda", enabled=False):
-            kz, qz, V, g = self._project(x, dt)
+            kz, qz, V, g = self._project(x, dt, hx)
             wo = self._fused_weight(dt)[2]
             res = core.core_forward(
                 kz, qz, V, g, keys1=self.keys1, keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(),
@@ -256,7 +258,7 @@ class RunTimeSdm(nn.Module):
         device = device if device is not None else self.keys1.device
         return core.DecodeState.empty(batch, self.h, self.M, self.dh, device, core.pick_pitch(self.k, self.n_sub))
 
-    def step(self, x, state, reset=None):
+    def step(self, x, state, reset=None, hx=None):
         """One token for each of B streams: x [B, d] (or [B, 1, d]) -> y of the same shape, with the recurrence of
         forward_sequential (track4_onesdm_models.py:276-300) carried in ``state`` (updated in place).  reset [B] bool
         or None empties a stream's memory before its token reads (a BOS, :287-289)."""
@@ -270,7 +272,7 @@ class RunTimeSdm(nn.Module):
                                "torch.inference_mode()")
         dt = self._compute_dtype(x2)
         with torch.autocast("cuda", enabled=False):
-            kz, qz, V, g = self._project(x2.unsqueeze(1), dt)
+            kz, qz, V, g = self._project(x2.unsqueeze(1), dt, None if hx is None else hx.reshape(x2.shape[0], 1, -1))
             wo = self._fused_weight(dt)[2]
             r = core.decode_step(
                 kz[:, 0], qz[:, 0], V[:, 0], None if g is None else g[:, 0], state, keys1=self.keys1,

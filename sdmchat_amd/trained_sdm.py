@@ -71,9 +71,11 @@ class TrainedSdm(nn.Module):
             self._cast = (key,) + tuple(w.detach().to(dt) for w in ws)
         return self._cast[1], self._cast[2]
 
-    def _picks(self, x, dt):
-        """RMSNorm, the query map and the addressing: slots, scores, weights [B, H, T, pitch]."""
-        hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
+    def _picks(self, x, dt, hx=None):
+        """RMSNorm, the query map and the addressing: slots, scores, weights [B, H, T, pitch].  hx: the normed input
+        when the caller computed it."""
+        if hx is None:
+            hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
         q = torch.matmul(hx, self._weights(dt)[0].t())
         if self.keep_picks:
             self.last_q = q
@@ -104,14 +106,15 @@ class TrainedSdm(nn.Module):
         self.last_si = cfg["slots"][..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
         return self.wo(r).to(x.dtype)
 
-    def forward(self, x):
+    def forward(self, x, hx=None):
+        """x [B, T, d] -> y [B, T, d].  hx: rms_norm(x) in the compute dtype, when the caller has it (inference)."""
         self._check(x)
         if self._training(x):
             return self._forward_train(x)
         B, T, _ = x.shape
         dt = self._compute_dtype(x)
         with torch.autocast("cuda", enabled=False):
-            si, _, w = self._picks(x, dt)
+            si, _, w = self._picks(x, dt, hx)
             r = core.table_read(si, w, self.values, self.k, out_dtype=dt)
             y = torch.matmul(r, self._weights(dt)[1].t()).to(x.dtype)
         kk = min(self.k, min(self.k, self.n_sub) ** 2)

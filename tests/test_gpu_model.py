@@ -59,3 +59,25 @@ def test_model_logits_match_oracle(ffn, reset_at_bos):
         got = m(torch.from_numpy(idx).cuda()).double().cpu().numpy()
     scale = np.abs(want).max()
     np.testing.assert_allclose(got, want, atol=1e-4 * scale, rtol=1e-4)
+
+
+@pytest.mark.parametrize("ffn", ["mlp", "sdm"])
+def test_fused_residual_loop_equals_layer_by_layer(ffn):
+    """Inference folds each residual add into the next stage's input norm (one kernel) and runs SwiGLU's gate and up
+    as one GEMM: the final hidden state equals the layer-by-layer x = x + layer(x), nf(x) of the same modules, bit
+    for bit in bfloat16 (both use the same norm kernel and torch's add rounding), and SwiGLU's fused gate agrees
+    with the reference's three GEMMs to bfloat16 rounding."""
+    from sdmchat_amd.model import _norm
+    m = _model(ffn, True, 1).cuda().to(torch.bfloat16).eval()
+    idx = torch.from_numpy(_idx(1)).cuda()
+    say("fused residual loop", ffn)
+    with torch.no_grad():
+        got = m.hidden(idx)
+        want = _norm(m.residual(idx), m.nf)
+        assert torch.equal(got, want)
+        if ffn == "mlp":
+            mlp = m.mlps[0]
+            h = torch.randn(3, 50, 64, device="cuda").to(torch.bfloat16)
+            fused = mlp(h)
+            ref = mlp.down(torch.nn.functional.silu(mlp.gate(h)) * mlp.up(h))
+            torch.testing.assert_close(fused.float(), ref.float(), rtol=2e-2, atol=2e-3)
