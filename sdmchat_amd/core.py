@@ -7,6 +7,7 @@ stream; nothing synchronises.
 import ctypes
 
 import torch
+from torch.utils.weak import WeakIdKeyDictionary
 
 from . import _lib
 
@@ -347,6 +348,22 @@ def decode_step(kz, qz, v, gate_logits, state, *, keys1, keys2, log_scale, decay
     return out
 
 
+_W32 = WeakIdKeyDictionary()
+
+
+def _f32_weight(w, device):
+    """A norm weight as the contiguous float32 device vector the kernels read; a conversion is kept per weight
+    tensor until the tensor changes in place (its version counter), so a bfloat16 model converts each weight once."""
+    if w.dtype == torch.float32 and w.device == device and w.is_contiguous():
+        return w.detach()
+    hit = _W32.get(w)
+    if hit is not None and hit[0] == w._version and hit[1].device == device:
+        return hit[1]
+    f = w.detach().to(device=device, dtype=torch.float32).contiguous()
+    _W32[w] = (w._version, f)
+    return f
+
+
 def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
     """RMSNorm of the last dimension with the reference's rounding (track4_sdmllm_models.py:63-71):
     cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), float32 math; out_dtype defaults to x.dtype."""
@@ -362,7 +379,7 @@ def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
     if out is None:
         out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     o2 = out.view(-1, d)
-    wf = w.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    wf = _f32_weight(w, x.device)
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     rc = lib.sdm_rt_rms_norm(_ptr(x2), x2.stride(0) if x2.numel() else d, _DT[x.dtype], x2.shape[0], d, _ptr(wf),
@@ -411,7 +428,7 @@ def add_rms_norm(x, y, w, eps=1e-6, out_dtype=None, inplace=True):
     s = x if inplace else torch.empty_like(x)
     out_dtype = out_dtype or x.dtype
     out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
-    wf = w.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    wf = _f32_weight(w, x.device)
     lib = _lib.load()
     rows = x.numel() // d
     stream = torch.cuda.current_stream(x.device).cuda_stream

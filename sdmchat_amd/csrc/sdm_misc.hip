@@ -115,6 +115,50 @@ __global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restri
   }
 }
 
+// The same read with the columns split eighth by eighth over the XCDs.  A launch deals its workgroups to the 8 XCDs
+// in turn (workgroup i to XCD i mod 8), so with slice = blockIdx % 8 each XCD reads only its eighth of every row and
+// its L2 holds H * M * dh / 8 values of the tables, where the read above makes every XCD's L2 cycle through whole
+// tables larger than it.  A thread owns 16 bytes of a row slice for one (token, head): dh / (8 * kVec) threads per
+// token, `tok` tokens per workgroup; the sums run over the picks in the same order as above (the same results).
+template <int KP, typename VT, typename OutT>
+__global__ void __launch_bounds__(256) table_read_sliced_kernel(const int32_t* __restrict__ slots,
+                                                                const float* __restrict__ wts,
+                                                                const VT* __restrict__ values, OutT* __restrict__ out,
+                                                                int64_t out_stride, int B, int T, int H, int M, int dh,
+                                                                int kk, int tpt, int tok) {
+  constexpr int kVec = 16 / static_cast<int>(sizeof(VT));
+  const int slice = static_cast<int>(blockIdx.x & 7u);
+  const int64_t rest = blockIdx.x >> 3;   // (token group, head)
+  const int h = static_cast<int>(rest % H);
+  const int64_t n = (rest / H) * tok + threadIdx.x / tpt;
+  const int part = static_cast<int>(threadIdx.x % tpt);
+  if (static_cast<int>(threadIdx.x) >= tok * tpt || n >= static_cast<int64_t>(B) * T) return;
+  const int b = static_cast<int>(n / T);
+  const int t = static_cast<int>(n - static_cast<int64_t>(b) * T);
+  const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
+  int sl[KP];
+  float w[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    sl[j] = min(max(slots[pb + j], 0), M - 1);
+    w[j] = j < kk ? wts[pb + j] : 0.f;
+  }
+  const int c0 = slice * (dh >> 3) + part * kVec;
+  const VT* tab = values + static_cast<int64_t>(h) * M * dh + c0;
+  float v[KP][kVec];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) load_vals<kVec, VT>(tab + static_cast<int64_t>(sl[j]) * dh, v[j]);
+  float acc[kVec];
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w[j], v[j][e], acc[e]);
+  }
+  store_vals<kVec, OutT>(out + n * out_stride + static_cast<int64_t>(h) * dh + c0, acc);
+}
+
 }  // namespace sdmrt
 
 using namespace sdmrt;
@@ -250,11 +294,28 @@ int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float
   if (out_row_stride < static_cast<int64_t>(p.H) * p.dh)
     return set_err(SDM_RT_EINVAL, "out_row_stride %lld < heads * head_dim", (long long)out_row_stride);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(p.B) * p.T * p.H);
+  const int64_t n_tok = static_cast<int64_t>(p.B) * p.T;
+  // the XCD-sliced read when a slice is whole 16-byte pieces and the tables outgrow an XCD's L2 share (1 MiB)
+  const int vb = values_dtype == SDM_RT_BF16 ? 2 : 4;
+  const int kvec = 16 / vb;
+  const bool sliced = p.dh % (8 * kvec) == 0 && p.dh / (8 * kvec) <= 256 &&
+                      static_cast<int64_t>(p.H) * p.M * p.dh * vb >= (int64_t{1} << 20);
+  const int tpt = p.dh / (8 * kvec);
+  const int tok = sliced ? 256 / tpt : 1;
+  const int64_t groups = (n_tok + tok - 1) / tok;
+  if (sliced && groups * p.H * 8 > 0x7fffffff) return set_err(SDM_RT_EUNSUPPORTED, "too many tokens for one launch");
+  const unsigned blocks = static_cast<unsigned>(sliced ? groups * p.H * 8 : n_tok * p.H);
 #define SDM_RT_TABLE(KP, VT, OT)                                                                                   \
-  hipLaunchKernelGGL((table_read_kernel<KP, VT, OT>), dim3(blocks), dim3(256), 0, st, slots, weights,             \
-                     static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, p.H, p.M, p.dh, \
-                     p.kk)
+  do {                                                                                                             \
+    if (sliced)                                                                                                    \
+      hipLaunchKernelGGL((table_read_sliced_kernel<KP, VT, OT>), dim3(blocks), dim3(tok * tpt), 0, st, slots,     \
+                         weights, static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, \
+                         p.H, p.M, p.dh, p.kk, tpt, tok);                                                          \
+    else                                                                                                           \
+      hipLaunchKernelGGL((table_read_kernel<KP, VT, OT>), dim3(blocks), dim3(256), 0, st, slots, weights,         \
+                         static_cast<const VT*>(values), static_cast<OT*>(out), out_row_stride, p.B, p.T, p.H,     \
+                         p.M, p.dh, p.kk);                                                                         \
+  } while (0)
 #define SDM_RT_TABLE_KP(VT, OT) \
   if (p.pitch == 8) SDM_RT_TABLE(8, VT, OT); else SDM_RT_TABLE(16, VT, OT)
   if (values_dtype == SDM_RT_BF16) {

@@ -187,7 +187,7 @@ class OneSdmLM(nn.Module):
         if not stages:
             return _norm(x, self.nf)
         kind, i, norm = stages[0]
-        x = x.contiguous().clone()   # the residual stream, updated in place
+        x = x.contiguous()   # the residual stream (enfold's fresh output), updated in place
         hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
         for n, (kind, i, norm) in enumerate(stages):
             y = apply(kind, i, x, hx)

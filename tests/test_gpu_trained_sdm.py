@@ -17,7 +17,9 @@ Q_DELTA = 1e-6
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("H,n_sub,dh,k,vdt,odt", [(1, 64, 768, 16, torch.float32, torch.float32),
+@pytest.mark.parametrize("H,n_sub,dh,k,vdt,odt", [(1, 64, 768, 16, torch.float32, torch.float32),   # XCD-sliced
+                                                   (1, 64, 768, 16, torch.bfloat16, torch.bfloat16),  # XCD-sliced
+                                                   (2, 32, 512, 8, torch.bfloat16, torch.float32),    # XCD-sliced
                                                    (4, 8, 64, 8, torch.bfloat16, torch.float32),
                                                    (3, 6, 20, 5, torch.float32, torch.bfloat16)])
 def test_table_read_matches_the_weighted_row_sum(H, n_sub, dh, k, vdt, odt):
