@@ -33,7 +33,8 @@ fade set to 0 (us_per_step_head0_fade0).  --no-decode skips it.
 model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12 layers of d=768 with this mixer
 (12 heads, M=1,024, k=8): "swiglu" = each layer's per-token step a SwiGLU of hidden 2,048 (the survey's config 3),
 "trained_sdm" = a TrainedSdm of 4,096 slots, one head of width 768, k=16 (config 4); bf16 weights and activations,
-synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm.
+synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm; graph_ms
+is the same forward replayed from a HIP graph captured at that shape (ForwardGraph), median of 5 replays.
 --no-model skips it.
 
 decode_model: the FULL model (the trained_sdm arm above) decoding 64 independent streams, one fresh random token
@@ -235,7 +236,7 @@ def model_bench(dev):
     """Whole OneSdmLM forward (logits) for the SwiGLU and the TrainedSdm arms (see the module doc)."""
     import torch
 
-    from sdmchat_amd import synthetic as S
+    from sdmchat_amd import ForwardGraph, synthetic as S
 
     out = {}
     idx = torch.from_numpy(S.model_tokens(B, T, seed=11)).to(dev)
@@ -254,9 +255,22 @@ def model_bench(dev):
                 torch.cuda.synchronize()
                 ts.append(e0.elapsed_time(e1))
         ms = sorted(ts)[2]
-        out[name] = {"ms": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
-        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
-        del m
+        with torch.no_grad():   # the same forward replayed from a HIP graph (ForwardGraph)
+            gr = ForwardGraph(m, B, T)
+            tg = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                gr.run(idx)
+                e1.record()
+                torch.cuda.synchronize()
+                tg.append(e0.elapsed_time(e1))
+        gms = sorted(tg)[2]
+        out[name] = {"ms": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1), "graph_ms": round(gms, 3),
+                     "graph_tokens_per_s": round(B * T / (gms * 1e-3), 1)}
+        log(f"model {name}: {ms:.2f} ms per forward, {B * T / (ms * 1e-3) / 1e6:.2f} M tokens/s; "
+            f"HIP graph {gms:.2f} ms, {B * T / (gms * 1e-3) / 1e6:.2f} M tokens/s")
+        del m, gr
         torch.cuda.empty_cache()
     mf = S.MODEL_FULL
     out["workload"] = (f"OneSdmLM forward (logits): B={B} T={T}, vocabulary {mf['V']}, {mf['layers']} layers, "

@@ -5,8 +5,9 @@
 ``OneSdmLM``        the whole language model around the mixer (same constructor and state_dict; no archive)
 ``core``            torch-facing wrappers of the C ABI (addressing, the SDM core)
 ``synthetic``       seeded synthetic parameters and inputs of the layer workloads
-``build``           compiles ``csrc/sdm_rt.hip`` into ``lib/libsdm_rt.so``
+``DecodeGraph``, ``ForwardGraph``  OneSdmLM.step and OneSdmLM.forward at fixed shapes, captured in HIP graphs
+``build``           compiles ``csrc/*.hip`` into ``lib/libsdm_rt.so``
 """
 from .runtime_sdm import RMSNorm, RunTimeSdm  # noqa: F401
 from .trained_sdm import TrainedSdm  # noqa: F401
-from .model import DecodeGraph, ModelDecodeState, OneSdmLM, decode_state_bytes  # noqa: F401
+from .model import DecodeGraph, ForwardGraph, ModelDecodeState, OneSdmLM, decode_state_bytes  # noqa: F401

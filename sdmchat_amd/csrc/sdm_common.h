@@ -667,32 +667,40 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
       float inv[2];
       if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
       else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
-      // after the swap below lane l holds every score of address row l
+      // after the swap below lane l holds every score of address row l.  The tile's 32 keys are taken CAP at a
+      // time (sub-keys 2 GR grp ... 2 GR grp + 2 GR - 1), each group sorted and merged into the half's best: the
+      // same top CAP as one 32-key selection (the keys are distinct), with a quarter of the keys live at once.
       const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
-      double c[32];
+      constexpr int GR = CAP / 2;   // score registers per group
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]),
-                                                         false, false);
-        const int i0 = 32 * tile + 8 * (r / 4) + (r % 4);
-        if (hf == 0) {
-          c[r] = half_key<KL::FS1, NS>(__uint_as_float(sw[0]), dinv, i0);
-          c[16 + r] = half_key<KL::FS1, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+      for (int grp = 0; grp < 16 / GR; ++grp) {
+        double c[CAP];
+#pragma unroll
+        for (int rr = 0; rr < GR; ++rr) {
+          const int r = GR * grp + rr;
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]),
+                                                           false, false);
+          const int i0 = 32 * tile + 8 * (r / 4) + (r % 4);
+          if (hf == 0) {
+            c[rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[0]), dinv, i0);
+            c[GR + rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+          } else {
+            c[rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[0]), dinv, i0);
+            c[GR + rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+          }
+          if (!FULL) {   // sub-keys past n_sub are never picked
+            if (i0 >= g.n_sub) c[rr] = key_invalid(c[rr]);
+            if (i0 + 4 >= g.n_sub) c[GR + rr] = key_invalid(c[GR + rr]);
+          }
+        }
+        if constexpr (CAP == 8) sort8_desc(c);
+        else bitonic_sort_desc<CAP>(c);
+        if (tile == 0 && grp == 0) {
+#pragma unroll
+          for (int r = 0; r < CAP; ++r) best[r] = c[r];
         } else {
-          c[r] = half_key<KL::FS2, NS>(__uint_as_float(sw[0]), dinv, i0);
-          c[16 + r] = half_key<KL::FS2, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+          merge_top_desc<CAP>(best, c);
         }
-        if (!FULL) {   // sub-keys past n_sub are never picked
-          if (i0 >= g.n_sub) c[r] = key_invalid(c[r]);
-          if (i0 + 4 >= g.n_sub) c[16 + r] = key_invalid(c[16 + r]);
-        }
-      }
-      top_k_desc<CAP, 32>(c);
-      if (tile == 0) {
-#pragma unroll
-        for (int r = 0; r < CAP; ++r) best[r] = c[r];
-      } else {
-        merge_top_desc<CAP>(best, c);
       }
     }
 #pragma unroll
@@ -882,9 +890,13 @@ __host__ __device__ constexpr size_t scan_lds_bytes(int M, int CW, int n_chunks,
          sizeof(float) * 68 + sizeof(int32_t) * pad4(n_chunks);
 }
 
-// static LDS of plan_kernel (picks, fade powers, totals)
-__host__ __device__ constexpr size_t plan_static_lds(int KP) {
-  return 2 * kChunk * KP * (2 + 4) + 4 * (kChunk + 4) + 64;
+// static LDS of plan_kernel (fade powers, totals)
+__host__ __device__ constexpr size_t plan_static_lds(int) { return 4 * (kChunk + 4) + 64; }
+// plan_kernel's first-rank table: M 16-bit entries, padded to 16 bytes
+__host__ __device__ constexpr size_t plan_rank_bytes(int M) { return (2 * static_cast<size_t>(M) + 15) / 16 * 16; }
+// plan_kernel's dynamic LDS before the sub-keys: writer masks, first ranks, write weights by rank
+__host__ __device__ constexpr size_t plan_dynamic_lds(int M, int KP) {
+  return 8 * static_cast<size_t>(M) + plan_rank_bytes(M) + 4 * static_cast<size_t>(kChunk) * KP;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -945,8 +957,8 @@ inline int make_plan(const sdm_rt_dims* d, Plan* p, bool core = true) {
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations and T = %d do not fit a slab of 8 columns in LDS", p->M,
                    p->T);
   p->groups = p->dh / (p->cw32 ? p->cw32 : p->cw);   // the workspace is sized for the larger group count
-  if (plan_static_lds(p->pitch) + 8 * static_cast<size_t>(p->M) + 8 * static_cast<size_t>(p->n_sub) * p->half + 256 >
-      kLdsBytes)
+  if (plan_static_lds(p->pitch) + plan_dynamic_lds(p->M, p->pitch) + 8 * static_cast<size_t>(p->n_sub) * p->half +
+          256 > kLdsBytes)
     return set_err(SDM_RT_EUNSUPPORTED, "M = %d locations: writer masks and sub-keys do not fit in LDS", p->M);
   const size_t slabs = static_cast<size_t>(p->B) * p->H;
   const size_t n_plans = slabs * p->n_chunks;

@@ -53,7 +53,7 @@ struct PlanArgs {
 // owned writes and the later writers of the slots written more than once; entry counts are prefix-summed within
 // each wave.
 template <int HALF, int KP, typename InT, int MODE>
-__global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
+__global__ void __launch_bounds__(128, 4) plan_kernel(PlanArgs a) {
   constexpr PlanGeom pg{KP};
   const int c = blockIdx.x;
   const int h = blockIdx.y;
@@ -67,12 +67,14 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   const int L = min(kChunk, a.T - c0);
   const float lam = a.decay[h];
 
-  __shared__ __attribute__((aligned(16))) uint16_t pk_slot[2][kChunk][KP];
-  __shared__ __attribute__((aligned(16))) float pk_w[2][kChunk][KP];
   __shared__ float pw[kChunk + 4];
   __shared__ int tot[4];
-  extern __shared__ unsigned long long wmask[];   // [M], then (per-thread path) the head's sub-keys [2][n_sub][HALF]
-  float* kn = reinterpret_cast<float*>(wmask + M);
+  // dynamic: the writers of every slot [M] (bit q: position q wrote it), the first rank of every slot's writes [M],
+  // the write weights by slot and rank [64 KP], then (per-thread path) the head's sub-keys [2][n_sub][HALF]
+  extern __shared__ unsigned long long wmask[];
+  uint16_t* sbase = reinterpret_cast<uint16_t*>(wmask + M);
+  float* wtab = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(sbase) + plan_rank_bytes(M));
+  float* kn = wtab + kChunk * KP;
 
   if (c == 0 && a.sync && tid < a.groups) a.sync[(static_cast<int64_t>(b) * a.g.H + h) * a.groups + tid] = 0u;
   if (c == 0 && h == 0 && b == 0 && a.sync && tid == 0)
@@ -90,7 +92,9 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   }
   if constexpr (MODE == 0) __syncthreads();
 
-  // addressing
+  // addressing: the position's picks (slots; pads M) and weights, kept in registers
+  int ms[KP];
+  float ws[KP];
   {
     int slot[KP];
     float w[KP], sc[KP];
@@ -109,8 +113,8 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
       const bool live = p < L && j < kk;
-      pk_slot[set][p][j] = static_cast<uint16_t>(live ? slot[j] : M);
-      pk_w[set][p][j] = live ? w[j] : 0.f;
+      ms[j] = live ? slot[j] : M;
+      ws[j] = live ? w[j] : 0.f;
     }
   }
   // resets of the chunk (OM:229-233, 287-289): a reader sees the writers of its own segment only, no carried state
@@ -123,35 +127,35 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   __syncthreads();
   // mark the writers of every slot
   if (set == 0 && p < L) {
-    for (int j = 0; j < kk; ++j) atomicOr(&wmask[pk_slot[0][p][j]], 1ull << p);
+    for (int j = 0; j < kk; ++j) atomicOr(&wmask[ms[j]], 1ull << p);
   }
   __syncthreads();
-  // weight with which position q wrote slot m (a position's picks are distinct locations)
-  auto wweight = [&](int q, int m) {
-    float r = 0.f;
-#pragma unroll
-    for (int g8 = 0; g8 < KP / 8; ++g8) {   // the row's picks and weights in 16-byte reads
-      const uint4 sv = *reinterpret_cast<const uint4*>(&pk_slot[0][q][8 * g8]);
-      const float4 wa = *reinterpret_cast<const float4*>(&pk_w[0][q][8 * g8]);
-      const float4 wb = *reinterpret_cast<const float4*>(&pk_w[0][q][8 * g8 + 4]);
-      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-      const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int sj = static_cast<int>((sw[j / 2] >> (16 * (j % 2))) & 0xffffu);
-        if (8 * g8 + j < kk && sj == m) r = wv[j];
-      }
+  // the write weights by slot and rank: the writes of slot m, in ascending position, are wtab[sbase[m] ...]; the
+  // write of position q is at rank popcount(wmask[m] below q) (a position's picks are distinct locations)
+  {
+    const int spt = (M + 127) / 128;   // slots per thread
+    const int m0 = min(tid * spt, M), m1 = min(m0 + spt, M);
+    int n = 0;
+    for (int m = m0; m < m1; ++m) n += __builtin_popcountll(wmask[m]);
+    const int inc = wave_incl_scan(n, p);
+    if (p == 63) tot[set] = inc;
+    __syncthreads();
+    int run = inc - n + (set == 1 ? tot[0] : 0);
+    for (int m = m0; m < m1; ++m) {
+      sbase[m] = static_cast<uint16_t>(run);
+      run += __builtin_popcountll(wmask[m]);
     }
-    return r;
-  };
-  int ms[KP];
-  float ws[KP];
-#pragma unroll
-  for (int j = 0; j < KP; ++j) {
-    ms[j] = pk_slot[set][p][j];
-    ws[j] = pk_w[set][p][j];
   }
+  __syncthreads();
+  auto rank_below = [&](int m, int q) {   // sbase[m] + the writes of slot m by positions before q
+    return static_cast<int>(sbase[m]) + __builtin_popcountll(wmask[m] & ((1ull << q) - 1ull));
+  };
+  if (set == 0 && p < L) {
+    for (int j = 0; j < kk; ++j) wtab[rank_below(ms[j], p)] = ws[j];
+  }
+  __syncthreads();
   unsigned long long mk[KP];           // read side: the earlier writers of each read slot
+  int rk[KP];                          // read side: the rank in wtab of each read slot's next earlier writer
   unsigned long long touched = 0ull;   // read side: every earlier position contributing to this one
   int n_in = 0;                        // read side: contributions
   int n_e = 0;                         // entries in the variable part (read side: past the inline; write: later writers)
@@ -162,6 +166,7 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
 #pragma unroll
       for (int i = 0; i < KP; ++i) {
         mk[i] = i < kk ? wmask[ms[i]] & below : 0ull;
+        rk[i] = i < kk ? rank_below(ms[i], seg0 >= 0 ? seg0 : 0) : 0;
         touched |= mk[i];
       }
       n_in = __builtin_popcountll(touched);
@@ -224,10 +229,18 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     while (touched) {
       const int q = __builtin_ctzll(touched);
       touched &= touched - 1ull;
+      // q's weight for each of p's read slots it wrote: every slot's next writer is read at once (the slots q
+      // did not write add nothing)
+      float wq[KP];
+#pragma unroll
+      for (int i = 0; i < KP; ++i) wq[i] = wtab[min(rk[i], kChunk * KP - 1)];
       float coef = 0.f;
 #pragma unroll
-      for (int i = 0; i < KP; ++i)
-        if ((mk[i] >> q) & 1ull) coef = fmaf(ws[i], wweight(q, ms[i]), coef);
+      for (int i = 0; i < KP; ++i) {
+        const bool hit = (mk[i] >> q) & 1ull;
+        coef = fmaf(ws[i], hit ? wq[i] : 0.f, coef);
+        rk[i] += hit ? 1 : 0;
+      }
       coef *= pw[p - 1 - q];
       if (j < kInline) {
         qb |= static_cast<unsigned long long>(q) << (8 * j);
@@ -261,12 +274,13 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
         wcv[j] = __float_as_uint(pw[L - 1 - p] * ws[j]);
         if ((more >> j) & 1u) {
           const int m = ms[j];
-          unsigned long long mm = (wmask[m] & keep) & ~(1ull << p);
+          unsigned long long mm = (wmask[m] & keep) & ~(1ull << p);   // every writer of m after p
           const int e_first = e;
+          int rank = rank_below(m, p) + 1;
           while (mm) {
             const int q = __builtin_ctzll(mm);
             mm &= mm - 1ull;
-            ent[e++] = make_uint2(__float_as_uint(pw[L - 1 - q] * wweight(q, m)), static_cast<uint32_t>(q));
+            ent[e++] = make_uint2(__float_as_uint(pw[L - 1 - q] * wtab[rank++]), static_cast<uint32_t>(q));
           }
           ent[r++] = make_uint2(wo[j], static_cast<uint32_t>(e_first) | (static_cast<uint32_t>(e - e_first) << 16));
         }
@@ -285,7 +299,7 @@ struct PlanLaunch {
   template <int KP, int MODE>
   static int go(const Plan& p, const PlanArgs& a, hipStream_t st) {
     dim3 grid(p.n_chunks, p.H, p.B);
-    const size_t lds = sizeof(unsigned long long) * p.M + (MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
+    const size_t lds = plan_dynamic_lds(p.M, KP) + (MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
     static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MODE>));
     if (!ok) return lds_err("plan");
     hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MODE>), grid, dim3(128), lds, st, a);

@@ -305,3 +305,30 @@ class DecodeGraph:
         return self.logits
 
     step = run
+
+
+class ForwardGraph:
+    """OneSdmLM.forward for token batches of one shape [B, T] captured in a HIP graph (prefill at a fixed shape):
+    ``run(idx)`` copies the tokens into the graph's input, replays it and returns the graph's logits tensor
+    (overwritten by the next run).  Capture first runs the forward twice on the same shapes, so that every workspace
+    and parameter cache exists before capture; replays launch the whole forward at once, without the host's
+    per-kernel work between launches.  Inference only; the model's parameters must not be replaced while the graph
+    is in use (in-place updates are seen by the replays)."""
+
+    def __init__(self, model, B, T):
+        dev = model.emb.weight.device
+        self.model = model
+        self.idx = torch.zeros(B, T, dtype=torch.long, device=dev)
+        with torch.no_grad():
+            for _ in range(2):
+                model(self.idx)
+            torch.cuda.synchronize(dev)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.logits = model(self.idx)
+
+    def run(self, idx):
+        """idx [B, T] int64 -> logits [B, T, V]."""
+        self.idx.copy_(idx)
+        self.graph.replay()
+        return self.logits

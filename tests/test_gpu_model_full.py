@@ -11,13 +11,15 @@ and 534-555.
   t bit-identical; reset at BOS makes the logits after a BOS equal those of the suffix run alone.
 - decode: 64 FULL-arm streams of seeded random tokens, 128 steps: step logits equal the forward's over the same
   tokens; prefill + step equals the forward; a HIP graph of steps replays equal to eager steps.
+- a HIP graph of the forward (ForwardGraph, both arms in bfloat16) replays equal to the eager forward, bit for bit,
+  on three token batches with eager work between the replays.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import sdm_fp64 as O
-from sdmchat_amd import DecodeGraph, decode_state_bytes, synthetic as S
+from sdmchat_amd import DecodeGraph, ForwardGraph, decode_state_bytes, synthetic as S
 from tests._gpu_util import say
 
 pytestmark = pytest.mark.gpu
@@ -181,6 +183,23 @@ def test_decode_graph_replays_equal_eager_steps():
             for a, b in zip(graphed.layers, eager.layers):
                 assert torch.equal(a.mem, b.mem) and torch.equal(a.scale, b.scale) and torch.equal(a.last, b.last)
         assert graphed.pos == eager.pos == 12
+
+
+@pytest.mark.parametrize("arm", ARMS)
+def test_forward_graph_replays_equal_eager(arm):
+    m = S.full_model(arm, layers=3, reset_at_bos=True, bos_id=7).cuda().to(torch.bfloat16).eval()
+    B, T = 2, 300
+    say("ForwardGraph", arm, B, T)
+    with torch.no_grad():
+        g = ForwardGraph(m, B, T)
+        for rep in range(3):
+            idx = torch.from_numpy(S.model_tokens(B, T, seed=40 + rep)).cuda()
+            idx[:, 100 + 30 * rep] = 7   # a BOS
+            out = g.run(idx).clone()
+            torch.randn(1000, device="cuda").sum()   # eager work between replays
+            ref = m(idx)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {rep}: logits differ"
 
 
 def test_decode_state_bytes():
