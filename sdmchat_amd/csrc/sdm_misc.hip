@@ -76,6 +76,34 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const T* __restrict__ gu,
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// The KP picks of one (token, head) of a table read: slots clamped into the table (pads, -1, and stray ids stay
+// inside it) and weights (0 past kk), in 16-byte loads when both arrays are 16-byte aligned (the pick rows are
+// KP * 4 bytes at multiples of KP * 4 bytes, so the base pointers decide)
+template <int KP>
+__device__ __forceinline__ void load_picks(const int32_t* sp, const float* wp, int M, int kk, int (&sl)[KP],
+                                           float (&w)[KP]) {
+  if ((reinterpret_cast<uintptr_t>(sp) | reinterpret_cast<uintptr_t>(wp)) & 15u) {
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      sl[j] = min(max(sp[j], 0), M - 1);
+      w[j] = j < kk ? wp[j] : 0.f;
+    }
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < KP / 4; ++q) {
+    const int4 s4 = reinterpret_cast<const int4*>(sp)[q];
+    const float4 w4 = reinterpret_cast<const float4*>(wp)[q];
+    const int sv[4] = {s4.x, s4.y, s4.z, s4.w};
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sl[4 * q + e] = min(max(sv[e], 0), M - 1);
+      w[4 * q + e] = 4 * q + e < kk ? wv[e] : 0.f;
+    }
+  }
+}
+
 // table read: the weighted sum of the picked rows of per-head value tables (TrainedSdm.forward's embedding_bag,
 // track4_onesdm_models.py:448-455): out[n][h * dh + c] = sum_j w[n][h][j] * values[h][slot[n][h][j]][c] in float32,
 // picks in order.  One workgroup of 256 threads per (token, head); thread i takes columns 4i ... 4i + 3 of every
@@ -95,11 +123,7 @@ __global__ void __launch_bounds__(256) table_read_kernel(const int32_t* __restri
   const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
   int sl[KP];
   float w[KP];
-#pragma unroll
-  for (int j = 0; j < KP; ++j) {
-    sl[j] = min(max(slots[pb + j], 0), M - 1);   // pads (-1) and stray ids stay inside the table
-    w[j] = j < kk ? wts[pb + j] : 0.f;
-  }
+  load_picks<KP>(slots + pb, wts + pb, M, kk, sl, w);
   const VT* tab = values + static_cast<int64_t>(h) * M * dh;
   for (int c0 = 4 * static_cast<int>(threadIdx.x); c0 < dh; c0 += 1024) {
     float v[KP][4];
@@ -138,23 +162,37 @@ __global__ void __launch_bounds__(256) table_read_sliced_kernel(const int32_t* _
   const int64_t pb = ((static_cast<int64_t>(b) * H + h) * T + t) * KP;
   int sl[KP];
   float w[KP];
-#pragma unroll
-  for (int j = 0; j < KP; ++j) {
-    sl[j] = min(max(slots[pb + j], 0), M - 1);
-    w[j] = j < kk ? wts[pb + j] : 0.f;
-  }
+  load_picks<KP>(slots + pb, wts + pb, M, kk, sl, w);
   const int c0 = slice * (dh >> 3) + part * kVec;
   const VT* tab = values + static_cast<int64_t>(h) * M * dh + c0;
-  float v[KP][kVec];
-#pragma unroll
-  for (int j = 0; j < KP; ++j) load_vals<kVec, VT>(tab + static_cast<int64_t>(sl[j]) * dh, v[j]);
   float acc[kVec];
 #pragma unroll
   for (int e = 0; e < kVec; ++e) acc[e] = 0.f;
+  if ((reinterpret_cast<uintptr_t>(values) & 15u) == 0) {
+    // 16-byte rows pieces kept raw until their turn (4 registers a pick; bfloat16 unpacked by shifts)
+    uint4 raw[KP];
 #pragma unroll
-  for (int j = 0; j < KP; ++j) {
+    for (int j = 0; j < KP; ++j) raw[j] = *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(sl[j]) * dh);
 #pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w[j], v[j][e], acc[e]);
+    for (int j = 0; j < KP; ++j) {
+      const uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (sizeof(VT) == 2) {
+          acc[2 * q] = fmaf(w[j], __uint_as_float(wd[q] << 16), acc[2 * q]);
+          acc[2 * q + 1] = fmaf(w[j], __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
+        } else {
+          acc[q] = fmaf(w[j], __uint_as_float(wd[q]), acc[q]);
+        }
+      }
+    }
+  } else {   // a table not 16-byte aligned: element loads, one pick at a time
+    for (int j = 0; j < KP; ++j) {
+      float v[kVec];
+      load_vals<kVec, VT>(tab + static_cast<int64_t>(sl[j]) * dh, v);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w[j], v[e], acc[e]);
+    }
   }
   store_vals<kVec, OutT>(out + n * out_stride + static_cast<int64_t>(h) * dh + c0, acc);
 }
