@@ -90,6 +90,26 @@ __device__ __forceinline__ void lds_seg_store(float* p, const Seg<CPL>& r) {
   }
 }
 
+// 8 consecutive floats of a slab row, and 8 consecutive values of a value row, from LDS (16-byte accesses)
+__device__ __forceinline__ void lds_row8(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void lds_row8_store(float* p, const float (&v)[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void lds_vals8(const float* p, float (&v)[8]) { lds_row8(p, v); }
+__device__ __forceinline__ void lds_vals8(const bf16_t* p, float (&v)[8]) {
+  const uint4 t = *reinterpret_cast<const uint4*>(p);
+  const uint32_t wd[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = __uint_as_float(wd[q] << 16);
+    v[2 * q + 1] = __uint_as_float(wd[q] & 0xffff0000u);
+  }
+}
+
 __device__ __forceinline__ uint32_t u4_word(const uint4& q, int i) {
   return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
 }
@@ -472,12 +492,16 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     const int n_x = static_cast<int>(reinterpret_cast<const uint32_t*>(varc)[3]);
     if (n_x > 0) {
       lds_barrier();
+      // CW / 8 lanes per slot, 8 columns each: 64 * 8 / CPL slots at a time (one round for the usual n_x)
+      constexpr int LPS = CW / 8;
+      const int l_s = tid % LPS, grp = tid / LPS;
       auto later = [&](auto st) {
-        for (int r = p; r < n_x; r += kChunk) {
+        for (int r = grp; r < n_x; r += kScanThreads / LPS) {
           const uint2 xr = ent_at(x0 + r, st);
-          float* row = reinterpret_cast<float*>(A_lane_w + xr.x);
+          float* row = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(A + 8 * l_s) + xr.x);
           float* crow = reinterpret_cast<float*>(cnt_b + (xr.x >> kShift));
-          Seg<CPL> z = lds_seg<CPL>(row);
+          float z[8];
+          lds_row8(row, z);
           const float cold = *crow;
           const int e0 = static_cast<int>(xr.y & 0xffffu), n = min(static_cast<int>(xr.y >> 16), kChunk);
           float csum_w = 0.f;
@@ -486,14 +510,15 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
             const uint2 e_1 = ent_at(e0 + min(e + 1, n - 1), st);
             const float c_0 = __uint_as_float(e_0.x) * inv_mu;
             const float c_1 = e + 1 < n ? __uint_as_float(e_1.x) * inv_mu : 0.f;
-            const Seg<CPL> v0 = lds_seg<CPL>(&s_vc[(e_0.y & 63u) * CW + cl]);
-            const Seg<CPL> v1 = lds_seg<CPL>(&s_vc[(e_1.y & 63u) * CW + cl]);
+            float v0[8], v1[8];
+            lds_vals8(&s_vc[(e_0.y & 63u) * CW + 8 * l_s], v0);
+            lds_vals8(&s_vc[(e_1.y & 63u) * CW + 8 * l_s], v1);
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) z.v[k] = fmaf(c_1, v1.v[k], fmaf(c_0, v0.v[k], z.v[k]));
+            for (int k = 0; k < 8; ++k) z[k] = fmaf(c_1, v1[k], fmaf(c_0, v0[k], z[k]));
             csum_w += c_0 + c_1;
           }
-          lds_seg_store<CPL>(row, z);
-          if (l8 == 0) *crow = cold + csum_w;
+          lds_row8_store(row, z);
+          if (l_s == 0) *crow = cold + csum_w;
         }
       };
       if (all_staged) later(std::true_type{});
