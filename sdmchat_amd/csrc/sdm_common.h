@@ -871,6 +871,29 @@ struct PlanGeom {
   __host__ __device__ constexpr int stride() const { return (off_var() + 16 + 8 * max_entries() + 255) / 256 * 256; }
 };
 
+// The pick plan (picks of at most 8; written by plan_kernel<..., PICK = true>, executed by pick_scan_kernel):
+//   read records R[8][64], 16 bytes each, record (i, p) for pick i of position p:
+//     w0  read slot (bits 0..15; pads and positions past the chunk's end: M) | q (bits 16..21) | n_in (bits 24..31)
+//     w1  read weight (0 for pads and when a reset earlier in the chunk hides the carried state)
+//     w2  coefficient of the position's in-chunk read contribution number i (q its source position), 0 if i >= n_in
+//     w3  entry index of the position's contributions past the eighth (contribution j >= 8 is entry w3 + j - 8)
+//   write records W[8][64]:
+//     w0  write slot if p owns it (the first writer of the slot the chunk keeps), else M | q (bits 16..21) of the
+//         slot's first later writer | n_l (bits 24..31) later writers
+//     w1  lam^(L-1-p) * ww if owned, else 0
+//     w2  the first later writer's lam^(L-1-q) * ww (0 if none)
+//     w3  entry index of the later writers past the first
+//   variable part: a 16-byte header {bytes, flags (bit 31: the chunk holds a reset), n_ro, n_wo}, then n_ro entries
+//   of read contributions past the eighth of each position (by position, in ascending q), then n_wo entries of later
+//   writers past the first of each owned slot (ascending q): {c, q}
+struct PickGeom {
+  __host__ __device__ static constexpr int off_w() { return kChunk * 8 * 16; }
+  __host__ __device__ static constexpr int off_var() { return 2 * kChunk * 8 * 16; }
+  // at most sum_p max(p - 8, 0) = 1,540 contributions and 511 later writers past the inline ones
+  __host__ __device__ static constexpr int max_entries() { return 1540 + 511; }
+  __host__ __device__ static constexpr int stride() { return (off_var() + 16 + 8 * max_entries() + 255) / 256 * 256; }
+};
+
 // Bytes of a plan's variable part the scan stages in LDS (typical parts hold well under 1 KB; entries past the
 // staged bytes are read from the plan in global memory, so a crowded chunk costs time, not LDS).
 constexpr int kVarStage = 4096;
@@ -966,11 +989,15 @@ inline int make_plan(const sdm_rt_dims* d, Plan* p, bool core = true) {
   p->off_sizes = o;
   o = align_up(o + sizeof(int32_t) * n_plans, 256);
   p->off_plans = o;
-  o = align_up(o + static_cast<size_t>(PlanGeom{p->pitch}.stride()) * n_plans, 256);
+  // the plans of either scan (the pick plan serves picks of at most 8)
+  const int stride = p->pitch == 8 ? std::max(PlanGeom{8}.stride(), PickGeom::stride()) : PlanGeom{p->pitch}.stride();
+  o = align_up(o + static_cast<size_t>(stride) * n_plans, 256);
   p->off_sync = o;   // per slab and group a progress counter, then one status word
   o = align_up(o + sizeof(uint32_t) * (slabs * p->groups + 1), 256);
-  p->off_xch = o;    // per slab, chunk and group the 64 partial sums of squares of the out-norm
-  o = align_up(o + (d->out_norm && p->groups > 1 ? sizeof(float) * slabs * p->n_chunks * p->groups * kChunk : 0), 256);
+  // per slab, chunk and group the 64 partial sums of squares of the out-norm (8 bytes each: the pick scan pairs every
+  // sum with a flag that says it is written)
+  p->off_xch = o;
+  o = align_up(o + (d->out_norm && p->groups > 1 ? 8 * slabs * p->n_chunks * p->groups * kChunk : 0), 256);
   p->total = o;
   return SDM_RT_OK;
 }

@@ -1,9 +1,20 @@
-// sdm_forward.hip -- the forward of the SDM core (sdm_rt_forward): plan_kernel, then scan_kernel with the read-out
-// finished in place.  Replaces RunTimeSdm.forward between the projections and wo
-// (experiments/track4/sdmllm/track4_onesdm_models.py:195-274, finish :243-246 without wo).
-#include "sdm_scan.h"
+// sdm_forward.hip -- the forward of the SDM core (sdm_rt_forward): plan_kernel, then the scan with the read-out
+// finished in place (pick_scan_kernel where its shape fits, else scan_kernel).  Replaces RunTimeSdm.forward between
+// the projections and wo (experiments/track4/sdmllm/track4_onesdm_models.py:195-274, finish :243-246 without wo).
+#include <cstdlib>
+
+#include "sdm_pick.h"
 
 namespace sdmrt {
+
+// SDM_RT_SCAN=chunk in the environment keeps every shape on scan_kernel (read once per process)
+static bool pick_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("SDM_RT_SCAN");
+    return !(e && std::strcmp(e, "chunk") == 0);
+  }();
+  return on;
+}
 
 int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, const CoreIO& io, void* workspace,
              hipStream_t st) {
@@ -12,9 +23,10 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   unsigned char* plans = reinterpret_cast<unsigned char*>(ws + p.off_plans);
   uint32_t* sync = reinterpret_cast<uint32_t*>(ws + p.off_sync);
   float* xch = reinterpret_cast<float*>(ws + p.off_xch);
-  const int cw = scan_cw(p, io.in_dtype);
-  if (!cw) return SDM_RT_EUNSUPPORTED;
   const size_t vb = io.in_dtype == SDM_RT_BF16 ? 2 : 4;
+  const bool pick = pick_enabled() && pick_path(p, static_cast<int>(vb));
+  const int cw = pick ? kPickCols : scan_cw(p, io.in_dtype);
+  if (!cw) return SDM_RT_EUNSUPPORTED;
 
   PlanArgs pa{};
   pa.g = addr_geom(p, prm);
@@ -30,12 +42,14 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   pa.sizes = sizes;
   pa.sync = sync;
   pa.groups = p.groups;
+  pa.xch = pick && dims->out_norm && p.dh / cw > 1 ? reinterpret_cast<unsigned long long*>(xch) : nullptr;
+  pa.xgroups = p.dh / cw;
   pa.row_bytes = cw * static_cast<int>(sizeof(float));
   pa.B = p.B;
   pa.T = p.T;
   pa.M = p.M;
   pa.n_chunks = p.n_chunks;
-  int rc = io.in_dtype == SDM_RT_BF16 ? launch_plan_bf16(p, pa, st) : launch_plan_f32(p, pa, st);
+  int rc = io.in_dtype == SDM_RT_BF16 ? launch_plan_bf16(p, pa, st, pick) : launch_plan_f32(p, pa, st, pick);
   if (rc) return rc;
 
   ScanArgs s{};
@@ -66,9 +80,14 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   // direct copies of the value rows into LDS move 16-byte pieces: rows and the column groups in them aligned to 16
   s.v_direct = reinterpret_cast<uintptr_t>(io.v) % 16 == 0 && (static_cast<size_t>(io.v_stride) * vb) % 16 == 0 &&
                (static_cast<size_t>(p.dh) * vb) % 16 == 0 && (cw * vb) % 16 == 0;
+  if (pick)   // the pick scan loads two values at a time
+    s.v_direct = reinterpret_cast<uintptr_t>(io.v) % (2 * vb) == 0 && io.v_stride % 2 == 0;
   s.read_mean = dims->read_mean;
   s.read_eps = dims->read_eps;
   s.out_eps = dims->out_norm_eps;
+  if (pick)
+    return io.in_dtype == SDM_RT_BF16 ? launch_pick_scan_bf16(p, s, io.out_dtype, st)
+                                      : launch_pick_scan_f32(p, s, io.out_dtype, st);
   return io.in_dtype == SDM_RT_BF16 ? launch_scan_bf16(p, s, io.out_dtype, st) : launch_scan_f32(p, s, io.out_dtype, st);
 }
 

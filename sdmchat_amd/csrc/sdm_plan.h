@@ -42,17 +42,158 @@ struct PlanArgs {
   unsigned char* plans;    // [B][H][n_chunks][stride]
   int32_t* sizes;          // [B][H][n_chunks] bytes of each plan's variable part
   uint32_t* sync;          // [B*H][groups] scan progress counters, then a status word: zeroed here, or nullptr
+  unsigned long long* xch; // pick plans: [B*H][n_chunks][xgroups][64] out-norm partial sums, cleared here, or nullptr
   int groups;
+  int xgroups;             // column groups of the pick scan
   int row_bytes;           // bytes of a slab row in the scan's LDS (its column group width * 4)
   int B, T, M, n_chunks;
 };
+
+// The pick plan of one chunk (PickGeom, sdm_common.h) from the picks in registers and the writer masks in LDS:
+// wave 1 (set 1) writes the read records of its position (the in-chunk read contributions in ascending q, number j
+// into the record of pick j, those past the eighth into the variable part), wave 0 the write records (owned picks,
+// the first later writer inline, the others into the variable part).  Every thread of the block calls it.
+__device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, int c, int set, int p, int L, int M,
+                                               int kk, const int (&ms)[8], const float (&ws)[8],
+                                               const unsigned long long* wmask, const uint16_t* sbase,
+                                               const float* wtab, const float* pw, int* tot, int seg0,
+                                               unsigned long long rmask, unsigned long long keep) {
+  constexpr int KP = 8;
+  auto rank_below = [&](int m, int q) {   // sbase[m] + the writes of slot m by positions before q
+    return static_cast<int>(sbase[m]) + __builtin_popcountll(wmask[m] & ((1ull << q) - 1ull));
+  };
+  unsigned long long mk[KP];   // read side: the earlier writers (same segment) of each read slot
+  int rk[KP];                  // read side: the rank in wtab of each read slot's next earlier writer
+  unsigned long long touched = 0ull;
+  int n_in = 0, n_e = 0;
+  uint32_t own = 0u;
+  int nl[KP];                  // write side: later writers of each owned slot
+#pragma unroll
+  for (int j = 0; j < KP; ++j) nl[j] = 0;
+  if (p < L) {
+    if (set == 1) {
+      const unsigned long long below = ((1ull << p) - 1ull) & (seg0 >= 0 ? ~((1ull << seg0) - 1ull) : ~0ull);
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {
+        mk[i] = i < kk ? wmask[ms[i]] & below : 0ull;
+        rk[i] = i < kk ? rank_below(ms[i], seg0 >= 0 ? seg0 : 0) : 0;
+        touched |= mk[i];
+      }
+      n_in = __builtin_popcountll(touched);
+      n_e = max(n_in - KP, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KP; ++j) {
+        if (j < kk) {
+          const unsigned long long mm = wmask[ms[j]] & keep;
+          if (mm && __builtin_ctzll(mm) == p) {
+            own |= 1u << j;
+            nl[j] = __builtin_popcountll(mm) - 1;
+            n_e += max(nl[j] - 1, 0);
+          }
+        }
+      }
+    }
+  }
+  const int inc_e = wave_incl_scan(n_e, p);
+  if (p == 63) tot[set] = inc_e;
+  __syncthreads();
+  const int n_ro = tot[1], n_wo = tot[0];
+  const int64_t plan_id = (static_cast<int64_t>(b) * a.g.H + h) * a.n_chunks + c;
+  if (a.xch) {   // the chunk's out-norm partial sums: not yet written
+    unsigned long long* x = a.xch + plan_id * a.xgroups * kChunk;
+    for (int i = set * 64 + p; i < a.xgroups * kChunk; i += 128) x[i] = 0ull;
+  }
+  unsigned char* plan = a.plans + plan_id * PickGeom::stride();
+  uint2* ent = reinterpret_cast<uint2*>(plan + PickGeom::off_var() + 16);
+  if (set == 0 && p == 0) {
+    const int bytes = 16 + 8 * (n_ro + n_wo);
+    *reinterpret_cast<uint4*>(plan + PickGeom::off_var()) = make_uint4(
+        static_cast<uint32_t>(bytes), rmask ? 0x80000000u : 0u, static_cast<uint32_t>(n_ro), static_cast<uint32_t>(n_wo));
+    a.sizes[plan_id] = bytes;
+  }
+  const uint32_t mrow = static_cast<uint32_t>(M);
+  if (set == 1) {
+    const int e0 = inc_e - n_e;   // the position's first entry past its eighth contribution
+    float cj[KP];
+    uint32_t qj[KP];
+#pragma unroll
+    for (int i = 0; i < KP; ++i) {
+      cj[i] = 0.f;
+      qj[i] = 0u;
+    }
+    int j = 0;
+    while (touched) {
+      const int q = __builtin_ctzll(touched);
+      touched &= touched - 1ull;
+      float wq[KP];
+#pragma unroll
+      for (int i = 0; i < KP; ++i) wq[i] = wtab[min(rk[i], kChunk * KP - 1)];
+      float coef = 0.f;
+#pragma unroll
+      for (int i = 0; i < KP; ++i) {
+        const bool hit = (mk[i] >> q) & 1ull;
+        coef = fmaf(ws[i], hit ? wq[i] : 0.f, coef);
+        rk[i] += hit ? 1 : 0;
+      }
+      coef *= pw[p - 1 - q];
+      if (j < KP) {
+#pragma unroll
+        for (int t = 0; t < KP; ++t)
+          if (t == j) {
+            cj[t] = coef;
+            qj[t] = static_cast<uint32_t>(q);
+          }
+      } else {
+        ent[e0 + j - KP] = make_uint2(__float_as_uint(coef), static_cast<uint32_t>(q));
+      }
+      ++j;
+    }
+#pragma unroll
+    for (int i = 0; i < KP; ++i) {
+      const uint32_t slot = (p < L && i < kk) ? static_cast<uint32_t>(ms[i]) : mrow;
+      const float rw = (p < L && i < kk && seg0 < 0) ? ws[i] : 0.f;
+      *reinterpret_cast<uint4*>(plan + 16 * (i * kChunk + p)) =
+          make_uint4(slot | (qj[i] << 16) | (static_cast<uint32_t>(n_in) << 24), __float_as_uint(rw),
+                     __float_as_uint(cj[i]), static_cast<uint32_t>(e0));
+    }
+  } else {
+    int e = n_ro + inc_e - n_e;
+#pragma unroll
+    for (int jj = 0; jj < KP; ++jj) {
+      uint32_t w0 = mrow;
+      float wc = 0.f, l0 = 0.f;
+      const int e_first = e;
+      if ((own >> jj) & 1u) {
+        const int m = ms[jj];
+        w0 = static_cast<uint32_t>(m) | (static_cast<uint32_t>(nl[jj]) << 24);
+        wc = pw[L - 1 - p] * ws[jj];
+        if (nl[jj] > 0) {
+          unsigned long long mm = (wmask[m] & keep) & ~(1ull << p);   // every writer of m after p
+          int rank = rank_below(m, p) + 1;
+          const int q1 = __builtin_ctzll(mm);
+          mm &= mm - 1ull;
+          w0 |= static_cast<uint32_t>(q1) << 16;
+          l0 = pw[L - 1 - q1] * wtab[rank++];
+          while (mm) {
+            const int q = __builtin_ctzll(mm);
+            mm &= mm - 1ull;
+            ent[e++] = make_uint2(__float_as_uint(pw[L - 1 - q] * wtab[rank++]), static_cast<uint32_t>(q));
+          }
+        }
+      }
+      *reinterpret_cast<uint4*>(plan + PickGeom::off_w() + 16 * (jj * kChunk + p)) =
+          make_uint4(w0, __float_as_uint(wc), __float_as_uint(l0), static_cast<uint32_t>(e_first));
+    }
+  }
+}
 
 // plan_kernel: block (chunk, head, batch row), 128 threads: wave 0 addresses the write keys of the chunk's
 // positions, wave 1 the read queries (MODE 1, 2: on the matrix cores, MODE 0: per thread); the writers of every slot
 // are marked in 64-bit masks; wave 1 then finds each position's in-chunk read contributions, wave 0 each position's
 // owned writes and the later writers of the slots written more than once; entry counts are prefix-summed within
-// each wave.
-template <int HALF, int KP, typename InT, int MODE>
+// each wave.  PICK: the plan is a pick plan (emit_pick_plan) for pick_scan_kernel.
+template <int HALF, int KP, typename InT, int MODE, bool PICK = false>
 __global__ void __launch_bounds__(128, 4) plan_kernel(PlanArgs a) {
   constexpr PlanGeom pg{KP};
   const int c = blockIdx.x;
@@ -154,6 +295,10 @@ __global__ void __launch_bounds__(128, 4) plan_kernel(PlanArgs a) {
     for (int j = 0; j < kk; ++j) wtab[rank_below(ms[j], p)] = ws[j];
   }
   __syncthreads();
+  if constexpr (PICK) {
+    emit_pick_plan(a, b, h, c, set, p, L, M, kk, ms, ws, wmask, sbase, wtab, pw, tot, seg0, rmask, keep);
+    return;
+  }
   unsigned long long mk[KP];           // read side: the earlier writers of each read slot
   int rk[KP];                          // read side: the rank in wtab of each read slot's next earlier writer
   unsigned long long touched = 0ull;   // read side: every earlier position contributing to this one
@@ -296,25 +441,31 @@ __global__ void __launch_bounds__(128, 4) plan_kernel(PlanArgs a) {
 
 template <int HALF, typename InT>
 struct PlanLaunch {
-  template <int KP, int MODE>
+  template <int KP, int MODE, bool PICK>
   static int go(const Plan& p, const PlanArgs& a, hipStream_t st) {
     dim3 grid(p.n_chunks, p.H, p.B);
     const size_t lds = plan_dynamic_lds(p.M, KP) + (MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF);
-    static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MODE>));
+    static const bool ok = allow_lds(reinterpret_cast<const void*>(&plan_kernel<HALF, KP, InT, MODE, PICK>));
     if (!ok) return lds_err("plan");
-    hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MODE>), grid, dim3(128), lds, st, a);
+    hipLaunchKernelGGL((plan_kernel<HALF, KP, InT, MODE, PICK>), grid, dim3(128), lds, st, a);
     return check_launch("plan");
   }
-  static int run(const Plan& p, const PlanArgs& a, hipStream_t st) {
+  // pick: write pick plans (matrix-core addressing and picks of at most 8 only)
+  static int run(const Plan& p, const PlanArgs& a, hipStream_t st, bool pick) {
     if constexpr (mf_half(HALF)) {
-      if (use_mf(p)) return full_grid(p) ? go<8, 2>(p, a, st) : p.pitch == 8 ? go<8, 1>(p, a, st) : go<16, 1>(p, a, st);
+      if (use_mf(p)) {
+        if (pick) return full_grid(p) ? go<8, 2, true>(p, a, st) : go<8, 1, true>(p, a, st);
+        return full_grid(p) ? go<8, 2, false>(p, a, st)
+                            : p.pitch == 8 ? go<8, 1, false>(p, a, st) : go<16, 1, false>(p, a, st);
+      }
     }
-    return p.pitch == 8 ? go<8, 0>(p, a, st) : go<16, 0>(p, a, st);
+    if (pick) return set_err(SDM_RT_EINVAL, "pick plans need the matrix-core addressing");
+    return p.pitch == 8 ? go<8, 0, false>(p, a, st) : go<16, 0, false>(p, a, st);
   }
 };
 
 // defined in sdm_plan_bf16.hip and sdm_plan_f32.hip
-int launch_plan_bf16(const Plan& p, const PlanArgs& a, hipStream_t st);
-int launch_plan_f32(const Plan& p, const PlanArgs& a, hipStream_t st);
+int launch_plan_bf16(const Plan& p, const PlanArgs& a, hipStream_t st, bool pick);
+int launch_plan_f32(const Plan& p, const PlanArgs& a, hipStream_t st, bool pick);
 
 }  // namespace sdmrt

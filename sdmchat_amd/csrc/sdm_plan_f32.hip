@@ -3,6 +3,8 @@
 
 namespace sdmrt {
 
-int launch_plan_f32(const Plan& p, const PlanArgs& a, hipStream_t st) { return by_half<PlanLaunch, float>(p.half, p, a, st); }
+int launch_plan_f32(const Plan& p, const PlanArgs& a, hipStream_t st, bool pick) {
+  return by_half<PlanLaunch, float>(p.half, p, a, st, pick);
+}
 
 }  // namespace sdmrt

@@ -1,0 +1,142 @@
+"""GPU parity of the pick scan (pick plans + pick_scan_kernel), the scan sdm_rt_forward runs for picks of at most 8,
+head_dim a multiple of 32 and up to 1,024 locations, against the fp64 oracle.
+
+References: RunTimeSdm._chunk / forward / finish (track4_onesdm_models.py:215-274, :243-246) and the token
+recurrence of forward_sequential (:276-300) that the oracle restates; reset at BOS (:229-233, :287-289).
+
+The shapes here all take the pick path (head widths 32, 64 and 96, half widths 8 and 16, 64 or 256 locations); the
+cases mirror tests/test_gpu_core.py's for the other scan: lengths around the chunk, fades 0 and 1, the slab rescale,
+state carry, the final state, resets, crowded chunks whose plans overflow what the scan stages in LDS, unaligned
+value rows, three column groups sharing the out-norm, and the read modes.  Tolerances as there: float32 1e-5,
+bfloat16 2e-3 plus half a bfloat16 ulp.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests._gpu_util import assert_close, bf16_round, check_core, core_inputs, gpu_address, gpu_core, say
+
+pytestmark = pytest.mark.gpu
+
+PICK_PLAN_VAR = 2 * 64 * 8 * 16   # offset of a pick plan's variable part (after its read and write records)
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 130, 200])
+def test_ragged_lengths_and_extreme_fades(T):
+    decays = [0.0, 1.0, 0.5, 0.9, 0.99, 0.999, 0.0, 1.0]
+    check_core(*core_inputs(2, T, 8, 32, 16, 8, seed=144 + T, decays=decays, addr_bias=0.3), 8)
+
+
+def test_small_fades_rescale_the_slab_often():
+    check_core(*core_inputs(1, 400, 4, 32, 16, 8, seed=152, decays=(0.05, 0.1, 0.2, 0.3)), 8)
+
+
+@pytest.mark.parametrize("read_mode,out_norm,gate,dh", [("sum", True, True, 32), ("mean", False, True, 64),
+                                                        ("sum", False, False, 32), ("mean", True, False, 64)])
+def test_read_modes_norm_and_gate(read_mode, out_norm, gate, dh):
+    check_core(*core_inputs(1, 150, 4, dh, 32, 16, seed=145 + dh, gate=gate), 8, read_mode=read_mode,
+               out_norm=out_norm)
+
+
+def test_three_column_groups_share_the_out_norm():
+    """head_dim 96: three workgroups per slab add their partial sums of squares in one order."""
+    check_core(*core_inputs(2, 170, 2, 96, 16, 8, seed=146), 8)
+
+
+def test_fewer_picks_than_the_pitch():
+    """k = 5 of 64 locations: picks 5..7 of every record are pads (row M, weight 0)."""
+    check_core(*core_inputs(2, 140, 4, 32, 16, 8, seed=147, decays=(0.0, 0.7, 0.95, 1.0)), 5)
+
+
+def test_float32_values_bfloat16_out_and_unaligned_rows():
+    kz, qz, V, g, p = core_inputs(2, 100, 4, 64, 32, 16, seed=148)
+    check_core(kz, qz, V, g, p, 8, dtype=torch.float32, out_dtype=torch.bfloat16, tol=2e-3)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, out_dtype=torch.float32, tol=1e-5, fused=True)
+
+
+def test_state_carry_equals_one_pass():
+    kz, qz, V, g, p = core_inputs(2, 300, 4, 32, 16, 8, seed=149, decays=(0.0, 0.6, 0.99, 1.0))
+    r_all, (m_all, c_all) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
+    cut = 137
+    r1, st = gpu_core(kz[:, :cut], qz[:, :cut], V[:, :cut], g[:, :cut], p, 8, want_state=True)
+    r2, (m2, c2) = gpu_core(kz[:, cut:], qz[:, cut:], V[:, cut:], g[:, cut:], p, 8, state_in=st, want_state=True)
+    np.testing.assert_allclose(np.concatenate([r1, r2], 1), r_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(m2, m_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(c2, c_all, atol=1e-5, rtol=1e-5)
+
+
+def test_final_state_matches_oracle_recurrence():
+    from oracle import sdm_fp64 as O
+    B, T, H, dh = 2, 150, 4, 32
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 16, 8, seed=153, decays=(0.0, 0.5, 0.97, 1.0))
+    _, (mem, cnt) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
+    siw, _, ww = gpu_address(kz, p, 8, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8)
+    Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    _, _, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                       wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
+                                       (np.zeros((B, H, 64, dh)), np.zeros((B, H, 64))))
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,dh", [(64, 32), (150, 32), (150, 64)])
+def test_resets_match_the_oracle(T, dh):
+    from oracle import sdm_fp64 as O
+    B, H, n_sub = 3, 4, 8
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 16, n_sub, seed=190 + T + dh, decays=(0.0, 0.5, 0.97, 1.0))
+    reset = np.zeros((B, T), bool)
+    reset[0, [0, 20, 31, T - 1]] = True
+    reset[1, [1, 63]] = True
+    if T > 64:
+        reset[1, [64, 100, 101]] = True
+    r, (mem, cnt) = gpu_core(kz, qz, V, g, p, 8, want_state=True, reset=reset)
+    siw, _, ww = gpu_address(kz, p, 8, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8)
+    Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    num, den, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                           wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
+                                           (np.zeros((B, H, n_sub ** 2, dh)), np.zeros((B, H, n_sub ** 2))),
+                                           reset=reset)
+    r64 = O.finish(num, den, "mean", 1e-3, True, p["onorm_w"].astype(np.float64), 1e-2)
+    assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 1e-5, msg="read-out with resets")
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+
+
+def test_crowded_chunks_read_past_the_staged_plan():
+    """A large address bias sends every token to nearly the same locations: positions have dozens of in-chunk read
+    contributions (past the eight a pick plan keeps in its records) and slots many later writers, so the variable
+    parts run past the 4 KB the scan stages in LDS and the rest is read from the plan in global memory.  The
+    workspace shows that pick plans were written (their headers, at the pick plan's offset, hold the sizes) and
+    that they overflowed."""
+    from sdmchat_amd import core
+    B, T, H = 2, 200, 4
+    kz, qz, V, g, p = core_inputs(B, T, H, 32, 16, 8, seed=191, addr_bias=4.0)
+    check_core(kz, qz, V, g, p, 8)
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    ws = core.CoreWorkspace()
+    core.core_forward(*(torch.from_numpy(a).cuda() for a in (kz, qz, V, g)), keys1=tp["keys1"], keys2=tp["keys2"],
+                      log_scale=tp["log_scale"], decay=tp["decay"], addr_b=tp["addr_b"], onorm_w=tp["onorm_w"],
+                      gate_bias=tp["gate_bias"], k=8, workspace=ws)
+    torch.cuda.synchronize()
+    n_plans = B * H * ((T + 63) // 64)
+    buf = ws.buf.cpu()
+    sizes = buf[:4 * n_plans].view(torch.int32)
+    say(f"variable-part bytes per plan: max {int(sizes.max())}, mean {float(sizes.float().mean()):.0f}")
+    assert int(sizes.max()) > 4096
+    off_plans = (4 * n_plans + 255) // 256 * 256
+    stride = (len(buf) - off_plans) // n_plans   # an upper bound; the plans sit at a fixed stride from off_plans
+    hdr = buf[off_plans + PICK_PLAN_VAR:off_plans + PICK_PLAN_VAR + 4].view(torch.int32)
+    assert int(hdr[0]) == int(sizes[0]) and stride > PICK_PLAN_VAR
+
+
+def test_bench_shape_slabs_bf16():
+    """B=8, T=2048, H=12 in bfloat16 (the bench workload): picks against the oracle and the read-out of four slabs
+    against the fp64 recurrence on the kernel's picks."""
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=151)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3,
+                       slabs=[(0, 0), (2, 5), (5, 9), (7, 11)])
+    say("bench-shape picks that differ from the oracle (all at near-ties):", flips)
