@@ -25,6 +25,12 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _rows16(t2):
+    """A 2-D view whose rows are contiguous and all start 16-byte aligned."""
+    es = t2.element_size()
+    return t2.stride(1) == 1 and t2.data_ptr() % 16 == 0 and (t2.stride(0) * es) % 16 == 0
+
+
 def _f32(t, device):
     if t is None:
         return None
@@ -373,7 +379,7 @@ def rms_norm(x, w, eps=1e-6, out_dtype=None, out=None):
         raise ValueError(f"rms_norm: dtype {x.dtype} is not float32 or bfloat16")
     d = x.shape[-1]
     x2 = x.reshape(-1, d)
-    if x2.numel() and x2.stride(1) != 1:
+    if x2.numel() and not _rows16(x2):   # the kernel reads rows in 16-byte pieces
         x2 = x2.contiguous()
     out_dtype = out_dtype or x.dtype
     if out is None:
@@ -444,7 +450,7 @@ def silu_mul(gate_up):
         raise ValueError("silu_mul needs a float32 or bfloat16 ROCm tensor")
     f2 = gate_up.shape[-1]
     g2 = gate_up.reshape(-1, f2)
-    if g2.stride(1) != 1:
+    if g2.numel() and not _rows16(g2):   # the kernel reads rows in 16-byte pieces
         g2 = g2.contiguous()
     out = torch.empty(gate_up.shape[:-1] + (f2 // 2,), dtype=gate_up.dtype, device=gate_up.device)
     lib = _lib.load()

@@ -24,7 +24,7 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   uint32_t* sync = reinterpret_cast<uint32_t*>(ws + p.off_sync);
   float* xch = reinterpret_cast<float*>(ws + p.off_xch);
   const size_t vb = io.in_dtype == SDM_RT_BF16 ? 2 : 4;
-  const bool pick = pick_enabled() && pick_path(p, static_cast<int>(vb));
+  const bool pick = pick_enabled() && pick_path(p);
   const int cw = pick ? kPickCols : scan_cw(p, io.in_dtype);
   if (!cw) return SDM_RT_EUNSUPPORTED;
 

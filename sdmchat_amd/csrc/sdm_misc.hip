@@ -5,51 +5,97 @@
 
 namespace sdmrt {
 
-// rms_norm: one wave per row; lanes take 8 consecutive values at a time.  ADD: the row is x + y rounded to the input
-// type (a residual add), which is also written to sum (in place over x is allowed: each value is read and written
-// by the same lane).
-template <typename InT, typename OutT, bool ADD>
+// x rounded to T and back (bfloat16: the hardware conversion, nearest even)
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (sizeof(T) == 2) return __uint_as_float(pack_bf16(x, 0.f) << 16);
+  else return x;
+}
+// 8 values from / to T (16-byte pieces: p is 16-byte aligned, as the launchers check)
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = __uint_as_float(w[e] << 16);
+      v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  } else {
+    const float4 q0 = reinterpret_cast<const float4*>(p)[0], q1 = reinterpret_cast<const float4*>(p)[1];
+    v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+    v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                                              pack_bf16(v[6], v[7]));
+  } else {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+// the sum over the 32 lanes of each half of the wave, in every lane of the half (DPP within rows of 16, then
+// rows 0 + 1 and 2 + 3, read back from lanes 31 and 63)
+__device__ __forceinline__ float half_wave_sum(float v, int lane) {
+  v += dpp_f<0xb1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror: every lane of a row holds the row's sum
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));   // row_bcast:15
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  return lane < 32 ? lo : hi;
+}
+
+// rms_norm: two rows per wave, 32 lanes per row, each lane taking 8 consecutive values at a time (KC pieces of 8
+// per lane, KC = ceil(d / 256)); the row, the residual and the weights are all loaded before any use.  ADD: the row
+// is x + y rounded to the input type (a residual add), which is also written to sum (in place over x is allowed:
+// each value is read and written by the same lane).
+template <typename InT, typename OutT, bool ADD, int KC>
 __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* x, int64_t x_stride, const InT* y, int64_t y_stride,
                                                        InT* sum, int64_t sum_stride, OutT* __restrict__ out,
                                                        int64_t out_stride, const float* __restrict__ w, int64_t rows,
                                                        int d, float eps) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= rows) return;   // whole waves
-  const InT* src = x + row * x_stride;
-  constexpr int kMax = 4;    // 8 * 64 * 4 = 2048 values per row in registers
-  float v[kMax][8];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6) * 2 + (lane >> 5);
+  const int hl = lane & 31;
+  const bool live = row < rows;   // both halves of a wave take part in the sums
+  const int64_t r = live ? row : 0;
+  float v[KC][8], wv[KC][8];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMax; ++k) {
-    const int c = 8 * (lane + 64 * k);
+  for (int k = 0; k < KC; ++k) {
+    const int c = 8 * (hl + 32 * k);
     if (c < d) {
-      load_vals<8, InT>(src + c, v[k]);
+      load8<InT>(x + r * x_stride + c, v[k]);
+      load8<float>(w + c, wv[k]);
       if constexpr (ADD) {
         float u[8];
-        load_vals<8, InT>(y + row * y_stride + c, u);
+        load8<InT>(y + r * y_stride + c, u);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[k][e] = to_f32(from_f32<InT>(v[k][e] + u[e]));   // x + y in the input type
-        store_vals<8, InT>(sum + row * sum_stride + c, v[k]);
+        for (int e = 0; e < 8; ++e) v[k][e] = round_to<InT>(v[k][e] + u[e]);   // x + y in the input type
+        if (live) store8<InT>(sum + r * sum_stride + c, v[k]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
     }
   }
+  ss = half_wave_sum(ss, lane);
+  const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
+  if (!live) return;
+  OutT* dst = out + r * out_stride;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
-  OutT* dst = out + row * out_stride;
-#pragma unroll
-  for (int k = 0; k < kMax; ++k) {
-    const int c = 8 * (lane + 64 * k);
+  for (int k = 0; k < KC; ++k) {
+    const int c = 8 * (hl + 32 * k);
     if (c < d) {
-      float wv[8];
-      load_vals<8, float>(w + c, wv);
       float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = to_f32(from_f32<InT>(v[k][e] * r)) * wv[e];   // .to(x.dtype) * w
-      store_vals<8, OutT>(dst + c, o);
+      for (int e = 0; e < 8; ++e) o[e] = round_to<InT>(v[k][e] * rs) * wv[k][e];   // .to(x.dtype) * w
+      store8<OutT>(dst + c, o);
     }
   }
 }
@@ -65,14 +111,13 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const T* __restrict__ gu,
   const int c = static_cast<int>(i - row * per_row);
   if (row >= rows) return;
   float g[8], u[8], o[8];
-  load_vals<8, T>(gu + row * gu_stride + c, g);
-  load_vals<8, T>(gu + row * gu_stride + f + c, u);
+  load8<T>(gu + row * gu_stride + c, g);
+  load8<T>(gu + row * gu_stride + f + c, u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float s = to_f32(from_f32<T>(g[e] / (1.f + expf(-g[e]))));
-    o[e] = s * u[e];
+    o[e] = round_to<T>(g[e] / (1.f + expf(-g[e]))) * u[e];
   }
-  store_vals<8, T>(out + row * out_stride + c, o);
+  store8<T>(out + row * out_stride + c, o);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -197,6 +242,26 @@ __global__ void __launch_bounds__(256) table_read_sliced_kernel(const int32_t* _
   store_vals<kVec, OutT>(out + n * out_stride + static_cast<int64_t>(h) * dh + c0, acc);
 }
 
+// a row-major array whose rows all start 16-byte aligned (the norm and silu kernels load 16 bytes at a time)
+inline bool aligned16(const void* p, int64_t row_stride, sdm_rt_dtype dt) {
+  const int64_t es = dt == SDM_RT_BF16 ? 2 : 4;
+  return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (row_stride * es) % 16 == 0;
+}
+
+// rms_norm_kernel with kc pieces of 8 values per lane (d <= 256 kc)
+template <typename IT, typename OT, bool ADD, typename... Args>
+int norm_launch(int kc, unsigned blocks, hipStream_t st, Args... args) {
+  switch (kc) {
+    case 1: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 1>), dim3(blocks), dim3(256), 0, st, args...); break;
+    case 2: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 2>), dim3(blocks), dim3(256), 0, st, args...); break;
+    case 3: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 3>), dim3(blocks), dim3(256), 0, st, args...); break;
+    case 4: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 4>), dim3(blocks), dim3(256), 0, st, args...); break;
+    case 5: case 6: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 6>), dim3(blocks), dim3(256), 0, st, args...); break;
+    default: hipLaunchKernelGGL((rms_norm_kernel<IT, OT, ADD, 8>), dim3(blocks), dim3(256), 0, st, args...); break;
+  }
+  return SDM_RT_OK;
+}
+
 }  // namespace sdmrt
 
 using namespace sdmrt;
@@ -215,11 +280,14 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
   if (rows == 0) return SDM_RT_OK;
   if (!x || !w || !out) return set_err(SDM_RT_EINVAL, "x, w and out must not be NULL");
   if (x_row_stride < d || out_row_stride < d) return set_err(SDM_RT_EINVAL, "row strides must be >= d");
+  if (!aligned16(x, x_row_stride, in_dtype) || !aligned16(out, out_row_stride, out_dtype) || !aligned16(w, 0, SDM_RT_F32))
+    return set_err(SDM_RT_EINVAL, "x, out and w rows must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
-#define SDM_RT_NORM(IT, OT)                                                                                     \
-  hipLaunchKernelGGL((rms_norm_kernel<IT, OT, false>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x), \
-                     x_row_stride, nullptr, 0, nullptr, 0, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  const unsigned blocks = static_cast<unsigned>((rows + 7) / 8);
+  const int kc = (d + 255) / 256;
+#define SDM_RT_NORM(IT, OT)                                                                                       \
+  rc = norm_launch<IT, OT, false>(kc, blocks, st, static_cast<const IT*>(x), x_row_stride, nullptr, 0, nullptr, 0, \
+                                  static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
   if (in_dtype == SDM_RT_BF16) {
     if (out_dtype == SDM_RT_BF16) SDM_RT_NORM(bf16_t, bf16_t);
     else SDM_RT_NORM(bf16_t, float);
@@ -228,6 +296,7 @@ int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, 
     else SDM_RT_NORM(float, float);
   }
 #undef SDM_RT_NORM
+  if (rc) return rc;
   return check_launch("rms_norm");
 }
 
@@ -245,12 +314,17 @@ int sdm_rt_add_rms_norm(const void* x, int64_t x_row_stride, const void* y, int6
   if (!x || !y || !w || !sum_out || !out) return set_err(SDM_RT_EINVAL, "x, y, w, sum_out and out must not be NULL");
   if (x_row_stride < d || y_row_stride < d || sum_row_stride < d || out_row_stride < d)
     return set_err(SDM_RT_EINVAL, "row strides must be >= d");
+  if (!aligned16(x, x_row_stride, in_dtype) || !aligned16(y, y_row_stride, in_dtype) ||
+      !aligned16(sum_out, sum_row_stride, in_dtype) || !aligned16(out, out_row_stride, out_dtype) ||
+      !aligned16(w, 0, SDM_RT_F32))
+    return set_err(SDM_RT_EINVAL, "x, y, sum_out, out and w rows must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
-#define SDM_RT_ADD_NORM(IT, OT)                                                                                   \
-  hipLaunchKernelGGL((rms_norm_kernel<IT, OT, true>), dim3(blocks), dim3(256), 0, st, static_cast<const IT*>(x),   \
-                     x_row_stride, static_cast<const IT*>(y), y_row_stride, static_cast<IT*>(sum_out),              \
-                     sum_row_stride, static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
+  const unsigned blocks = static_cast<unsigned>((rows + 7) / 8);
+  const int kc = (d + 255) / 256;
+#define SDM_RT_ADD_NORM(IT, OT)                                                                                \
+  rc = norm_launch<IT, OT, true>(kc, blocks, st, static_cast<const IT*>(x), x_row_stride,                       \
+                                 static_cast<const IT*>(y), y_row_stride, static_cast<IT*>(sum_out), sum_row_stride, \
+                                 static_cast<OT*>(out), out_row_stride, w, rows, d, eps)
   if (in_dtype == SDM_RT_BF16) {
     if (out_dtype == SDM_RT_BF16) SDM_RT_ADD_NORM(bf16_t, bf16_t);
     else SDM_RT_ADD_NORM(bf16_t, float);
@@ -259,6 +333,7 @@ int sdm_rt_add_rms_norm(const void* x, int64_t x_row_stride, const void* y, int6
     else SDM_RT_ADD_NORM(float, float);
   }
 #undef SDM_RT_ADD_NORM
+  if (rc) return rc;
   return check_launch("add_rms_norm");
 }
 
@@ -273,6 +348,8 @@ int sdm_rt_silu_mul(const void* gate_up, int64_t gate_up_row_stride, sdm_rt_dtyp
   if (!gate_up || !out) return set_err(SDM_RT_EINVAL, "gate_up and out must not be NULL");
   if (gate_up_row_stride < 2 * static_cast<int64_t>(f) || out_row_stride < f)
     return set_err(SDM_RT_EINVAL, "gate_up_row_stride must be >= 2 f and out_row_stride >= f");
+  if (!aligned16(gate_up, gate_up_row_stride, dtype) || !aligned16(out, out_row_stride, dtype))
+    return set_err(SDM_RT_EINVAL, "gate_up and out rows must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t threads = rows * (f / 8);
   const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);

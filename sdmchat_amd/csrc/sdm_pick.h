@@ -29,18 +29,17 @@ constexpr int kPickThreads = 1024;   // 64 positions x 8 picks x 2 column halves
 constexpr int kPickCols = 32;        // value columns per workgroup
 
 // LDS of one pick scan workgroup: the slab A[M + 1][32] and counts cnt[M + 1], by chunk parity two buffers of the
-// chunk's value rows [64][32] (vb bytes per value) and of its staged variable part, the fade powers pw[68] and the
-// variable-part sizes of the n_chunks plans
-__host__ __device__ constexpr size_t pick_lds_bytes(int M, int n_chunks, int vb) {
+// chunk's value rows [64][32] (float32, whatever the value type) and of its staged variable part, the fade powers
+// pw[68] and the variable-part sizes of the n_chunks plans
+__host__ __device__ constexpr size_t pick_lds_bytes(int M, int n_chunks) {
   return sizeof(float) * (static_cast<size_t>(M + 1) * kPickCols + pad4(M + 1)) +
-         2 * static_cast<size_t>(vb) * kChunk * kPickCols + 2 * static_cast<size_t>(kVarStage) + sizeof(float) * 68 +
+         2 * sizeof(float) * kChunk * kPickCols + 2 * static_cast<size_t>(kVarStage) + sizeof(float) * 68 +
          sizeof(int32_t) * pad4(n_chunks);
 }
 
 // the pick scan serves this shape (values of vb bytes)
-inline bool pick_path(const Plan& p, int vb) {
-  return use_mf(p) && p.pitch == 8 && p.dh % kPickCols == 0 && p.M <= 1024 &&
-         pick_lds_bytes(p.M, p.n_chunks, vb) <= kLdsBytes;
+inline bool pick_path(const Plan& p) {
+  return use_mf(p) && p.pitch == 8 && p.dh % kPickCols == 0 && p.M <= 1024 && pick_lds_bytes(p.M, p.n_chunks) <= kLdsBytes;
 }
 
 template <int CTRL>
@@ -61,20 +60,9 @@ __device__ __forceinline__ float pos_sum(float v) {
   return v;
 }
 
-// four consecutive values of a value row (bfloat16: raw pairs, float32: floats)
+// four consecutive float32 values of a value row in LDS
 template <typename VT>
 struct VPiece;
-template <>
-struct VPiece<bf16_t> {
-  uint2 w;
-  __device__ __forceinline__ void load(const bf16_t* p) { w = *reinterpret_cast<const uint2*>(p); }
-  __device__ __forceinline__ void fma4(float c, float* acc) const {
-    acc[0] = fmaf(c, __uint_as_float(w.x << 16), acc[0]);
-    acc[1] = fmaf(c, __uint_as_float(w.x & 0xffff0000u), acc[1]);
-    acc[2] = fmaf(c, __uint_as_float(w.y << 16), acc[2]);
-    acc[3] = fmaf(c, __uint_as_float(w.y & 0xffff0000u), acc[3]);
-  }
-};
 template <>
 struct VPiece<float> {
   float4 w;
@@ -104,7 +92,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   const int h = s - b_row * a.H;
   float* A = lds;                                                          // [M + 1][32]
   float* cnt = A + static_cast<size_t>(M + 1) * CW;                        // [M + 1]
-  VT* s_v = reinterpret_cast<VT*>(cnt + pad4(M + 1));                      // [2][64][32]
+  float* s_v = cnt + pad4(M + 1);                                          // [2][64][32]
   unsigned char* var = reinterpret_cast<unsigned char*>(s_v + 2 * kChunk * CW);   // [2][VS]
   float* pw = reinterpret_cast<float*>(var + 2 * VS);                      // [68]
   int32_t* s_sizes = reinterpret_cast<int32_t*>(pw + 68);
@@ -179,14 +167,37 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
                                PickGeom::off_var() + 4 * tid;
     return 4 * tid < min(bytes, VS) ? *reinterpret_cast<const uint32_t*>(src) : 0u;
   };
-  auto stage = [&](int c, const VPair& vv, uint32_t vr) {
-    *reinterpret_cast<VPair*>(s_v + (c & 1) * kChunk * CW + p * CW + 2 * u) = vv;
+  auto stage = [&](int c, const VPair& vv, uint32_t vr) {   // the values as float32
+    float2 f;
+    if constexpr (sizeof(VT) == 2) f = make_float2(__uint_as_float(vv << 16), __uint_as_float(vv & 0xffff0000u));
+    else f = make_float2(__uint_as_float(vv.x), __uint_as_float(vv.y));
+    *reinterpret_cast<float2*>(s_v + (c & 1) * kChunk * CW + p * CW + 2 * u) = f;
     reinterpret_cast<uint32_t*>(var + (c & 1) * VS)[tid] = vr;
   };
+  // the lane's two read-out columns at position p of chunk 0; chunk c is c * 64 rows further (bfloat16 rounded to
+  // nearest even by the hardware conversion)
+  OutT* r_lane = static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b_row) * a.T + p) * a.r_stride +
+                 static_cast<int64_t>(h) * a.dh + col0 + fcol;
+  const bool r_vec = reinterpret_cast<uintptr_t>(r_lane) % (2 * sizeof(OutT)) == 0 &&
+                     (static_cast<uint64_t>(a.r_stride) * sizeof(OutT)) % (2 * sizeof(OutT)) == 0;
   auto store_r = [&](int c, const float (&x)[2]) {
-    OutT* dst = static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b_row) * a.T + c * kChunk + p) * a.r_stride +
-                static_cast<int64_t>(h) * a.dh + col0 + fcol;
-    store_vals<2, OutT>(dst, x);
+    OutT* dst = r_lane + static_cast<int64_t>(c) * kChunk * a.r_stride;
+    if constexpr (sizeof(OutT) == 2) {
+      const uint32_t w = pack_bf16(x[0], x[1]);
+      if (r_vec) {
+        *reinterpret_cast<uint32_t*>(dst) = w;
+      } else {
+        reinterpret_cast<uint16_t*>(dst)[0] = static_cast<uint16_t>(w);
+        reinterpret_cast<uint16_t*>(dst)[1] = static_cast<uint16_t>(w >> 16);
+      }
+    } else {
+      if (r_vec) {
+        *reinterpret_cast<float2*>(dst) = make_float2(x[0], x[1]);
+      } else {
+        dst[0] = x[0];
+        dst[1] = x[1];
+      }
+    }
   };
   // The out-norm exchange between the G groups of a slab: every group stores its per-position partial sum of
   // squares of chunk c as one 64-bit word {sum, 1} (the plan kernel cleared the words), and finishes chunk c's
@@ -254,7 +265,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     const int c0 = c * kChunk;
     const int L = min(kChunk, a.T - c0);
     const unsigned char* varc = var + (c & 1) * VS;
-    const VT* s_vc = s_v + (c & 1) * kChunk * CW;
+    const float* s_vc = s_v + (c & 1) * kChunk * CW;
     const int bytes = s_sizes[c];
     const bool all_staged = bytes <= VS;
     const unsigned char* gvar =
@@ -281,8 +292,8 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     float dl = sw * cnt[rslot];
     if (pick < n_in) {   // contribution number `pick` of the position
       const float cc = __uint_as_float(rr.z);
-      const VT* vrow = s_vc + ((rr.x >> 16) & 63u) * CW;
-      VPiece<VT> vq[4];
+      const float* vrow = s_vc + ((rr.x >> 16) & 63u) * CW;
+      VPiece<float> vq[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) vq[t].load(vrow + soff[t] / 4);
 #pragma unroll
@@ -294,7 +305,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         for (int j = 8 + pick; j < n_in; j += 8) {
           const uint2 e = ent_at(static_cast<int>(rr.w) + j - 8, st);
           const float ce = __uint_as_float(e.x);
-          VPiece<VT> vq[4];
+          VPiece<float> vq[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) vq[t].load(s_vc + (e.y & 63u) * CW + soff[t] / 4);
 #pragma unroll
@@ -387,7 +398,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         y[4 * t + 2] = q4.z;
         y[4 * t + 3] = q4.w;
       }
-      VPiece<VT> vp[4];
+      VPiece<float> vp[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) vp[t].load(s_vc + p * CW + soff[t] / 4);
       const float a0 = __uint_as_float(wr.y) * inv_mu;
@@ -396,7 +407,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
       for (int t = 0; t < 4; ++t) vp[t].fma4(a0, y + 4 * t);
       if (n_l > 0) {
         const float a1 = __uint_as_float(wr.z) * inv_mu;
-        VPiece<VT> vl[4];
+        VPiece<float> vl[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) vl[t].load(s_vc + ((wr.x >> 16) & 63u) * CW + soff[t] / 4);
 #pragma unroll
@@ -407,7 +418,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
             for (int e = 0; e < n_l - 1; ++e) {
               const uint2 en = ent_at(static_cast<int>(wr.w) + e, st);
               const float ae = __uint_as_float(en.x) * inv_mu;
-              VPiece<VT> ve[4];
+              VPiece<float> ve[4];
 #pragma unroll
               for (int t = 0; t < 4; ++t) ve[t].load(s_vc + (en.y & 63u) * CW + soff[t] / 4);
 #pragma unroll
@@ -451,12 +462,12 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
 
 template <typename VT, typename OutT>
 int launch_pick_scan_t(const Plan& p, const ScanArgs& a, hipStream_t st) {
-  const size_t lds = pick_lds_bytes(p.M, p.n_chunks, static_cast<int>(sizeof(VT)));
+  const size_t lds = pick_lds_bytes(p.M, p.n_chunks);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&pick_scan_kernel<VT, OutT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(kLdsBytes));
   if (attr != hipSuccess) return set_err(SDM_RT_ELAUNCH, "pick scan: cannot enable %zu bytes of LDS", kLdsBytes);
-  if (a.groups * kPickCols != p.dh || a.sync_stride < a.groups || !pick_path(p, static_cast<int>(sizeof(VT))))
+  if (a.groups * kPickCols != p.dh || a.sync_stride < a.groups || !pick_path(p))
     return set_err(SDM_RT_EINVAL, "pick scan: %d groups for head_dim %d", a.groups, p.dh);
   const int slabs8 = (p.B * p.H + 7) / 8 * 8;
   hipLaunchKernelGGL((pick_scan_kernel<VT, OutT>), dim3(slabs8 * a.groups), dim3(kPickThreads), lds, st, a);
