@@ -200,6 +200,16 @@ int sdm_rt_add_rms_norm(const void* x, int64_t x_row_stride, const void* y, int6
 int sdm_rt_silu_mul(const void* gate_up, int64_t gate_up_row_stride, sdm_rt_dtype dtype, int64_t rows, int32_t f,
                     void* out, int64_t out_row_stride, void* stream);
 
+/* y = x W^T (+ bias) for a few rows of x (bfloat16 in and out, float32 sums, bias added before the one rounding):
+ * a decode step's dense maps, F.linear / matmul in the reference (RunTimeSdm's wk, wq, wv, wg and wo,
+ * track4_onesdm_models.py:199-207, :247; TrainedSdm's wq and wo, :443-455) when x holds one token per stream.
+ *   x  [rows][k] bf16, row stride >= k;  W  [n][k] bf16 (a Linear's weight), row stride >= k;  bias  [n] bf16 or NULL;
+ *   y  [rows][n] bf16, row stride >= n.  n a multiple of 32, k a positive multiple of 64, x and W rows 16-byte
+ *   aligned.  Every workgroup takes 64 rows x 32 columns and splits k over four waves, whose sums are added in a
+ *   fixed order (deterministic). */
+int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, const void* bias,
+                     void* y, int64_t y_row_stride, int64_t rows, int32_t n, int32_t k, void* stream);
+
 /* ---- training: forward with saved tensors, and the backward ------------------------------------------------
  * The reference trains RunTimeSdm through torch autograd of its chunked dense forward (RunTimeSdm.forward under
  * torch.utils.checkpoint, track4_onesdm_models.py:259-268).  These two entry points replace that autograd for the

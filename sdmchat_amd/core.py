@@ -461,6 +461,41 @@ def silu_mul(gate_up):
     return out
 
 
+GEMM_ROWS_MAX = 256   # row counts up to this use sdm_rt_gemm_rows; larger products go to the GEMM library
+
+
+def linear(x, w, bias=None, as_matmul=False):
+    """F.linear(x, w, bias) (y = x w^T + bias).  A bfloat16 product of a few rows (a decode step's projections:
+    at most GEMM_ROWS_MAX rows of x, w [n, k] with n a multiple of 32 and k of 64) runs on sdm_rt_gemm_rows, float32
+    sums and the bias added before the one rounding, as the GEMM library rounds; every other product is F.linear
+    (torch.matmul(x, w.t()) with ``as_matmul``, for the call sites written that way)."""
+    k = x.shape[-1]
+    n = w.shape[0]
+    rows = x.numel() // k if k else 0
+    fits = (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2
+            and w.shape[1] == k and (bias is None or (bias.dtype == torch.bfloat16 and bias.numel() == n))
+            and 0 < rows <= GEMM_ROWS_MAX and n % 32 == 0 and n > 0 and k % 64 == 0 and k > 0
+            and not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, w, bias))))
+    if not fits:
+        if as_matmul and bias is None:
+            return torch.matmul(x, w.t())
+        return torch.nn.functional.linear(x, w, bias)
+    x2 = x.reshape(rows, k)
+    if not _rows16(x2):
+        x2 = x2.contiguous()
+    if not _rows16(w):
+        w = w.contiguous()
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    y = torch.empty(x.shape[:-1] + (n,), dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.sdm_rt_gemm_rows(_ptr(x2), x2.stride(0), _ptr(w), w.stride(0), _ptr(bias), _ptr(y), n, rows, n, k,
+                              ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return y
+
+
 def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape

@@ -55,7 +55,7 @@ class SwiGLU(nn.Module):
         if (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))) \
                 or x.device.type != "cuda" or torch.is_autocast_enabled("cuda"):
             return self.down(F.silu(self.gate(x)) * self.up(x))
-        return self.down(core.silu_mul(F.linear(x, self._gate_up())))
+        return core.linear(core.silu_mul(core.linear(x, self._gate_up())), self.down.weight, self.down.bias)
 
 
 def trained_sdm_params(d, n_sub, heads, d_a):
@@ -147,7 +147,9 @@ class OneSdmLM(nn.Module):
         return self.emb(idx)
 
     def project(self, h):
-        return h @ self.emb.weight.t() if self.tie else self.head(h)
+        if self.tie:
+            return core.linear(h, self.emb.weight, as_matmul=True)   # h @ E^T
+        return core.linear(h, self.head.weight, self.head.bias)
 
     def unfold(self, x):
         return self.project(_norm(x, self.nf))

@@ -157,7 +157,7 @@ class RunTimeSdm(nn.Module):
         if hx is None:
             hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
         W, bias = self._fused_weight(dt)[:2]
-        proj = F.linear(hx, W, bias)                                   # [B, T, padded rows]
+        proj = core.linear(hx, W, bias)                                # [B, T, padded rows]
         o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
         g = proj[..., o_g:o_g + H] if self.write_gate else None
         return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
@@ -281,7 +281,7 @@ class RunTimeSdm(nn.Module):
                 k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
                 out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
                 params=self._core_params(x.device))
-            y = torch.matmul(r, wo.t()).to(x.dtype)
+            y = core.linear(r, wo, as_matmul=True).to(x.dtype)
         return y.reshape(x.shape)
 
     def forward_sequential(self, x, reset=None):

@@ -76,7 +76,7 @@ class TrainedSdm(nn.Module):
         when the caller computed it."""
         if hx is None:
             hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
-        q = torch.matmul(hx, self._weights(dt)[0].t())
+        q = core.linear(hx, self._weights(dt)[0], as_matmul=True)
         if self.keep_picks:
             self.last_q = q
         prm = self._prm.get(x.device, self.keys1, self.keys2, None, self.log_scale, None, None, None)
@@ -116,7 +116,7 @@ class TrainedSdm(nn.Module):
         with torch.autocast("cuda", enabled=False):
             si, _, w = self._picks(x, dt, hx)
             r = core.table_read(si, w, self.values, self.k, out_dtype=dt)
-            y = torch.matmul(r, self._weights(dt)[1].t()).to(x.dtype)
+            y = core.linear(r, self._weights(dt)[1], as_matmul=True).to(x.dtype)
         kk = min(self.k, min(self.k, self.n_sub) ** 2)
         self.last_si = si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
         return y

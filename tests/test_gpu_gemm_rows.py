@@ -1,0 +1,59 @@
+"""GPU tests of sdm_rt_gemm_rows (core.linear for a few bfloat16 rows: a decode step's projections, F.linear in the
+reference, track4_onesdm_models.py:199-207, :247, :443-455) against the float32 product of the same bfloat16 inputs:
+the kernel sums in float32 (in another order than a GEMM library) and rounds once, with the bias, to bfloat16, so
+every value is within one bfloat16 unit of the float32 product rounded, and nearly all equal it."""
+import pytest
+import torch
+
+from sdmchat_amd import core
+from tests._gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(x, w, b):
+    y = x.float() @ w.float().t()
+    if b is not None:
+        y = y + b.float()
+    return y
+
+
+@pytest.mark.parametrize("rows,n,k,bias", [(64, 2560, 768, True), (64, 768, 768, False), (1, 768, 768, True),
+                                           (37, 4096, 768, False), (100, 768, 2048, False), (256, 32768, 768, False),
+                                           (5, 96, 128, True)])
+def test_gemm_rows_matches_float32_product(rows, n, k, bias):
+    g = torch.Generator(device="cpu").manual_seed(rows * 7 + n + k)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(torch.bfloat16).cuda()
+    b = torch.randn(n, generator=g).to(torch.bfloat16).cuda() if bias else None
+    say("gemm_rows", rows, n, k, bias)
+    with torch.no_grad():
+        got = core.linear(x, w, b)
+    want = _ref(x, w, b)
+    assert got.dtype == torch.bfloat16 and got.shape == (rows, n)
+    diff = (got.float() - want).abs()
+    assert bool((diff <= want.abs() * 2.0 ** -7 + 1e-6).all()), float((diff - want.abs() * 2.0 ** -7).max())
+    assert float((got == want.to(torch.bfloat16)).float().mean()) > 0.97
+
+
+def test_gemm_rows_strided_rows_batched_shape_and_determinism():
+    g = torch.Generator(device="cpu").manual_seed(3)
+    base = torch.randn(8, 3, 1024, generator=g).to(torch.bfloat16).cuda()
+    x = base[:, 1, 128:896]                  # rows 3 * 1024 apart, 16-byte aligned
+    w = (torch.randn(768, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        y1 = core.linear(x, w, as_matmul=True)
+        y2 = core.linear(x.contiguous()[None], w, as_matmul=True)[0]
+    assert torch.equal(y1, y2)
+    d = (y1.float() - _ref(x, w, None)).abs()
+    assert bool((d <= _ref(x, w, None).abs() * 2.0 ** -7 + 1e-6).all())
+
+
+def test_gemm_rows_leaves_other_products_to_the_library():
+    x = torch.randn(300, 768, device="cuda").to(torch.bfloat16)   # more rows than the kernel takes
+    w = torch.randn(64, 768, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        assert torch.equal(core.linear(x, w), torch.nn.functional.linear(x, w))
+    wr = w.clone().requires_grad_(True)                            # autograd recording: the library's product
+    y = core.linear(x[:8], wr)
+    assert y.grad_fn is not None
