@@ -230,8 +230,9 @@ class RunTimeSdm(nn.Module):
                 self.last_picks = tuple(
                     core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
                                  params=prm)[0] for z in (kz, qz))
-        # the gate logits alone ([B, T, H]; a view would keep the whole projection buffer alive)
-        self._gate_src = (g.contiguous() if g is not None else None, None, (B, T, H), x.device)
+        # the gate logits as a view of the projection buffer ([B, T, H], strided): a copy costs a launch per layer,
+        # the view keeps the buffer until the next forward (the whole fused projection, ~84 MB at B=8, T=2048)
+        self._gate_src = (g, None, (B, T, H), x.device)
         self._last_gate = None
         self.last_state = state
         return y
