@@ -194,7 +194,7 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
 // owned writes and the later writers of the slots written more than once; entry counts are prefix-summed within
 // each wave.  PICK: the plan is a pick plan (emit_pick_plan) for pick_scan_kernel.
 template <int HALF, int KP, typename InT, int MODE, bool PICK = false>
-__global__ void __launch_bounds__(128, 4) plan_kernel(PlanArgs a) {
+__global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
   constexpr PlanGeom pg{KP};
   const int c = blockIdx.x;
   const int h = blockIdx.y;
