@@ -871,27 +871,34 @@ struct PlanGeom {
   __host__ __device__ constexpr int stride() const { return (off_var() + 16 + 8 * max_entries() + 255) / 256 * 256; }
 };
 
-// The pick plan (picks of at most 8; written by plan_kernel<..., PICK = true>, executed by pick_scan_kernel):
-//   read records R[8][64], 16 bytes each, record (i, p) for pick i of position p:
+// The pick plan (picks of at most 8, at most 1,024 locations; written by plan_kernel<..., PICK = true>, executed by
+// pick_scan_kernel):
+//   read records R[8][64], 12 bytes each, record (i, p) for pick i of position p:
 //     w0  read slot (bits 0..15; pads and positions past the chunk's end: M) | q (bits 16..21) | n_in (bits 24..31)
 //     w1  read weight (0 for pads and when a reset earlier in the chunk hides the carried state)
 //     w2  coefficient of the position's in-chunk read contribution number i (q its source position), 0 if i >= n_in
-//     w3  entry index of the position's contributions past the eighth (contribution j >= 8 is entry w3 + j - 8)
-//   write records W[8][64]:
-//     w0  write slot if p owns it (the first writer of the slot the chunk keeps), else M | q (bits 16..21) of the
-//         slot's first later writer | n_l (bits 24..31) later writers
+//   write records W[8][64], 12 bytes each:
+//     w0  write slot if p owns it (the first writer of the slot the chunk keeps), else M (bits 0..10) | q (bits
+//         11..16) of the slot's first later writer | n_l (bits 17..22) later writers | the index of the later
+//         writers past the first among the write entries (bits 23..31; a chunk holds at most 510 such entries)
 //     w1  lam^(L-1-p) * ww if owned, else 0
 //     w2  the first later writer's lam^(L-1-q) * ww (0 if none)
-//     w3  entry index of the later writers past the first
-//   variable part: a 16-byte header {bytes, flags (bit 31: the chunk holds a reset), n_ro, n_wo}, then n_ro entries
-//   of read contributions past the eighth of each position (by position, in ascending q), then n_wo entries of later
-//   writers past the first of each owned slot (ascending q): {c, q}
+//   variable part: a 16-byte header {bytes, flags (bit 31: the chunk holds a reset), n_ro, n_wo}; a table of 64
+//   16-bit entry indices, position p's first contribution past the eighth; then n_ro entries of read contributions
+//   past the eighth of each position (by position, in ascending q) and n_wo entries of later writers past the first
+//   of each owned slot (ascending q): {c, q}.  The records hold no entry index of their own (12 bytes, not 16: the
+//   plans are written once and read once per call, so their size is core traffic).
 struct PickGeom {
-  __host__ __device__ static constexpr int off_w() { return kChunk * 8 * 16; }
-  __host__ __device__ static constexpr int off_var() { return 2 * kChunk * 8 * 16; }
+  static constexpr int kRec = 12;   // bytes of a record
+  __host__ __device__ static constexpr int off_w() { return kChunk * 8 * kRec; }
+  __host__ __device__ static constexpr int off_var() { return 2 * kChunk * 8 * kRec; }
+  // entries start after the header and the 16-bit table of the positions' first read entries
+  __host__ __device__ static constexpr int off_ent() { return 16 + 2 * kChunk; }
   // at most sum_p max(p - 8, 0) = 1,540 contributions and 511 later writers past the inline ones
   __host__ __device__ static constexpr int max_entries() { return 1540 + 511; }
-  __host__ __device__ static constexpr int stride() { return (off_var() + 16 + 8 * max_entries() + 255) / 256 * 256; }
+  __host__ __device__ static constexpr int stride() {
+    return (off_var() + off_ent() + 8 * max_entries() + 255) / 256 * 256;
+  }
 };
 
 // Bytes of a plan's variable part the scan stages in LDS (typical parts hold well under 1 KB; entries past the

@@ -141,11 +141,11 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   float mu = 1.f;
 
   // this lane's read and write records of chunk c
-  auto load_recs = [&](int c, uint4& rr, uint4& wr) {
+  auto load_recs = [&](int c, uint3& rr, uint3& wr) {
     const unsigned char* base = plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) +
-                                16 * (pick * kChunk + p);
-    rr = *reinterpret_cast<const uint4*>(base);
-    wr = *reinterpret_cast<const uint4*>(base + PickGeom::off_w());
+                                PickGeom::kRec * (pick * kChunk + p);
+    rr = *reinterpret_cast<const uint3*>(base);
+    wr = *reinterpret_cast<const uint3*>(base + PickGeom::off_w());
   };
   // chunk c's value rows and variable part, loaded into registers (two values of row p at columns 2 u, 2 u + 1;
   // dword tid of the variable part) and stored into LDS buffer c & 1 at the end of the previous chunk.  (Direct
@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   float rq[3][2] = {};
   float sq[3] = {0.f, 0.f, 0.f};
 
-  uint4 rr, wr;
+  uint3 rr, wr;
   load_recs(0, rr, wr);
   stage(0, load_v(0), load_var(0, a.sizes[static_cast<int64_t>(s) * a.n_chunks]));
   lds_barrier();
@@ -258,7 +258,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     // the next chunk's records, values and variable part are loaded into registers during this chunk (the last
     // chunk loads its own again)
     const int cn = min(c + 1, a.n_chunks - 1);
-    uint4 rr_n, wr_n;
+    uint3 rr_n, wr_n;
     load_recs(cn, rr_n, wr_n);
     const VPair v_n = load_v(cn);
     const uint32_t var_n = load_var(cn, s_sizes[cn]);
@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     const unsigned char* gvar =
         plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) + PickGeom::off_var();
     auto ent_at = [&](int e, auto st) {
-      const int o = 16 + 8 * min(max(e, 0), PickGeom::max_entries() - 1);
+      const int o = PickGeom::off_ent() + 8 * min(max(e, 0), PickGeom::max_entries() - 1);
       if constexpr (decltype(st)::value) return *reinterpret_cast<const uint2*>(varc + o);
       else return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
     };
@@ -301,9 +301,10 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
       dl += cc;
     }
     if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
+      const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
       auto over = [&](auto st) {
         for (int j = 8 + pick; j < n_in; j += 8) {
-          const uint2 e = ent_at(static_cast<int>(rr.w) + j - 8, st);
+          const uint2 e = ent_at(e0 + j - 8, st);
           const float ce = __uint_as_float(e.x);
           VPiece<float> vq[4];
 #pragma unroll
@@ -385,9 +386,9 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     // ---- write: the owner lanes add their faded values and those of the slot's later writers ----
     const float inv_mu = fast_rcp(mu_new);
-    const int wslot = static_cast<int>(wr.x & 0xffffu);
+    const int wslot = static_cast<int>(wr.x & 0x7ffu);
     if (wslot != M) {
-      const int n_l = static_cast<int>(wr.x >> 24);
+      const int n_l = static_cast<int>((wr.x >> 17) & 63u);
       float y[16];
       unsigned char* row = A_w + wslot * (CW * 4);
 #pragma unroll
@@ -409,14 +410,16 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         const float a1 = __uint_as_float(wr.z) * inv_mu;
         VPiece<float> vl[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) vl[t].load(s_vc + ((wr.x >> 16) & 63u) * CW + soff[t] / 4);
+        for (int t = 0; t < 4; ++t) vl[t].load(s_vc + ((wr.x >> 11) & 63u) * CW + soff[t] / 4);
 #pragma unroll
         for (int t = 0; t < 4; ++t) vl[t].fma4(a1, y + 4 * t);
         cw += a1;
         if (n_l > 1) {   // later writers past the first, from the variable part
+          // the write entries follow the header's n_ro read entries
+          const int w_e0 = static_cast<int>(reinterpret_cast<const uint32_t*>(varc)[2] + (wr.x >> 23));
           auto later = [&](auto st) {
             for (int e = 0; e < n_l - 1; ++e) {
-              const uint2 en = ent_at(static_cast<int>(wr.w) + e, st);
+              const uint2 en = ent_at(w_e0 + e, st);
               const float ae = __uint_as_float(en.x) * inv_mu;
               VPiece<float> ve[4];
 #pragma unroll

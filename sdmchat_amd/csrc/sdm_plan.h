@@ -105,9 +105,9 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
     for (int i = set * 64 + p; i < a.xgroups * kChunk; i += 128) x[i] = 0ull;
   }
   unsigned char* plan = a.plans + plan_id * PickGeom::stride();
-  uint2* ent = reinterpret_cast<uint2*>(plan + PickGeom::off_var() + 16);
+  uint2* ent = reinterpret_cast<uint2*>(plan + PickGeom::off_var() + PickGeom::off_ent());
   if (set == 0 && p == 0) {
-    const int bytes = 16 + 8 * (n_ro + n_wo);
+    const int bytes = PickGeom::off_ent() + 8 * (n_ro + n_wo);
     *reinterpret_cast<uint4*>(plan + PickGeom::off_var()) = make_uint4(
         static_cast<uint32_t>(bytes), rmask ? 0x80000000u : 0u, static_cast<uint32_t>(n_ro), static_cast<uint32_t>(n_wo));
     a.sizes[plan_id] = bytes;
@@ -115,6 +115,7 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
   const uint32_t mrow = static_cast<uint32_t>(M);
   if (set == 1) {
     const int e0 = inc_e - n_e;   // the position's first entry past its eighth contribution
+    reinterpret_cast<uint16_t*>(plan + PickGeom::off_var() + 16)[p] = static_cast<uint16_t>(e0);
     float cj[KP];
     uint32_t qj[KP];
 #pragma unroll
@@ -153,9 +154,9 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
     for (int i = 0; i < KP; ++i) {
       const uint32_t slot = (p < L && i < kk) ? static_cast<uint32_t>(ms[i]) : mrow;
       const float rw = (p < L && i < kk && seg0 < 0) ? ws[i] : 0.f;
-      *reinterpret_cast<uint4*>(plan + 16 * (i * kChunk + p)) =
-          make_uint4(slot | (qj[i] << 16) | (static_cast<uint32_t>(n_in) << 24), __float_as_uint(rw),
-                     __float_as_uint(cj[i]), static_cast<uint32_t>(e0));
+      *reinterpret_cast<uint3*>(plan + PickGeom::kRec * (i * kChunk + p)) =
+          make_uint3(slot | (qj[i] << 16) | (static_cast<uint32_t>(n_in) << 24), __float_as_uint(rw),
+                     __float_as_uint(cj[i]));
     }
   } else {
     int e = n_ro + inc_e - n_e;
@@ -163,17 +164,18 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
     for (int jj = 0; jj < KP; ++jj) {
       uint32_t w0 = mrow;
       float wc = 0.f, l0 = 0.f;
-      const int e_first = e;
       if ((own >> jj) & 1u) {
         const int m = ms[jj];
-        w0 = static_cast<uint32_t>(m) | (static_cast<uint32_t>(nl[jj]) << 24);
+        // the later writers past the first start at write entry e - n_ro (< 511)
+        w0 = static_cast<uint32_t>(m) | (static_cast<uint32_t>(nl[jj]) << 17) |
+             (static_cast<uint32_t>(e - n_ro) << 23);
         wc = pw[L - 1 - p] * ws[jj];
         if (nl[jj] > 0) {
           unsigned long long mm = (wmask[m] & keep) & ~(1ull << p);   // every writer of m after p
           int rank = rank_below(m, p) + 1;
           const int q1 = __builtin_ctzll(mm);
           mm &= mm - 1ull;
-          w0 |= static_cast<uint32_t>(q1) << 16;
+          w0 |= static_cast<uint32_t>(q1) << 11;
           l0 = pw[L - 1 - q1] * wtab[rank++];
           while (mm) {
             const int q = __builtin_ctzll(mm);
@@ -182,8 +184,8 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
           }
         }
       }
-      *reinterpret_cast<uint4*>(plan + PickGeom::off_w() + 16 * (jj * kChunk + p)) =
-          make_uint4(w0, __float_as_uint(wc), __float_as_uint(l0), static_cast<uint32_t>(e_first));
+      *reinterpret_cast<uint3*>(plan + PickGeom::off_w() + PickGeom::kRec * (jj * kChunk + p)) =
+          make_uint3(w0, __float_as_uint(wc), __float_as_uint(l0));
     }
   }
 }

@@ -18,7 +18,7 @@ from tests._gpu_util import assert_close, bf16_round, check_core, core_inputs, g
 
 pytestmark = pytest.mark.gpu
 
-PICK_PLAN_VAR = 2 * 64 * 8 * 16   # offset of a pick plan's variable part (after its read and write records)
+PICK_PLAN_VAR = 2 * 64 * 8 * 12   # offset of a pick plan's variable part (after its 12-byte read and write records)
 
 
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 130, 200])
