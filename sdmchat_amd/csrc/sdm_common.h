@@ -879,15 +879,17 @@ struct PlanGeom {
 //     w2  coefficient of the position's in-chunk read contribution number i (q its source position), 0 if i >= n_in
 //   write records W[8][64], 12 bytes each:
 //     w0  write slot if p owns it (the first writer of the slot the chunk keeps), else M (bits 0..10) | q (bits
-//         11..16) of the slot's first later writer | n_l (bits 17..22) later writers | the index of the later
-//         writers past the first among the write entries (bits 23..31; a chunk holds at most 510 such entries)
+//         11..16) of the slot's first later writer | n_l (bits 17..22) later writers | the entry index of the later
+//         writers past the first (bits 23..31; a chunk holds at most 510 such entries, and they come first)
 //     w1  lam^(L-1-p) * ww if owned, else 0
 //     w2  the first later writer's lam^(L-1-q) * ww (0 if none)
 //   variable part: a 16-byte header {bytes, flags (bit 31: the chunk holds a reset), n_ro, n_wo}; a table of 64
-//   16-bit entry indices, position p's first contribution past the eighth; then n_ro entries of read contributions
-//   past the eighth of each position (by position, in ascending q) and n_wo entries of later writers past the first
-//   of each owned slot (ascending q): {c, q}.  The records hold no entry index of their own (12 bytes, not 16: the
-//   plans are written once and read once per call, so their size is core traffic).
+//   16-bit entry indices, position p's first contribution past the eighth; then n_wo entries of later writers past
+//   the first of each owned slot (by record, ascending q) and n_ro entries of read contributions past the eighth of
+//   each position (by position, ascending q): {c, q}.  The write entries come first: an owner walks its slot's in
+//   sequence, so in a crowded chunk they should sit in the part the scan stages in LDS.  The records hold no entry
+//   index of their own (12 bytes, not 16: the plans are written once and read once per call, so their size is
+//   core traffic).
 struct PickGeom {
   static constexpr int kRec = 12;   // bytes of a record
   __host__ __device__ static constexpr int off_w() { return kChunk * 8 * kRec; }

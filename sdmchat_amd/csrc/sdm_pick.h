@@ -415,8 +415,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         for (int t = 0; t < 4; ++t) vl[t].fma4(a1, y + 4 * t);
         cw += a1;
         if (n_l > 1) {   // later writers past the first, from the variable part
-          // the write entries follow the header's n_ro read entries
-          const int w_e0 = static_cast<int>(reinterpret_cast<const uint32_t*>(varc)[2] + (wr.x >> 23));
+          const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
           auto later = [&](auto st) {
             for (int e = 0; e < n_l - 1; ++e) {
               const uint2 en = ent_at(w_e0 + e, st);

@@ -114,7 +114,7 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
   }
   const uint32_t mrow = static_cast<uint32_t>(M);
   if (set == 1) {
-    const int e0 = inc_e - n_e;   // the position's first entry past its eighth contribution
+    const int e0 = n_wo + inc_e - n_e;   // the position's first entry past its eighth contribution (after the writes')
     reinterpret_cast<uint16_t*>(plan + PickGeom::off_var() + 16)[p] = static_cast<uint16_t>(e0);
     float cj[KP];
     uint32_t qj[KP];
@@ -159,16 +159,15 @@ __device__ __forceinline__ void emit_pick_plan(const PlanArgs& a, int b, int h, 
                      __float_as_uint(cj[i]));
     }
   } else {
-    int e = n_ro + inc_e - n_e;
+    int e = inc_e - n_e;   // the write entries come first: the owners walk them in sequence, so they stay in LDS
 #pragma unroll
     for (int jj = 0; jj < KP; ++jj) {
       uint32_t w0 = mrow;
       float wc = 0.f, l0 = 0.f;
       if ((own >> jj) & 1u) {
         const int m = ms[jj];
-        // the later writers past the first start at write entry e - n_ro (< 511)
-        w0 = static_cast<uint32_t>(m) | (static_cast<uint32_t>(nl[jj]) << 17) |
-             (static_cast<uint32_t>(e - n_ro) << 23);
+        // the later writers past the first start at entry e (< 511)
+        w0 = static_cast<uint32_t>(m) | (static_cast<uint32_t>(nl[jj]) << 17) | (static_cast<uint32_t>(e) << 23);
         wc = pw[L - 1 - p] * ws[jj];
         if (nl[jj] > 0) {
           unsigned long long mm = (wmask[m] & keep) & ~(1ull << p);   // every writer of m after p

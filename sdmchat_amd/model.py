@@ -320,7 +320,10 @@ class ForwardGraph:
     def __init__(self, model, B, T):
         dev = model.emb.weight.device
         self.model = model
-        self.idx = torch.zeros(B, T, dtype=torch.long, device=dev)
+        # varied tokens for the warm-up forwards: a batch of one repeated token makes every position of a chunk pick
+        # the same locations, the mixer core's slowest input (it costs time, not correctness)
+        V = model.emb.weight.shape[0]
+        self.idx = torch.arange(B * T, device=dev).mul_(7919).remainder_(V).view(B, T)
         with torch.no_grad():
             for _ in range(2):
                 model(self.idx)
