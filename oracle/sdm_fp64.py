@@ -187,6 +187,37 @@ def scan_recurrence(siw, ww, sir, wr, V, lam, state=None, reset=None):
     return num, den, mem, cnt
 
 
+def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam):
+    """scan_recurrence (OM:276-300) from an empty memory without resets, the fade carried as one factor per head: with
+    mem_t = lam^t * P_t, a step reads lam^t * P at its read rows and adds (write) / lam^(t+1) to P at its write rows,
+    so it touches 2k rows instead of fading all M.  The same values up to float64 rounding (checked against
+    scan_recurrence in tests/test_oracle.py); it needs every lam^T above 1e-290 (no lam of 0).
+    Returns num (B, H, T, dh), den (B, H, T)."""
+    B, H, T, k = siw.shape
+    dh = V.shape[-1]
+    M = int(max(siw.max(initial=0), sir.max(initial=0))) + 1
+    lam = np.asarray(lam, np.float64)
+    if T and not (np.min(lam) > 0 and np.min(lam) ** T > 1e-290):
+        raise ValueError("scan_recurrence_rescaled: lam^T underflows; use scan_recurrence")
+    P = np.zeros((B, H, M, dh))
+    C = np.zeros((B, H, M))
+    bi = np.arange(B)[:, None, None]
+    hi = np.arange(H)[None, :, None]
+    num = np.zeros((B, H, T, dh))
+    den = np.zeros((B, H, T))
+    S = np.ones(H)   # lam^t
+    for t in range(T):
+        rows = sir[:, :, t]
+        num[:, :, t] = np.einsum("bhk,bhkd->bhd", wr[:, :, t], P[bi, hi, rows]) * S[None, :, None]
+        den[:, :, t] = np.einsum("bhk,bhk->bh", wr[:, :, t], C[bi, hi, rows]) * S[None, :]
+        S = S * lam
+        wrow = siw[:, :, t]
+        inv = (1.0 / S)[None, :, None]
+        np.add.at(P, (bi, hi, wrow), (ww[:, :, t] * inv)[..., None] * V[:, :, t, None, :])
+        np.add.at(C, (bi, hi, wrow), ww[:, :, t] * inv)
+    return num, den
+
+
 def scan_closed_form(siw, ww, sir, wr, V, lam):
     """The same read written as the double sum of the closed form (O(T^2 k^2), tiny inputs only):
     num_t = sum_{s<t} lam^(t-1-s) sum_{i,j} wr[t,i] ww[s,j] [sir[t,i] == siw[s,j]] V_s; den with V -> 1."""

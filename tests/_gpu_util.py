@@ -125,14 +125,21 @@ def min_margin(z, p, k):
     return float(O.topk_margin(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), k).min())
 
 
-def scan_from_picks(siw, ww, sir, wr, V, lam, H, read_mode="mean", out_norm=True, onorm_w=None, M=None):
-    """fp64 recurrence + finish from given picks/weights (B, H, T, kk) and values V (B, T, H*dh)."""
+def scan_from_picks(siw, ww, sir, wr, V, lam, H, read_mode="mean", out_norm=True, onorm_w=None, M=None,
+                    rescaled=False):
+    """fp64 recurrence + finish from given picks/weights (B, H, T, kk) and values V (B, T, H*dh).  rescaled: the
+    recurrence with the fade carried per head (oracle scan_recurrence_rescaled: the same values, a step touches only
+    its picked rows; no final state, returned as None)."""
     B, T, W = V.shape
     dh = W // H
     Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
-    state = (np.zeros((B, H, M, dh)), np.zeros((B, H, M)))
-    num, den, mem, cnt = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
-                                           wr.astype(np.float64), Vb, np.asarray(lam, np.float64), state)
+    args = (siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64), wr.astype(np.float64), Vb,
+            np.asarray(lam, np.float64))
+    if rescaled:
+        num, den = O.scan_recurrence_rescaled(*args)
+        mem = cnt = None
+    else:
+        num, den, mem, cnt = O.scan_recurrence(*args, (np.zeros((B, H, M, dh)), np.zeros((B, H, M))))
     r = O.finish(num, den, read_mode, 1e-3, out_norm, None if onorm_w is None else onorm_w.astype(np.float64), 1e-2)
     return r.transpose(0, 2, 1, 3).reshape(B, T, W), (mem, cnt)
 
@@ -195,11 +202,12 @@ def check_picks(z, p, k, si, w, gate=None):
 
 
 def check_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, tol=1e-5, read_mode="mean", out_norm=True,
-               fused=False, slabs=None):
+               fused=False, slabs=None, rescaled=False):
     """sdm_rt_forward against the fp64 oracle in two parts: (1) the addressing kernel's picks and weights against
     the oracle's (check_picks); (2) the read-out against the fp64 recurrence + finish driven by those same picks and
     weights.  When no pick differs, the read-out is also compared with the fully independent oracle.  ``slabs``
-    restricts (2) to a list of (b, h).  Returns the number of differing picks."""
+    restricts (2) to a list of (b, h); rescaled runs (2) on the oracle's per-head-fade recurrence (long sequences,
+    every slab) and skips the independent oracle.  Returns the number of differing picks."""
     out_dtype = out_dtype or dtype
     bf16_out = out_dtype == torch.bfloat16
     B, T, _ = V.shape
@@ -214,9 +222,9 @@ def check_core(kz, qz, V, g, p, k, dtype=torch.float32, out_dtype=None, tol=1e-5
     flips = check_picks(kz, p, k, siw, ww, g) + check_picks(qz, p, k, sir, wr)
     on = p["onorm_w"] if out_norm else None
     if slabs is None:
-        want, _ = scan_from_picks(siw, ww, sir, wr, V, p["decay"], H, read_mode, out_norm, on, M)
+        want, _ = scan_from_picks(siw, ww, sir, wr, V, p["decay"], H, read_mode, out_norm, on, M, rescaled)
         assert_close(r, want, tol, bf16_out, "read-out given the kernel's picks")
-        if flips == 0:
+        if flips == 0 and not rescaled:
             full, _ = oracle_core(kz, qz, V, g, p, k, read_mode, out_norm)
             assert_close(r, full, tol, bf16_out, "read-out against the independent oracle")
     else:

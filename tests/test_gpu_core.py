@@ -4,7 +4,7 @@ References: RunTimeSdm.prepare / _chunk / forward / finish (track4_onesdm_models
 forward_sequential (:276-300), whose token recurrence the oracle restates.
 
 Each case is checked in two parts (tests/_gpu_util.check_core): the picks and weights of the addressing kernel
-against the oracle's (picks identical wherever the fp64 top-k margin is >= 1e-6, weights within 2e-6), then the
+against the oracle's (picks identical wherever the fp64 score gap is >= 2.4e-7, weights within 2e-6), then the
 read-out against the fp64 recurrence driven by those picks -- plus the fully independent oracle when no pick
 differs.  Tolerances: float32 1e-5 (abs and rel); bfloat16 2e-3, plus half a bfloat16 ulp for outputs that are
 themselves rounded to bfloat16.
@@ -103,11 +103,11 @@ def test_zero_length_and_empty_batch():
 
 
 def test_bench_shape_bf16():
-    """B=8, T=2048, H=12, bf16: every pick against the oracle, and the read-out of three (batch row, head) slabs
-    against the fp64 recurrence."""
+    """B=8, T=2048, H=12, bf16: every pick against the oracle, and the read-out of all 96 (batch row, head) slabs
+    against the fp64 recurrence (its per-head-fade form) on the kernel's picks."""
     kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=51)
     kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
-    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, slabs=[(0, 0), (3, 7), (7, 11)])
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, rescaled=True)
     say("bench-shape picks that differ from the oracle (all at near-ties):", flips)
 
 

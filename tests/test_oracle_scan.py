@@ -36,6 +36,26 @@ def test_recurrence_equals_closed_form_double_sum(lams):
     assert np.all(num[:, :, 0] == 0) and np.all(den[:, :, 0] == 0)
 
 
+def test_rescaled_recurrence_equals_recurrence():
+    """The fade carried as one factor per head (scan_recurrence_rescaled, what the bench-shape GPU test runs over
+    all 96 slabs) gives scan_recurrence's values: random picks, repeated slots, fades from 0.5 to 1 over 300 steps
+    (lam^T down to 1e-90), and an underflowing fade is refused."""
+    rng = np.random.Generator(np.random.PCG64(31))
+    B, H, T, k, M, dh = 2, 4, 300, 4, 24, 6
+    siw = _distinct_ids(rng, (B, H, T), k, M)
+    sir = _distinct_ids(rng, (B, H, T), k, M)
+    ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
+    V = rng.standard_normal((B, H, T, dh))
+    lam = np.array([0.5, 0.9, 0.999, 1.0])
+    num, den, _, _ = O.scan_recurrence(siw, ww, sir, wr, V, lam,
+                                       state=(np.zeros((B, H, M, dh)), np.zeros((B, H, M))))
+    n2, d2 = O.scan_recurrence_rescaled(siw, ww, sir, wr, V, lam)
+    np.testing.assert_allclose(n2, num, rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(d2, den, rtol=1e-10, atol=1e-14)
+    with pytest.raises(ValueError):
+        O.scan_recurrence_rescaled(siw, ww, sir, wr, V, np.array([0.0, 0.9, 0.9, 0.9]))
+
+
 def test_recurrence_state_carry_is_the_same_as_one_pass():
     rng = np.random.Generator(np.random.PCG64(22))
     B, H, T, k, M, dh = 1, 2, 20, 2, 9, 4
