@@ -6,8 +6,9 @@ parameter and buffer names and shapes (so ``load_state_dict(strict=True)`` accep
 address bias drawn from ``torch.Generator().manual_seed(4321 + seed)``, :159-185) and the same
 ``forward(x, reset=None) -> Tensor[B, T, d]`` in ``x.dtype``.
 
-What runs where: the input RMSNorm and the four input projections (one fused GEMM) and the output map ``wo`` are
-dense torch ops (hipBLASLt); the SDM core between them -- product-key addressing, softmax weights, write gate, the
+What runs where: the input RMSNorm, the four input projections (two GEMMs: [wk; wq; wg] and wv; one of both for a
+decode step's few rows) and the output map ``wo`` are dense ops (hipBLASLt, or sdm_rt_gemm_rows for a few rows); the
+SDM core between them -- product-key addressing, softmax weights, write gate, the
 faded write / causal read of the memory and the mean read with its per-head norm -- is one call into
 ``libsdm_rt.so`` (sdm_rt_forward).  There is no CPU or pure-torch fallback: a missing library, a CPU tensor or an
 unsupported option raises.
@@ -103,23 +104,33 @@ class RunTimeSdm(nn.Module):
         return torch.sigmoid(self.decay_logit) if self.learn_decay else self.decays_fixed
 
     # -- fused input projection ----------------------------------------------------------------------------------
+    def _rows_a(self):
+        """Rows of the first projection map, [wk; wq; wg] padded to a multiple of 256 (a shape hipBLASLt runs well)."""
+        rows = 2 * self.h * self.d_a + (self.h if self.write_gate else 0)
+        return (rows + 255) // 256 * 256
+
     def _fused_weight(self, dtype):
-        """[wk; wq; wv; wg] stacked (rows padded to a multiple of 256, a shape hipBLASLt runs well), the matching
-        bias (zero except wg.bias on the gate rows; None without the write gate) and wo, all in ``dtype``, cached
-        until one of these tensors changes (data pointer or in-place version)."""
-        ws = (self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight)
+        """The projections in one buffer, [wk; wq; wg; zero rows up to _rows_a(); wv], the matching bias (zero
+        except wg.bias on the gate rows; None without the write gate) and wo, all in ``dtype``, cached until one of
+        these tensors changes (data pointer or in-place version).  The sequence forward maps the two row ranges
+        separately (two GEMMs of 1,792 and 768 columns at the layer shape run faster than one of 2,560 with the
+        bias); a decode step maps the whole buffer at once."""
+        ws = (self.wk.weight, self.wq.weight, self.wg.weight, self.wv.weight)
         srcs = ws + (self.wg.bias, self.wo.weight)
         key = (dtype, ws[0].device, self.write_gate) + tuple((t.data_ptr(), t._version) for t in srcs)
         if self._fused is not None and self._fused[0] == key:
             return self._fused[1:]
-        rows = sum(w.shape[0] for w in ws)
-        padded = (rows + 255) // 256 * 256
-        W = torch.zeros(padded, self.d, dtype=dtype, device=ws[0].device)
-        W[:rows].copy_(torch.cat([w.detach() for w in ws], 0))
+        H, d_a, d = self.h, self.d_a, self.d
+        ra = self._rows_a()
+        o_g = 2 * H * d_a
+        W = torch.zeros(ra + d, self.d, dtype=dtype, device=ws[0].device)
+        W[:o_g].copy_(torch.cat([self.wk.weight.detach(), self.wq.weight.detach()], 0))
+        W[ra:].copy_(self.wv.weight.detach())
         bias = None
         if self.write_gate:   # the gate logit rounds once, as the reference's wg(hx) under autocast (OM:205)
-            bias = torch.zeros(padded, dtype=dtype, device=ws[0].device)
-            bias[rows - self.h:rows].copy_(self.wg.bias.detach())
+            W[o_g:o_g + H].copy_(self.wg.weight.detach())
+            bias = torch.zeros(ra + d, dtype=dtype, device=ws[0].device)
+            bias[o_g:o_g + H].copy_(self.wg.bias.detach())
         wo = self.wo.weight.detach().to(dtype)
         self._fused = (key, W, bias, wo)
         return W, bias, wo
@@ -149,40 +160,49 @@ class RunTimeSdm(nn.Module):
         raise ValueError(f"unsupported input dtype {x.dtype}")
 
     def _project(self, x, dt, hx=None):
-        """RMSNorm then one fused GEMM for wk, wq, wv, wg (prepare, track4_onesdm_models.py:197-206).  Returns views
-        kz, qz [B, T, H * d_a], V [B, T, d] and gate logits [B, T, H] (None without the write gate) of one buffer.
-        The gate bias is the GEMM's bias, so W_g hx + b rounds to dt once, as wg(hx) does; addr_b is added inside
-        the core.  hx: the normed input when the caller computed it (in dt, as the norm below gives it)."""
-        H, d_a, d = self.h, self.d_a, self.d
+        """RMSNorm then the projections wk, wq, wv, wg (prepare, track4_onesdm_models.py:197-206): one GEMM for
+        [wk; wq; wg] and one for wv (one GEMM of the whole buffer for a few rows).  Returns views kz, qz
+        [B, T, H * d_a] and gate logits [B, T, H] (None without the write gate) of the first map's output, and V
+        [B, T, d].  The gate bias is the GEMM's bias, so W_g hx + b rounds to dt once, as wg(hx) does; addr_b is
+        added inside the core.  hx: the normed input when the caller computed it (in dt, as the norm below gives
+        it)."""
+        H, d_a = self.h, self.d_a
         if hx is None:
             hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)   # the norm, then the cast to dt
         W, bias = self._fused_weight(dt)[:2]
-        proj = core.linear(hx, W, bias)                                # [B, T, padded rows]
-        o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
-        g = proj[..., o_g:o_g + H] if self.write_gate else None
-        return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
+        ra = self._rows_a()
+        if hx.numel() // hx.shape[-1] <= core.GEMM_ROWS_MAX:
+            proj = core.linear(hx, W, bias)                            # [B, T, ra + d]
+            pa, V = proj[..., :ra], proj[..., ra:]
+        else:
+            pa = core.linear(hx, W[:ra], None if bias is None else bias[:ra])
+            V = core.linear(hx, W[ra:])
+        o_q, o_g = H * d_a, 2 * H * d_a
+        g = pa[..., o_g:o_g + H] if self.write_gate else None
+        return pa[..., :o_q], pa[..., o_q:o_g], V, g
 
     def _training(self, x):
         return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
 
     def _project_train(self, x):
         """The differentiable prepare (:195-206) up to the projections: the input norm on the RMSNorm kernel
-        (core.RmsNormFunction, with its float32 backward) and the same padded fused GEMM with the gate bias as
-        inference, so both forwards compute the same values.  Under autocast the GEMM runs in its dtype, as in the
-        reference.  Returns kz, qz, V, g (None without the write gate)."""
-        H, d_a, d = self.h, self.d_a, self.d
+        (core.RmsNormFunction, with its float32 backward) and the same two maps as inference ([wk; wq; wg] padded,
+        with the gate bias, then wv), so both forwards compute the same values.  Under autocast the GEMMs run in its
+        dtype, as in the reference.  Returns kz, qz, V, g (None without the write gate)."""
+        H, d_a = self.h, self.d_a
         hx = core.RmsNormFunction.apply(grad_scale(x, self.mem_in_grad), self.norm.w, self.norm.eps,
                                         torch.promote_types(x.dtype, self.norm.w.dtype)).float()
-        W = torch.cat([self.wk.weight, self.wq.weight, self.wv.weight, self.wg.weight], 0)
-        rows = W.shape[0]
-        pad = (rows + 255) // 256 * 256 - rows
-        W = F.pad(W, (0, 0, 0, pad))
+        Wa = torch.cat([self.wk.weight, self.wq.weight] + ([self.wg.weight] if self.write_gate else []), 0)
+        rows = Wa.shape[0]
+        ra = self._rows_a()
+        Wa = F.pad(Wa, (0, 0, 0, ra - rows))
+        o_q, o_g = H * d_a, 2 * H * d_a
         # the gate bias inside the projection, so the logit rounds once, as wg(hx) does
-        bias = F.pad(self.wg.bias, (rows - H, pad)) if self.write_gate else None
-        proj = F.linear(hx, W, bias)
-        o_q, o_v, o_g = H * d_a, 2 * H * d_a, 2 * H * d_a + d
-        g = proj[..., o_g:o_g + H] if self.write_gate else None
-        return proj[..., :o_q], proj[..., o_q:o_v], proj[..., o_v:o_g], g
+        bias = F.pad(self.wg.bias, (o_g, ra - rows)) if self.write_gate else None
+        pa = F.linear(hx, Wa, bias)
+        V = F.linear(hx, self.wv.weight)
+        g = pa[..., o_g:o_g + H] if self.write_gate else None
+        return pa[..., :o_q], pa[..., o_q:o_g], V, g
 
     def _forward_train(self, x, reset):
         """The differentiable forward: _project_train, the core through SdmCoreFunction, finish's wo (:247)."""
