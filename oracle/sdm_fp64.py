@@ -190,15 +190,16 @@ def scan_recurrence(siw, ww, sir, wr, V, lam, state=None, reset=None):
 def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam):
     """scan_recurrence (OM:276-300) from an empty memory without resets, the fade carried as one factor per head: with
     mem_t = lam^t * P_t, a step reads lam^t * P at its read rows and adds (write) / lam^(t+1) to P at its write rows,
-    so it touches 2k rows instead of fading all M.  The same values up to float64 rounding (checked against
-    scan_recurrence in tests/test_oracle.py); it needs every lam^T above 1e-290 (no lam of 0).
+    so it touches 2k rows instead of fading all M; when a head's factor falls below 1e-100 it is folded into P (one
+    pass over that head's memory).  The same values up to float64 rounding (checked against scan_recurrence in
+    tests/test_oracle_scan.py); every lam must be above 0 (use scan_recurrence for a fade of 0).
     Returns num (B, H, T, dh), den (B, H, T)."""
     B, H, T, k = siw.shape
     dh = V.shape[-1]
     M = int(max(siw.max(initial=0), sir.max(initial=0))) + 1
     lam = np.asarray(lam, np.float64)
-    if T and not (np.min(lam) > 0 and np.min(lam) ** T > 1e-290):
-        raise ValueError("scan_recurrence_rescaled: lam^T underflows; use scan_recurrence")
+    if T and not np.min(lam) > 0:
+        raise ValueError("scan_recurrence_rescaled: a fade of 0; use scan_recurrence")
     P = np.zeros((B, H, M, dh))
     C = np.zeros((B, H, M))
     bi = np.arange(B)[:, None, None]
@@ -211,6 +212,11 @@ def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam):
         num[:, :, t] = np.einsum("bhk,bhkd->bhd", wr[:, :, t], P[bi, hi, rows]) * S[None, :, None]
         den[:, :, t] = np.einsum("bhk,bhk->bh", wr[:, :, t], C[bi, hi, rows]) * S[None, :]
         S = S * lam
+        low = S < 1e-100
+        if low.any():   # fold the small factor into the memory of those heads
+            P[:, low] *= S[low][None, :, None, None]
+            C[:, low] *= S[low][None, :, None]
+            S = np.where(low, 1.0, S)
         wrow = siw[:, :, t]
         inv = (1.0 / S)[None, :, None]
         np.add.at(P, (bi, hi, wrow), (ww[:, :, t] * inv)[..., None] * V[:, :, t, None, :])

@@ -132,6 +132,16 @@ def test_crowded_chunks_read_past_the_staged_plan():
     assert int(hdr[0]) == int(sizes[0]) and stride > PICK_PLAN_VAR
 
 
+def test_long_sequence_32k_positions_bf16():
+    """T = 32,768 positions in one call (512 chunks per slab: the scan's table of plan sizes near the end of its LDS),
+    one batch row, 12 heads, bf16: every pick against the oracle and the read-out of every slab against the fp64
+    recurrence on the kernel's picks (its per-head-fade form, the factor folded into the memory as it shrinks)."""
+    kz, qz, V, g, p = core_inputs(1, 32768, 12, 64, 64, 32, seed=161)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, rescaled=True)
+    say("T=32768 picks that differ from the oracle (all at near-ties):", flips)
+
+
 def test_bench_shape_slabs_bf16():
     """B=8, T=2048, H=12 in bfloat16 (the bench workload): picks against the oracle and the read-out of all 96
     slabs against the fp64 recurrence on the kernel's picks (the per-head-fade form of the recurrence)."""

@@ -38,10 +38,10 @@ def test_recurrence_equals_closed_form_double_sum(lams):
 
 def test_rescaled_recurrence_equals_recurrence():
     """The fade carried as one factor per head (scan_recurrence_rescaled, what the bench-shape GPU test runs over
-    all 96 slabs) gives scan_recurrence's values: random picks, repeated slots, fades from 0.5 to 1 over 300 steps
-    (lam^T down to 1e-90), and an underflowing fade is refused."""
+    all 96 slabs) gives scan_recurrence's values: random picks, repeated slots, fades from 0.5 to 1 over 900 steps
+    (0.5^900 = 1e-271: the factor is folded into the memory several times), and a fade of 0 is refused."""
     rng = np.random.Generator(np.random.PCG64(31))
-    B, H, T, k, M, dh = 2, 4, 300, 4, 24, 6
+    B, H, T, k, M, dh = 2, 4, 900, 4, 24, 6
     siw = _distinct_ids(rng, (B, H, T), k, M)
     sir = _distinct_ids(rng, (B, H, T), k, M)
     ww, wr = rng.random((B, H, T, k)), rng.random((B, H, T, k))
