@@ -19,7 +19,7 @@ module: the whole layer is MFMA-bound (79.6 GFLOP per call against 55.2 MB): mod
 FLOPs / 2.5 PFLOP/s) / module time.  copy_gbs: a 1 GiB device-to-device copy, for context.
 
 cpu_baseline: the float32 torch CPU restatement of the reference forward (oracle/sdm_torch32.py, the reference's
-dense chunk algorithm) on the same workload, all host cores, one warm call then best of three; also at config 1
+dense chunk algorithm) on the same workload, all host cores, one warm call then best of three; also at B=1, T=256
 (B=1, T=256), with the CPU model.  In the same leg the oracle checks the whole models: model.logit_agreement is the
 float32 GPU logits of both full-width models (B=1, T=64) against the fp64 oracle (oracle.sdm_fp64.model_forward).
 
@@ -31,14 +31,14 @@ rows.  us_per_step = replay time / 64 (device time, no host launch cost), report
 fade set to 0 (us_per_step_head0_fade0).  --no-decode skips it.
 
 model: the whole OneSdmLM forward (logits) at B=8, T=2048, vocabulary 32,768, 12 layers of d=768 with this mixer
-(12 heads, M=1,024, k=8): "swiglu" = each layer's per-token step a SwiGLU of hidden 2,048 (the survey's config 3),
-"trained_sdm" = a TrainedSdm of 4,096 slots, one head of width 768, k=16 (config 4); bf16 weights and activations,
+(12 heads, M=1,024, k=8): "swiglu" = each layer's per-token step a SwiGLU of hidden 2,048 (the PARTIAL model),
+"trained_sdm" = a TrainedSdm of 4,096 slots, one head of width 768, k=16 (the FULL model); bf16 weights and activations,
 synthetic seeded weights (the zero-start output maps and tables filled), median of 5 calls after 2 warm; graph_ms
 is the same forward replayed from a HIP graph captured at that shape (ForwardGraph), median of 5 replays.
 --no-model skips it.
 
 decode_model: the FULL model (the trained_sdm arm above) decoding 64 independent streams, one fresh random token
-per stream per step, through 32,832 positions (the survey's config 5), bf16 weights, float32 state carried in
+per stream per step, through 32,832 positions, bf16 weights, float32 state carried in
 place; steps run as HIP graphs of 64 (DecodeGraph), the tokens refilled between replays; us_per_step = replay time
 / 64, reported overall (median), as tokens/s (64 / us_per_step) and at positions 0, 1,024, 8,192 and 32,768.
 --no-decode-model skips it; --decode-model-steps N shortens it.
@@ -96,7 +96,7 @@ def _cpu_model():
 
 
 def cpu_baseline():
-    """The float32 CPU restatement of the reference forward at the bench shape (and at config 1, B1 T256), all host
+    """The float32 CPU restatement of the reference forward at the bench shape (and at B=1, T=256), all host
     cores, one warm call then best of three."""
     import torch
 
@@ -121,9 +121,9 @@ def cpu_baseline():
     best = best_of_3(torch.from_numpy(S.layer_input(B, T, D, seed=1)))
     best1 = best_of_3(torch.from_numpy(S.layer_input(1, 256, D, seed=1)))
     return {"value": round(B * T / best, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "cpu": _cpu_model(), "config1_tokens_per_s": round(256 / best1, 1),
+            "cpu": _cpu_model(), "b1_t256_tokens_per_s": round(256 / best1, 1),
             "sample": f"full workload B={B} T={T} in float32 (chunk 128), torch {torch.__version__} on the host CPU, "
-                      f"1 warm call then best of 3 ({best:.2f} s per call); config 1 (B=1, T=256) likewise "
+                      f"1 warm call then best of 3 ({best:.2f} s per call); B=1, T=256 likewise "
                       f"({best1 * 1e3:.1f} ms per call)"}
 
 

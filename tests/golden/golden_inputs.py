@@ -44,10 +44,10 @@ def layer_addresses(seed=21, N=2048, d=768, H=12, d_a=64, n_sub=32):
 # --- one RunTimeSdm layer ----------------------------------------------------------------------------------------
 def layer_case(name, seed):
     """(constructor kwargs, state dict of float32 arrays, x (B, T, d) float32) of a named layer case:
-    'config1' -- B=1, T=256, d=768, 12 heads, M=1,024, d_a 64, k 8, fades U(0.9, 0.999), chunk 128;
+    'b1_t256' -- B=1, T=256, d=768, 12 heads, M=1,024, d_a 64, k 8, fades U(0.9, 0.999), chunk 128;
     'edge'    -- B=2, T=40, d=32, 4 heads, n_sub 6, d_a 8, k 4, fades (0, 1, 0, 1), chunk 7."""
     r = _rng(seed)
-    if name == "config1":
+    if name == "b1_t256":
         B, T, d, H, n_sub, d_a, k, chunk = 1, 256, 768, 12, 32, 64, 8, 128
         decays = r.uniform(0.9, 0.999, size=H).astype(np.float32)
     elif name == "edge":

@@ -18,8 +18,8 @@ NAME.keys1 / NAME.keys2 (H, n_sub, d_a/2) float32, NAME.k (scalar), NAME.sv (N, 
 PCG64; only seeds and a checksum of each input are stored, the tests regenerate the inputs):
   addr.*     the reference's picks (si int16, sv float32) of the 24,576 layer-workload addresses
              (golden_inputs.layer_addresses: 2,048 tokens x 12 heads, bf16-rounded projections)
-  config1.*, edge.*   RunTimeSdm.forward in float32 on the CPU (no autocast): y, and the picks of prepare
-             (siw, sir int16 [B, H, T, kk]); config1 = B1 T256 d768 H12 M1024 k8, edge = d32 H4 n_sub 6 k4 chunk 7
+  b1_t256.*, edge.*   RunTimeSdm.forward in float32 on the CPU (no autocast): y, and the picks of prepare
+             (siw, sir int16 [B, H, T, kk]); b1_t256 = B1 T256 d768 H12 M1024 k8, edge = d32 H4 n_sub 6 k4 chunk 7
              with fades 0 and 1.  Seeds are searched (with the oracle, fp64) for inputs whose every addressing has
              a top-k margin above 2e-6, so the picks are the same in any correct float32 or float64 evaluation.
   model_mlp.*, model_sdm.*   the logits of a tiny OneSdmLM of each arm (golden_inputs.MODEL_KW, reset at BOS), with
@@ -134,8 +134,8 @@ def runtime_main():
     blob["addr.si"] = si.numpy().astype(np.int16)
     blob["addr.sv"] = sv.numpy().astype(np.float32)
     print("addr", z.shape, "->", tuple(si.shape), flush=True)
-    # 2. RunTimeSdm.forward at config 1 and the edge shape
-    for name, seed0 in (("config1", 100), ("edge", 200)):
+    # 2. RunTimeSdm.forward at B1 T256 (the layer's float32 validation workload) and the edge shape
+    for name, seed0 in (("b1_t256", 100), ("edge", 200)):
         for seed in range(seed0, seed0 + 60):
             kw, p, x = G.layer_case(name, seed)
             if _layer_margin(kw, p, x) > 2e-6:

@@ -5,7 +5,7 @@ tests/golden/make_golden.py from the reference's pk_address, RunTimeSdm and OneS
 - sdm_rt_address on the 24,576 addresses of the layer workload (bf16 values, as bf16 and as float32 input): picks in
   the reference's order; a pick may differ only where the two slots' fp64 scores are within 2.4e-7 (a float32-level
   tie), and the number of such addresses is printed (the tests of the oracle pin it against the same data).
-- RunTimeSdm.forward (float32) at config 1 and at the edge shape: y within 1e-5 of the output scale.
+- RunTimeSdm.forward (float32) at B=1, T=256 (the layer's float32 validation workload) and at the edge shape: y within 1e-5 of the output scale.
 - OneSdmLM (float32, tiny, both arms, reset at BOS): logits within 1e-5 of their scale.
 """
 import os
@@ -41,7 +41,7 @@ def test_gpu_picks_follow_reference_on_layer_addresses(dtype):
     np.testing.assert_allclose(sv, GOLD["addr.sv"], atol=2e-6, rtol=0)
 
 
-@pytest.mark.parametrize("name", ["config1", "edge"])
+@pytest.mark.parametrize("name", ["b1_t256", "edge"])
 def test_gpu_layer_equals_reference(name):
     kw, p, x = G.layer_case(name, int(GOLD[f"{name}.seed"]))
     assert G.digest(x) == GOLD[f"{name}.digest"]

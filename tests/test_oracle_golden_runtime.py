@@ -4,8 +4,9 @@ tests/golden/make_golden.py from the reference's pk_address, RunTimeSdm and OneS
 
 - pk_address on the 24,576 addresses of the layer workload: the oracle's picks equal the reference's, in order,
   except where the two candidates' fp64 scores are within 2.4e-7 (a float32-level tie; the count is printed).
-- RunTimeSdm.forward at config 1 (B1 T256 d768 H12 M1024 k8) and at the edge shape (d32 H4 n_sub 6 k4, chunk 7,
-  fades 0 and 1): the oracle's y within 2e-5 of the output scale, its picks equal to the reference's.
+- RunTimeSdm.forward at B1 T256 (the float32 validation workload, d768 H12 M1024 k8) and at the edge shape (d32 H4
+  n_sub 6 k4, chunk 7, fades 0 and 1): the oracle's y within 2e-5 of the output scale, its picks equal to the
+  reference's.
 - OneSdmLM logits of both arms (tiny, reset at BOS): the oracle's model_forward within 2e-5 of the logits' scale.
 """
 import os
@@ -40,7 +41,7 @@ def test_oracle_picks_equal_reference_on_layer_addresses():
     np.testing.assert_allclose(sv, GOLD["addr.sv"], atol=1e-6, rtol=0)
 
 
-@pytest.mark.parametrize("name", ["config1", "edge"])
+@pytest.mark.parametrize("name", ["b1_t256", "edge"])
 def test_oracle_layer_equals_reference(name):
     kw, p, x = G.layer_case(name, int(GOLD[f"{name}.seed"]))
     assert G.digest(x) == GOLD[f"{name}.digest"], "regenerated input differs from the recorded one"
