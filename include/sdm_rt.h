@@ -71,7 +71,7 @@ typedef struct {
   const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
 } sdm_rt_params;
 
-/* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (24 KB per
+/* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (33 KB per
  * 64 positions of one head at k <= 8) and, with out_norm, a float32 copy of the read-out. */
 size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
 
