@@ -132,6 +132,27 @@ def test_crowded_chunks_read_past_the_staged_plan():
     assert int(hdr[0]) == int(sizes[0]) and stride > PICK_PLAN_VAR
 
 
+def test_bench_shape_crowded_bf16():
+    """The bench shape with addresses that crowd (a large address bias: tokens pick nearly the same locations, many
+    contributions past the eight a record keeps and slots with many later writers; variable parts past the 4 KB the
+    scan stages, read from the plan), bf16: every pick against the oracle and every slab's read-out against the fp64
+    recurrence on the kernel's picks."""
+    from sdmchat_amd import core
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=171, addr_bias=4.0)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, rescaled=True)
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    ws = core.CoreWorkspace()
+    core.core_forward(*(torch.from_numpy(a).cuda().to(torch.bfloat16) for a in (kz, qz, V, g)), keys1=tp["keys1"],
+                      keys2=tp["keys2"], log_scale=tp["log_scale"], decay=tp["decay"], addr_b=tp["addr_b"],
+                      onorm_w=tp["onorm_w"], gate_bias=tp["gate_bias"], k=8, workspace=ws)
+    torch.cuda.synchronize()
+    sizes = ws.buf[:4 * 8 * 12 * 32].cpu().view(torch.int32)
+    say(f"crowded bench shape: {flips} picks at near-ties; variable parts mean {float(sizes.float().mean()):.0f} B, "
+        f"max {int(sizes.max())} B, {float((sizes > 4096).float().mean()) * 100:.0f}% past the staged 4 KB")
+    assert int(sizes.max()) > 4096
+
+
 def test_long_sequence_32k_positions_bf16():
     """T = 32,768 positions in one call (512 chunks per slab: the scan's table of plan sizes near the end of its LDS),
     one batch row, 12 heads, bf16: every pick against the oracle and the read-out of every slab against the fp64
