@@ -132,6 +132,14 @@ def test_crowded_chunks_read_past_the_staged_plan():
     assert int(hdr[0]) == int(sizes[0]) and stride > PICK_PLAN_VAR
 
 
+def test_bench_shape_fp32():
+    """The bench shape in float32 (the float32 validation build's arithmetic: float32 projections, values and
+    read-out): every pick against the oracle and every slab's read-out against the fp64 recurrence within 1e-5."""
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=181)
+    flips = check_core(kz, qz, V, g, p, 8, dtype=torch.float32, tol=1e-5, rescaled=True)
+    say("bench-shape float32 picks that differ from the oracle (all at near-ties):", flips)
+
+
 def test_bench_shape_crowded_bf16():
     """The bench shape with addresses that crowd (a large address bias: tokens pick nearly the same locations, many
     contributions past the eight a record keeps and slots with many later writers; variable parts past the 4 KB the
