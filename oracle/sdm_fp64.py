@@ -187,12 +187,13 @@ def scan_recurrence(siw, ww, sir, wr, V, lam, state=None, reset=None):
     return num, den, mem, cnt
 
 
-def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam):
+def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam, reset=None):
     """scan_recurrence (OM:276-300) from an empty memory without resets, the fade carried as one factor per head: with
     mem_t = lam^t * P_t, a step reads lam^t * P at its read rows and adds (write) / lam^(t+1) to P at its write rows,
     so it touches 2k rows instead of fading all M; when a head's factor falls below 1e-100 it is folded into P (one
     pass over that head's memory).  The same values up to float64 rounding (checked against scan_recurrence in
-    tests/test_oracle_scan.py); every lam must be above 0 (use scan_recurrence for a fade of 0).
+    tests/test_oracle_scan.py); every lam must be above 0 (use scan_recurrence for a fade of 0).  reset: optional
+    (B, T) bool, as in scan_recurrence (that batch row's memory emptied before position t reads, OM:287-289).
     Returns num (B, H, T, dh), den (B, H, T)."""
     B, H, T, k = siw.shape
     dh = V.shape[-1]
@@ -208,6 +209,10 @@ def scan_recurrence_rescaled(siw, ww, sir, wr, V, lam):
     den = np.zeros((B, H, T))
     S = np.ones(H)   # lam^t
     for t in range(T):
+        if reset is not None and np.any(reset[:, t]):
+            dead = np.asarray(reset[:, t], bool)
+            P[dead] = 0.0
+            C[dead] = 0.0
         rows = sir[:, :, t]
         num[:, :, t] = np.einsum("bhk,bhkd->bhd", wr[:, :, t], P[bi, hi, rows]) * S[None, :, None]
         den[:, :, t] = np.einsum("bhk,bhk->bh", wr[:, :, t], C[bi, hi, rows]) * S[None, :]

@@ -140,6 +140,35 @@ def test_bench_shape_fp32():
     say("bench-shape float32 picks that differ from the oracle (all at near-ties):", flips)
 
 
+def test_bench_shape_with_resets_bf16():
+    """Packed documents at the bench shape (forward(x, reset), OM:229-233): BOS resets every 100-700 positions, one
+    row without any, resets at a chunk's last and first positions and at the last position; bf16.  Every slab's
+    read-out against the fp64 recurrence with the resets on the kernel's picks."""
+    from oracle import sdm_fp64 as O
+    from tests._gpu_util import assert_close, gpu_address, gpu_core
+    B, T, H, dh = 8, 2048, 12, 64
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 64, 32, seed=191)
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    rng = np.random.Generator(np.random.PCG64(192))
+    reset = np.zeros((B, T), bool)
+    for b in range(B):
+        t = int(rng.integers(0, 50))
+        while t < T:
+            reset[b, t] = True
+            t += int(rng.integers(100, 700))
+    reset[3] = False
+    reset[5, [63, 64, 2047]] = True
+    say("bench shape with resets:", int(reset.sum()), "resets")
+    r = gpu_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, reset=reset)
+    siw, _, ww = gpu_address(kz, p, 8, dtype=torch.bfloat16, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8, dtype=torch.bfloat16)
+    Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    num, den = O.scan_recurrence_rescaled(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                          wr.astype(np.float64), Vb, p["decay"].astype(np.float64), reset=reset)
+    r64 = O.finish(num, den, "mean", 1e-3, True, p["onorm_w"].astype(np.float64), 1e-2)
+    assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 2e-3, True, msg="read-out with resets")
+
+
 def test_bench_shape_crowded_bf16():
     """The bench shape with addresses that crowd (a large address bias: tokens pick nearly the same locations, many
     contributions past the eight a record keeps and slots with many later writers; variable parts past the 4 KB the

@@ -39,7 +39,8 @@ def test_recurrence_equals_closed_form_double_sum(lams):
 def test_rescaled_recurrence_equals_recurrence():
     """The fade carried as one factor per head (scan_recurrence_rescaled, what the bench-shape GPU test runs over
     all 96 slabs) gives scan_recurrence's values: random picks, repeated slots, fades from 0.5 to 1 over 900 steps
-    (0.5^900 = 1e-271: the factor is folded into the memory several times), and a fade of 0 is refused."""
+    (0.5^900 = 1e-271: the factor is folded into the memory several times), with and without resets, and a fade of 0
+    is refused."""
     rng = np.random.Generator(np.random.PCG64(31))
     B, H, T, k, M, dh = 2, 4, 900, 4, 24, 6
     siw = _distinct_ids(rng, (B, H, T), k, M)
@@ -54,6 +55,14 @@ def test_rescaled_recurrence_equals_recurrence():
     np.testing.assert_allclose(d2, den, rtol=1e-10, atol=1e-14)
     with pytest.raises(ValueError):
         O.scan_recurrence_rescaled(siw, ww, sir, wr, V, np.array([0.0, 0.9, 0.9, 0.9]))
+    reset = np.zeros((B, T), bool)
+    reset[0, [0, 17, 18, 400]] = True
+    reset[1, [899]] = True
+    num, den, _, _ = O.scan_recurrence(siw, ww, sir, wr, V, lam, state=(np.zeros((B, H, M, dh)), np.zeros((B, H, M))),
+                                       reset=reset)
+    n3, d3 = O.scan_recurrence_rescaled(siw, ww, sir, wr, V, lam, reset=reset)
+    np.testing.assert_allclose(n3, num, rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(d3, den, rtol=1e-10, atol=1e-14)
 
 
 def test_recurrence_state_carry_is_the_same_as_one_pass():
