@@ -169,6 +169,21 @@ def test_bench_shape_with_resets_bf16():
     assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 2e-3, True, msg="read-out with resets")
 
 
+def test_bench_shape_state_carry_fp32():
+    """The bench shape in two calls of 1,024 positions, the second starting from the state the first left
+    (state_in / state_out over whole slabs of 1,024 locations), equals one call over 2,048 positions: the read-out
+    and the final state, float32."""
+    from tests._gpu_util import gpu_core
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=201)
+    r_all, (m_all, c_all) = gpu_core(kz, qz, V, g, p, 8, want_state=True)
+    cut = 1024
+    r1, st = gpu_core(kz[:, :cut], qz[:, :cut], V[:, :cut], g[:, :cut], p, 8, want_state=True)
+    r2, (m2, c2) = gpu_core(kz[:, cut:], qz[:, cut:], V[:, cut:], g[:, cut:], p, 8, state_in=st, want_state=True)
+    np.testing.assert_allclose(np.concatenate([r1, r2], 1), r_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(m2, m_all, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(c2, c_all, atol=1e-5, rtol=1e-5)
+
+
 def test_bench_shape_crowded_bf16():
     """The bench shape with addresses that crowd (a large address bias: tokens pick nearly the same locations, many
     contributions past the eight a record keeps and slots with many later writers; variable parts past the 4 KB the
