@@ -55,9 +55,14 @@ def _layer(d, n_sub, heads, d_a, k, seed):
     return m.cuda().eval(), x
 
 
-@pytest.mark.parametrize("d,n_sub,heads,d_a,k", [(768, 64, 1, 32, 16), (64, 8, 4, 16, 8), (96, 12, 3, 32, 12)])
-def test_trained_sdm_layer_matches_oracle(d, n_sub, heads, d_a, k):
+@pytest.mark.parametrize("d,n_sub,heads,d_a,k,BT", [(768, 64, 1, 32, 16, (2, 48)), (64, 8, 4, 16, 8, (2, 48)),
+                                                   (96, 12, 3, 32, 12, (2, 48)), (768, 64, 1, 32, 16, (8, 2048))])
+def test_trained_sdm_layer_matches_oracle(d, n_sub, heads, d_a, k, BT):
+    """The table layer against the oracle: picks (near-ties aside), weights, and the output on the kernel's own
+    picks; the FULL model's layer (4,096 slots, k=16) also at the bench's B=8, T=2048."""
     m, x = _layer(d, n_sub, heads, d_a, k, seed=82 + n_sub)
+    if BT != (2, 48):
+        x = np.random.Generator(np.random.PCG64(83)).standard_normal(BT + (d,)).astype(np.float32)
     say("TrainedSdm", d, n_sub, heads, d_a, k)
     with torch.no_grad():
         y = m(torch.from_numpy(x).cuda()).cpu().numpy()
