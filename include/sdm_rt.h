@@ -19,8 +19,15 @@
  *   - Every call is asynchronous on the given stream (a hipStream_t passed as void*; NULL is the null stream)
  *     and returns 0 on success or a negative status; sdm_rt_last_error() then describes the failure (a
  *     thread-local string).  Arguments are validated before anything is launched.
- *   - Calls hold no global mutable state; concurrent calls on different streams with different workspaces are
- *     safe.
+ *   - Calls keep their state in the caller's buffers and workspace, with two exceptions: the scratch array of
+ *     sdm_rt_forward_noalloc (one per device, shared by every call of that entry point) and the wait limit of
+ *     sdm_rt_set_wait_limit (one per process).
+ *   - Concurrency: the forward's scan runs the column groups of one (batch row, head) slab on different compute
+ *     units, and each waits (a bounded spin) for the others' partial sums of the out-norm.  Calls on different
+ *     streams with different workspaces compute the same results, provided the groups of a slab can be resident
+ *     together; when another kernel fills the GPU so that they cannot, a wait can give up.  A wait that gives up
+ *     leaves the read-outs of its chunk NaN and records a time-out that sdm_rt_status() reports
+ *     (SDM_RT_ETIMEOUT); it never hangs.
  */
 #ifndef SDM_RT_H
 #define SDM_RT_H
@@ -39,7 +46,8 @@ enum {
   SDM_RT_EINVAL = -1,     /* bad dimension, pointer, stride or alignment */
   SDM_RT_ENOSPACE = -2,   /* workspace too small */
   SDM_RT_EUNSUPPORTED = -3, /* a shape outside what the kernels are built for */
-  SDM_RT_ELAUNCH = -4     /* a HIP launch failed */
+  SDM_RT_ELAUNCH = -4,    /* a HIP launch failed */
+  SDM_RT_ETIMEOUT = -5    /* a forward's wait for the other column groups of a slab gave up (sdm_rt_status) */
 };
 
 /* Layer shape and options: the RunTimeSdm constructor arguments that reach the core
@@ -72,7 +80,9 @@ typedef struct {
 } sdm_rt_params;
 
 /* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (33 KB per
- * 64 positions of one head at k <= 8) and, with out_norm, a float32 copy of the read-out. */
+ * 64 positions of one head at k <= 8) and their sizes, the scan's progress counters and status word and, with
+ * out_norm and more than one column group per head, the out-norm's partial sums (512 bytes per 64 positions of a
+ * head and group). */
 size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
 
 /* Row pitch (entries per token and head) of the pick arrays sdm_rt_address writes: kk rounded up to 8. */
@@ -132,6 +142,17 @@ int sdm_rt_forward_noalloc(const sdm_rt_dims* dims, const sdm_rt_params* params,
                            void* r_out, int64_t out_row_stride, sdm_rt_dtype out_dtype,
                            const float* state_in_mem, const float* state_in_cnt,
                            float* state_out_mem, float* state_out_cnt, void* stream);
+
+/* Status of the last sdm_rt_forward (or, with workspace NULL, sdm_rt_forward_noalloc on the current device) that
+ * used this workspace with these dims: synchronises the stream, then returns SDM_RT_OK, or SDM_RT_ETIMEOUT when one
+ * of the scan's bounded waits gave up (the read-outs of that chunk are then NaN).  No reference counterpart: the
+ * reference's forward runs on one stream of dense tensor ops and has no such wait. */
+int sdm_rt_status(const sdm_rt_dims* dims, const void* workspace, void* stream);
+
+/* Polls a forward's wait makes before it gives up, for the whole process: polls < 0 restores the default (2^20,
+ * about a second), 0 makes every wait give up at once without looking at the partner's sum (for tests of the
+ * error path: every kernel still runs to its end).  No reference counterpart. */
+void sdm_rt_set_wait_limit(int64_t polls);
 
 /* Bytes of workspace sdm_rt_decode_step needs (the picks of one token per stream; 0 on invalid dims). */
 size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);

@@ -145,7 +145,7 @@ class CoreWorkspace:
 def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr_b=None, onorm_w=None,
                  gate_bias=None, k, read_mode="mean", out_norm=True, read_eps=1e-3, out_norm_eps=1e-2,
                  out_dtype=None, out=None, state_in=None, want_state=False, workspace=None, params=None, reset=None,
-                 no_alloc=False):
+                 no_alloc=False, check=False):
     """The SDM core between the projections and the output map (RunTimeSdm.forward minus wk/wq/wv/wg and wo).
 
     kz, qz [B, T, H * d_a]; v [B, T, H * dh]; gate_logits [B, T, H] or None (no write gate); all share one dtype,
@@ -153,7 +153,8 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
     (mem [B, H, M, dh], cnt [B, H, M]) float32 state.  ``params`` may carry a prepared (SdmRtParams, held) pair.
     reset [B, T] bool or None: where set, the memory is emptied before that position reads (forward(x, reset),
     track4_onesdm_models.py:229-233).  no_alloc: run on the library's fixed scratch (sdm_rt_forward_noalloc) instead
-    of a workspace."""
+    of a workspace.  check: synchronise the stream afterwards and raise SdmRtError if one of the scan's bounded
+    waits gave up (sdm_rt_status: the read-outs of that chunk are NaN)."""
     lib = _lib.load()
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape
@@ -206,9 +207,19 @@ def core_forward(kz, qz, v, gate_logits, *, keys1, keys2, log_scale, decay, addr
                                 _ptr(mem_in), _ptr(cnt_in), _ptr(mem_out), _ptr(cnt_out), _ptr(ws), ws.numel(),
                                 ctypes.c_void_p(stream))
     _lib.check(rc, lib)
+    if check:
+        rc = lib.sdm_rt_status(ctypes.byref(dims), None if no_alloc else _ptr(ws), ctypes.c_void_p(stream))
+        _lib.check(rc, lib)
     if want_state:
         return out, (mem_out, cnt_out)
     return out
+
+
+def set_wait_limit(polls):
+    """Polls a forward's wait for the other column groups of a slab makes before it gives up, process-wide
+    (sdm_rt_set_wait_limit): None or a negative value restores the default, 0 makes every wait give up at once (for
+    tests of the error path)."""
+    _lib.load().sdm_rt_set_wait_limit(-1 if polls is None else int(polls))
 
 
 def table_read(slots, weights, values, k, out_dtype=torch.float32, out=None):

@@ -1128,4 +1128,7 @@ struct CoreIO {
 int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, const CoreIO& io, void* workspace,
              hipStream_t st);
 
+// the current device's copy of sdm_rt_forward_noalloc's scratch array (sdm_noalloc.hip)
+int scratch_ptr(void** out);
+
 }  // namespace sdmrt

@@ -1,11 +1,20 @@
 // sdm_forward.hip -- the forward of the SDM core (sdm_rt_forward): plan_kernel, then the scan with the read-out
 // finished in place (pick_scan_kernel where its shape fits, else scan_kernel).  Replaces RunTimeSdm.forward between
 // the projections and wo (experiments/track4/sdmllm/track4_onesdm_models.py:195-274, finish :243-246 without wo).
+#include <atomic>
 #include <cstdlib>
 
 #include "sdm_pick.h"
 
 namespace sdmrt {
+
+static std::atomic<uint32_t> g_wait_limit{kSpinLimit};
+uint32_t wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+
+// the status word a forward's scan leaves in its workspace (after the progress counters)
+static size_t status_offset(const Plan& p) {
+  return p.off_sync + sizeof(uint32_t) * static_cast<size_t>(p.B) * p.H * p.groups;
+}
 
 // SDM_RT_SCAN=chunk in the environment keeps every shape on scan_kernel (read once per process)
 static bool pick_enabled() {
@@ -80,8 +89,9 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   // direct copies of the value rows into LDS move 16-byte pieces: rows and the column groups in them aligned to 16
   s.v_direct = reinterpret_cast<uintptr_t>(io.v) % 16 == 0 && (static_cast<size_t>(io.v_stride) * vb) % 16 == 0 &&
                (static_cast<size_t>(p.dh) * vb) % 16 == 0 && (cw * vb) % 16 == 0;
-  if (pick)   // the pick scan loads two values at a time
-    s.v_direct = reinterpret_cast<uintptr_t>(io.v) % (2 * vb) == 0 && io.v_stride % 2 == 0;
+  if (pick)   // the pick scan loads four values at a time
+    s.v_direct = reinterpret_cast<uintptr_t>(io.v) % (4 * vb) == 0 && io.v_stride % 4 == 0;
+  s.spin_limit = wait_limit();
   s.read_mean = dims->read_mean;
   s.read_eps = dims->read_eps;
   s.out_eps = dims->out_norm_eps;
@@ -101,6 +111,31 @@ size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims) {
   Plan p;
   if (make_plan(dims, &p) != SDM_RT_OK) return 0;
   return p.total;
+}
+
+void sdm_rt_set_wait_limit(int64_t polls) {
+  g_wait_limit.store(polls < 0 ? kSpinLimit : static_cast<uint32_t>(std::min<int64_t>(polls, 0xffffffffll)),
+                     std::memory_order_relaxed);
+}
+
+int sdm_rt_status(const sdm_rt_dims* dims, const void* workspace, void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (hipStreamSynchronize(st) != hipSuccess) return set_err(SDM_RT_ELAUNCH, "stream synchronisation failed");
+  if (p.B == 0 || p.T == 0) return SDM_RT_OK;
+  const unsigned char* ws = static_cast<const unsigned char*>(workspace);
+  if (!ws && (rc = scratch_ptr(reinterpret_cast<void**>(const_cast<unsigned char**>(&ws))))) return rc;
+  uint32_t word = 0;
+  if (hipMemcpy(&word, ws + status_offset(p), sizeof(word), hipMemcpyDeviceToHost) != hipSuccess)
+    return set_err(SDM_RT_ELAUNCH, "reading the status word failed");
+  if (word)
+    return set_err(SDM_RT_ETIMEOUT,
+                   "the scan's wait for the other column groups of a slab gave up: the read-outs of that chunk are "
+                   "NaN (were the slab's workgroups not all resident, e.g. beside another call filling the GPU?)");
+  return SDM_RT_OK;
 }
 
 int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims) {

@@ -3,29 +3,30 @@
 // forward and finish, experiments/track4/sdmllm/track4_onesdm_models.py:215-247 without wo).  It serves picks of at
 // most 8, head_dim a multiple of 32 and slabs of at most 1,024 locations; scan_kernel (sdm_scan.h) serves the rest.
 //
-// Layout of the work: 1,024 threads, one per (position p, pick i, column half hh): lane u = tid % 16 of position
-// p = tid / 16 holds b = u % 4, hh = (u / 4) % 2 and pick i = 2 b + u / 8.  A lane gathers the 16 columns of its
-// half of its pick's slab row (four 16-byte LDS reads), scales them by the read weight, adds the in-chunk
-// contribution the plan gave its record, and the eight pick lanes of the half then reduce-scatter the 16 sums
-// (DPP: reverse within the quad, swap neighbours in the quad, lanes 8 apart), after which the lane holds columns
-// 4 b + 2 (u / 8) and + 1 of its half.  The lane reads its four pieces (4 columns each) in the order b, b ^ 1,
-// 3 - b, (3 - b) ^ 1 of its half, which the reduction consumes without any register selects above the last stage,
-// and eight consecutive lanes then read eight different 16-byte pieces (all 32 banks) at every read.
-// The write of a chunk is done by the owner lanes: the lane of pick j owns the slot if its position is the first
-// writer of the slot the chunk keeps; it adds its faded value and those of the slot's later writers in the chunk to
-// the slot's row (read, add, write back: each slot has one owner, so the sums run in a fixed order and the result
-// is deterministic).
-// Records, the chunk's value rows and the variable part of its plan (contributions and later writers beyond the
-// first) are loaded into registers one chunk ahead; rows and variable part are stored into LDS at the end of the
-// previous chunk.  Decay bookkeeping, the out-norm exchange between the column groups of a slab and the
-// reset handling are those of scan_kernel (sdm_scan.h).
+// Layout of the work: 512 threads, one lane per (position p, pick j) of the chunk, tid = 8 p + j, each over all 32
+// columns of the group (eight 4-column pieces).
+//   read   lane j gathers the row of its read pick (eight 16-byte LDS reads) in the order j, j^1, j^2, j^3, j^7,
+//          j^6, j^5, j^4, scales it by the read weight and adds the in-chunk contribution number j the plan gave
+//          its record; the position's eight lanes then reduce-scatter the sums by DPP without register selects
+//          (lanes j and 7 - j exchange four pieces (row_half_mirror), then j and j^2, then j and j^1), after which
+//          lane j holds piece j (columns 4 j ... 4 j + 3) summed over the picks.  At every read the eight lanes of a
+//          position touch eight different pieces, i.e. all 32 banks.
+//   write  the lane of write pick j owns the slot if its position is the first writer of the slot the chunk keeps;
+//          it loads the slot's row and count during the read phase (no other lane writes that slot in the chunk),
+//          and after the barrier adds its faded value (value row p, assembled from the pieces the position's eight
+//          lanes staged, by DPP) and those of the slot's later writers in the chunk, and stores the row back: each
+//          slot has one owner, so the sums run in a fixed order and the result is deterministic.
+// Records, the chunk's value pieces and the variable part of its plan (contributions and later writers beyond the
+// first) are loaded into registers one chunk ahead; values and variable part are stored into LDS at the end of the
+// previous chunk.  Decay bookkeeping, the out-norm exchange between the column groups of a slab and the reset
+// handling are those of scan_kernel (sdm_scan.h); a wait of the exchange that gives up records a time-out in the
+// status word and leaves the chunk's read-outs NaN.
 #pragma once
 
 #include "sdm_scan.h"
 
 namespace sdmrt {
 
-constexpr int kPickThreads = 1024;   // 64 positions x 8 picks x 2 column halves
 constexpr int kPickCols = 32;        // value columns per workgroup
 
 // LDS of one pick scan workgroup: the slab A[M + 1][32] and counts cnt[M + 1], by chunk parity two buffers of the
@@ -46,20 +47,6 @@ template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
-// sum over the eight pick lanes of a column half (u % 4 and u / 8); every lane gets the same value
-__device__ __forceinline__ float pick_sum(float v) {
-  v += dppf<0xb1>(v);    // quad_perm [1,0,3,2]
-  v += dppf<0x4e>(v);    // quad_perm [2,3,0,1]
-  v += dppf<0x128>(v);   // row_ror:8 (lane u ^ 8)
-  return v;
-}
-// sum over all 16 lanes of a position
-__device__ __forceinline__ float pos_sum(float v) {
-  v = pick_sum(v);
-  v += dppf<0x124>(v);   // row_ror:4 (the other half: lane u - 4 mod 16)
-  return v;
-}
-
 // four consecutive float32 values of a value row in LDS
 template <typename VT>
 struct VPiece;
@@ -75,10 +62,13 @@ struct VPiece<float> {
   }
 };
 
+constexpr int kPickThreads = 512;    // 64 positions x 8 picks
+
 template <typename VT, typename OutT>
 __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   constexpr int CW = kPickCols;
   constexpr int VS = kVarStage;
+  constexpr int NT = kPickThreads;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int M = a.M;
   const int G = a.groups;
@@ -98,19 +88,14 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   int32_t* s_sizes = reinterpret_cast<int32_t*>(pw + 68);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int p = tid >> 4;
-  const int u = tid & 15;
-  const int bq = u & 3;               // this lane's final piece in its half
-  const int hh = (u >> 2) & 1;        // column half
-  const int io = u >> 3;              // which two columns of the piece
-  const int pick = 2 * bq + io;       // the pick (record) this lane reads
+  const int p = tid >> 3;
+  const int j = tid & 7;   // the lane's pick, and its final piece
   const int col0 = g * CW;
-  const int hcol = hh * 16;
-  // the lane's pieces, in the order the reduction consumes them
-  const int ord[4] = {bq, bq ^ 1, 3 - bq, (3 - bq) ^ 1};
-  const int fcol = hcol + 4 * bq + 2 * io;   // the lane's two final columns (in the group)
+  const int fcol = 4 * j;  // the lane's four read-out columns (in the group)
+  int soff[8];             // byte offsets of the lane's pieces in a 32-column row, in read order
+#pragma unroll
+  for (int k = 0; k < 8; ++k) soff[k] = 16 * (j ^ (k < 4 ? k : 11 - k));
   const float lam = a.decay[h];
   const bool norm = a.onorm_w != nullptr;
   const bool xnorm = norm && G > 1;
@@ -118,14 +103,14 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   const VT* v_b = static_cast<const VT*>(a.v) + static_cast<int64_t>(b_row) * a.T * a.v_stride +
                   static_cast<int64_t>(h) * a.dh + col0;
 
-  for (int i = tid; i < (M + 1) * CW; i += kPickThreads) {
+  for (int i = tid; i < (M + 1) * CW; i += NT) {
     const int m = i / CW;
     const int cc = i - m * CW;
     A[i] = (a.state_in_mem && m < M) ? a.state_in_mem[(static_cast<int64_t>(s) * M + m) * a.dh + col0 + cc] : 0.f;
   }
-  for (int m = tid; m <= M; m += kPickThreads)
+  for (int m = tid; m <= M; m += NT)
     cnt[m] = (a.state_in_cnt && m < M) ? a.state_in_cnt[static_cast<int64_t>(s) * M + m] : 0.f;
-  for (int i = tid; i < a.n_chunks; i += kPickThreads) s_sizes[i] = a.sizes[static_cast<int64_t>(s) * a.n_chunks + i];
+  for (int i = tid; i < a.n_chunks; i += NT) s_sizes[i] = a.sizes[static_cast<int64_t>(s) * a.n_chunks + i];
   if (tid <= kChunk) {
     float v = 1.f, sq = lam;   // lam^tid by squaring (as the plan computes it; exact for lam = 0 and lam = 1)
 #pragma unroll
@@ -135,93 +120,99 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     pw[tid] = v;
   }
-  float onw[2];
+  float onw[4];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) onw[k] = norm ? a.onorm_w[h * a.dh + col0 + fcol + k] : 1.f;
+  for (int k = 0; k < 4; ++k) onw[k] = norm ? a.onorm_w[h * a.dh + col0 + fcol + k] : 1.f;
   float mu = 1.f;
 
   // this lane's read and write records of chunk c
   auto load_recs = [&](int c, uint3& rr, uint3& wr) {
     const unsigned char* base = plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) +
-                                PickGeom::kRec * (pick * kChunk + p);
+                                PickGeom::kRec * (j * kChunk + p);
     rr = *reinterpret_cast<const uint3*>(base);
     wr = *reinterpret_cast<const uint3*>(base + PickGeom::off_w());
   };
-  // chunk c's value rows and variable part, loaded into registers (two values of row p at columns 2 u, 2 u + 1;
-  // dword tid of the variable part) and stored into LDS buffer c & 1 at the end of the previous chunk.  (Direct
-  // global-to-LDS copies would make the compiler wait for every load in flight before the first LDS read after
-  // them, the record prefetch included.)
-  using VPair = typename std::conditional<sizeof(VT) == 2, uint32_t, uint2>::type;
+  // chunk c's value rows and variable part, loaded into registers (row p, columns 4 j ... 4 j + 3; bytes 8 tid ...
+  // 8 tid + 7 of the variable part) and stored into LDS buffer c & 1 at the end of the previous chunk
+  using VQuad = typename std::conditional<sizeof(VT) == 2, uint2, uint4>::type;
   auto load_v = [&](int c) {
     const int row = min(c * kChunk + p, a.T - 1);
-    const VT* src = v_b + static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_stride) + 2 * u;
-    if (a.v_direct) return *reinterpret_cast<const VPair*>(src);
-    VPair pr;
-    VT* d = reinterpret_cast<VT*>(&pr);
-    d[0] = src[0];
-    d[1] = src[1];
-    return pr;
+    const VT* src = v_b + static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_stride) + fcol;
+    if (a.v_direct) return *reinterpret_cast<const VQuad*>(src);
+    VQuad q;
+    VT* d = reinterpret_cast<VT*>(&q);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[k] = src[k];
+    return q;
   };
   auto load_var = [&](int c, int bytes) {
     const unsigned char* src = plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) +
-                               PickGeom::off_var() + 4 * tid;
-    return 4 * tid < min(bytes, VS) ? *reinterpret_cast<const uint32_t*>(src) : 0u;
+                               PickGeom::off_var() + 8 * tid;
+    return 8 * tid < min(bytes, VS) ? *reinterpret_cast<const uint2*>(src) : make_uint2(0u, 0u);
   };
-  auto stage = [&](int c, const VPair& vv, uint32_t vr) {   // the values as float32
-    float2 f;
-    if constexpr (sizeof(VT) == 2) f = make_float2(__uint_as_float(vv << 16), __uint_as_float(vv & 0xffff0000u));
-    else f = make_float2(__uint_as_float(vv.x), __uint_as_float(vv.y));
-    *reinterpret_cast<float2*>(s_v + (c & 1) * kChunk * CW + p * CW + 2 * u) = f;
-    reinterpret_cast<uint32_t*>(var + (c & 1) * VS)[tid] = vr;
+  auto stage = [&](int c, const VQuad& vv, const uint2& vr) {   // the values as float32
+    float4 f;
+    if constexpr (sizeof(VT) == 2) {
+      f = make_float4(__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u), __uint_as_float(vv.y << 16),
+                      __uint_as_float(vv.y & 0xffff0000u));
+    } else {
+      f = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+    }
+    *reinterpret_cast<float4*>(s_v + (c & 1) * kChunk * CW + p * CW + fcol) = f;
+    reinterpret_cast<uint2*>(var + (c & 1) * VS)[tid] = vr;
   };
-  // the lane's two read-out columns at position p of chunk 0; chunk c is c * 64 rows further (bfloat16 rounded to
-  // nearest even by the hardware conversion)
+  // the lane's four read-out columns at position p of chunk 0; chunk c is c * 64 rows further
   OutT* r_lane = static_cast<OutT*>(a.r_out) + (static_cast<int64_t>(b_row) * a.T + p) * a.r_stride +
                  static_cast<int64_t>(h) * a.dh + col0 + fcol;
-  const bool r_vec = reinterpret_cast<uintptr_t>(r_lane) % (2 * sizeof(OutT)) == 0 &&
-                     (static_cast<uint64_t>(a.r_stride) * sizeof(OutT)) % (2 * sizeof(OutT)) == 0;
-  auto store_r = [&](int c, const float (&x)[2]) {
+  const bool r_vec = reinterpret_cast<uintptr_t>(r_lane) % (4 * sizeof(OutT)) == 0 &&
+                     (static_cast<uint64_t>(a.r_stride) * sizeof(OutT)) % (4 * sizeof(OutT)) == 0;
+  auto store_r = [&](int c, const float (&x)[4]) {
     OutT* dst = r_lane + static_cast<int64_t>(c) * kChunk * a.r_stride;
     if constexpr (sizeof(OutT) == 2) {
-      const uint32_t w = pack_bf16(x[0], x[1]);
+      const uint2 w = make_uint2(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]));
       if (r_vec) {
-        *reinterpret_cast<uint32_t*>(dst) = w;
+        *reinterpret_cast<uint2*>(dst) = w;
       } else {
-        reinterpret_cast<uint16_t*>(dst)[0] = static_cast<uint16_t>(w);
-        reinterpret_cast<uint16_t*>(dst)[1] = static_cast<uint16_t>(w >> 16);
+        uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+        d16[0] = static_cast<uint16_t>(w.x);
+        d16[1] = static_cast<uint16_t>(w.x >> 16);
+        d16[2] = static_cast<uint16_t>(w.y);
+        d16[3] = static_cast<uint16_t>(w.y >> 16);
       }
     } else {
       if (r_vec) {
-        *reinterpret_cast<float2*>(dst) = make_float2(x[0], x[1]);
+        *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
       } else {
-        dst[0] = x[0];
-        dst[1] = x[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dst[k] = x[k];
       }
     }
   };
   // The out-norm exchange between the G groups of a slab: every group stores its per-position partial sum of
   // squares of chunk c as one 64-bit word {sum, 1} (the plan kernel cleared the words), and finishes chunk c's
   // read-out two chunks later with the others' words, waiting (a bounded spin that rarely runs) until they are
-  // written.  With two groups the partner's word is loaded in the middle of the chunk and used at its end.
+  // written.  With two groups the partner's word is loaded in the middle of the chunk and used at its end.  A wait
+  // that gives up records a time-out in the status word and finishes the chunk with NaN read-outs.
   unsigned long long* xw = reinterpret_cast<unsigned long long*>(a.xch) + static_cast<int64_t>(s) * a.n_chunks * G * kChunk + p;
   auto xget = [&](int c, int gg) {
     return __hip_atomic_load(xw + (c * G + gg) * kChunk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   auto partner = [&](int c, int gg, unsigned long long v) {   // group gg's sum for chunk c, once written
+    if (a.spin_limit == 0) v = 0ull;   // waits give up at once (the error path's test)
     if (__ballot(!(v >> 32))) {
       for (uint32_t it = 0;; ++it) {
+        if (it >= a.spin_limit) {
+          if (lane == 0) store_sync(a.sync + static_cast<int64_t>(a.S) * a.sync_stride, 1u);
+          return __builtin_nanf("");
+        }
         __builtin_amdgcn_s_sleep(2);
         if (!(v >> 32)) v = xget(c, gg);
         if (!__ballot(!(v >> 32))) break;
-        if (it >= kSpinLimit) {
-          if (lane == 0) store_sync(a.sync + static_cast<int64_t>(a.S) * a.sync_stride, 1u);
-          break;
-        }
       }
     }
     return __uint_as_float(static_cast<uint32_t>(v));
   };
-  auto finish = [&](int c, const float (&x)[2], float ss, unsigned long long xo) {
+  auto finish = [&](int c, const float (&x)[4], float ss, unsigned long long xo) {
     float tot;
     if (G == 2) {
       const float o = partner(c, 1 - g, xo);
@@ -232,26 +223,32 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     if (p < min(kChunk, a.T - c * kChunk)) {
       const float inv = fast_rsqrt(tot * (1.f / static_cast<float>(a.dh)) + a.out_eps);
-      float o[2];
+      float o[4];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) o[k] = x[k] * inv * onw[k];
+      for (int k = 0; k < 4; ++k) o[k] = x[k] * inv * onw[k];
       store_r(c, o);
     }
   };
-  float rq[3][2] = {};
+  float rq[3][4] = {};
   float sq[3] = {0.f, 0.f, 0.f};
 
+  // the value piece this lane staged for the current chunk (piece j of row p), as float32
+  auto as_f4 = [&](const VQuad& vv) {
+    if constexpr (sizeof(VT) == 2)
+      return make_float4(__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u), __uint_as_float(vv.y << 16),
+                         __uint_as_float(vv.y & 0xffff0000u));
+    else
+      return make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+  };
   uint3 rr, wr;
   load_recs(0, rr, wr);
-  stage(0, load_v(0), load_var(0, a.sizes[static_cast<int64_t>(s) * a.n_chunks]));
+  VQuad v_cur = load_v(0);
+  stage(0, v_cur, load_var(0, a.sizes[static_cast<int64_t>(s) * a.n_chunks]));
   lds_barrier();
   const float lam_chunk = pw[kChunk];
   const float inv_dh = 1.f / static_cast<float>(a.dh);
   const unsigned char* A_b = reinterpret_cast<const unsigned char*>(A);
   unsigned char* A_w = reinterpret_cast<unsigned char*>(A);
-  int soff[4];   // byte offsets of the lane's pieces in a slab row
-#pragma unroll
-  for (int t = 0; t < 4; ++t) soff[t] = 4 * (hcol + 4 * ord[t]);
 
   for (int c = 0; c < a.n_chunks; ++c) {
     const bool fin2 = xnorm && c >= 2;
@@ -260,8 +257,8 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     const int cn = min(c + 1, a.n_chunks - 1);
     uint3 rr_n, wr_n;
     load_recs(cn, rr_n, wr_n);
-    const VPair v_n = load_v(cn);
-    const uint32_t var_n = load_var(cn, s_sizes[cn]);
+    const VQuad v_n = load_v(cn);
+    const uint2 var_n = load_var(cn, s_sizes[cn]);
     const int c0 = c * kChunk;
     const int L = min(kChunk, a.T - c0);
     const unsigned char* varc = var + (c & 1) * VS;
@@ -275,77 +272,110 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
       if constexpr (decltype(st)::value) return *reinterpret_cast<const uint2*>(varc + o);
       else return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
     };
+    // row v of the staged values, scaled by cf, added to acc (the lane's read order)
+    auto add_vrow = [&](float cf, int v, float (&acc)[32]) {
+      const float* vrow = s_vc + v * CW;
+      VPiece<float> vq[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vq[k].load(vrow + soff[k] / 4);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vq[k].fma4(cf, acc + 4 * k);
+    };
 
     // ---- read: the pick's row, scaled; the in-chunk contribution of this lane's record ----
     const int rslot = static_cast<int>(rr.x & 0xffffu);
     const int n_in = static_cast<int>(rr.x >> 24);
     const float sw = __uint_as_float(rr.y) * (mu * pw[p]);
-    float acc[16];
+    float acc[32];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float4 q4 = *reinterpret_cast<const float4*>(A_b + rslot * (CW * 4) + soff[t]);
-      acc[4 * t] = sw * q4.x;
-      acc[4 * t + 1] = sw * q4.y;
-      acc[4 * t + 2] = sw * q4.z;
-      acc[4 * t + 3] = sw * q4.w;
+    for (int k = 0; k < 8; ++k) {
+      const float4 q4 = *reinterpret_cast<const float4*>(A_b + rslot * (CW * 4) + soff[k]);
+      acc[4 * k] = sw * q4.x;
+      acc[4 * k + 1] = sw * q4.y;
+      acc[4 * k + 2] = sw * q4.z;
+      acc[4 * k + 3] = sw * q4.w;
     }
     float dl = sw * cnt[rslot];
-    if (pick < n_in) {   // contribution number `pick` of the position
+    if (j < n_in) {   // contribution number j of the position
       const float cc = __uint_as_float(rr.z);
-      const float* vrow = s_vc + ((rr.x >> 16) & 63u) * CW;
-      VPiece<float> vq[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) vq[t].load(vrow + soff[t] / 4);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) vq[t].fma4(cc, acc + 4 * t);
+      add_vrow(cc, static_cast<int>((rr.x >> 16) & 63u), acc);
       dl += cc;
     }
     if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
       const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
       auto over = [&](auto st) {
-        for (int j = 8 + pick; j < n_in; j += 8) {
-          const uint2 e = ent_at(e0 + j - 8, st);
+        for (int jj = 8 + j; jj < n_in; jj += 8) {
+          const uint2 e = ent_at(e0 + jj - 8, st);
           const float ce = __uint_as_float(e.x);
-          VPiece<float> vq[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) vq[t].load(s_vc + (e.y & 63u) * CW + soff[t] / 4);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) vq[t].fma4(ce, acc + 4 * t);
+          add_vrow(ce, static_cast<int>(e.y & 63u), acc);
           dl += ce;
         }
       };
       if (all_staged) over(std::true_type{});
       else over(std::false_type{});
     }
-    // reduce-scatter over the eight pick lanes of the half: 16 -> 8 -> 4 -> 2 columns
+    // the owned write slot's row and count, loaded now (no other lane writes the slot in this chunk; reads of it
+    // by other lanes do not change it), so the write phase after the barrier only adds and stores
+    const int wslot = static_cast<int>(wr.x & 0x7ffu);
+    float y[32];
+    float cw_old = 0.f;
+    if (wslot != M) {
+      const unsigned char* row = A_b + wslot * (CW * 4);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] += dppf<0x1b>(acc[8 + k]);   // quad_perm [3,2,1,0]: piece 3 - b
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] += dppf<0xb1>(acc[4 + k]);   // quad_perm [1,0,3,2]: piece b ^ 1
-    float r[2];
-    {
-      const float k0 = io ? acc[2] : acc[0], k1 = io ? acc[3] : acc[1];
-      const float s0 = io ? acc[0] : acc[2], s1 = io ? acc[1] : acc[3];
-      r[0] = k0 + dppf<0x128>(s0);   // row_ror:8: the lane of the other two columns
-      r[1] = k1 + dppf<0x128>(s1);
+      for (int k = 0; k < 8; ++k) {
+        const float4 q4 = *reinterpret_cast<const float4*>(row + soff[k]);
+        y[4 * k] = q4.x;
+        y[4 * k + 1] = q4.y;
+        y[4 * k + 2] = q4.z;
+        y[4 * k + 3] = q4.w;
+      }
+      cw_old = cnt[wslot];
     }
-    const float den = pick_sum(dl);
+    // the eight pieces of value row p in the lane's read order, from the pieces the position's eight lanes staged
+    // (lane x holds piece x): pieces j ^ 1, j ^ 2, j ^ 3 by quad permutes, j ^ 7 by the half-row mirror, and
+    // j ^ 6, j ^ 5, j ^ 4 by the mirror of the first three
+    float vp[32];
+    {
+      const float4 f = as_f4(v_cur);
+      const float x[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t1 = dppf<0xb1>(x[e]), t2 = dppf<0x4e>(x[e]), t3 = dppf<0x1b>(x[e]);
+        vp[e] = x[e];
+        vp[4 + e] = t1;
+        vp[8 + e] = t2;
+        vp[12 + e] = t3;
+        vp[16 + e] = dppf<0x141>(x[e]);
+        vp[20 + e] = dppf<0x141>(t1);
+        vp[24 + e] = dppf<0x141>(t2);
+        vp[28 + e] = dppf<0x141>(t3);
+      }
+    }
+    // reduce-scatter over the eight pick lanes of the position: 32 -> 16 -> 8 -> 4 columns
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] += dppf<0x141>(acc[16 + k]);   // row_half_mirror: lane 7 - j
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] += dppf<0x4e>(acc[8 + k]);      // quad_perm [2,3,0,1]: lane j ^ 2
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] += dppf<0xb1>(acc[4 + k]);      // quad_perm [1,0,3,2]: lane j ^ 1
+    float r[4] = {acc[0], acc[1], acc[2], acc[3]};
+    const float den = sum8(dl);
     if (a.read_mean) {
-      if (a.den_out && g == 0 && u == 0 && p < L) a.den_out[(static_cast<int64_t>(b_row) * a.T + c0 + p) * a.H + h] = den;
+      if (a.den_out && g == 0 && j == 0 && p < L) a.den_out[(static_cast<int64_t>(b_row) * a.T + c0 + p) * a.H + h] = den;
       const float inv = fast_rcp(den + a.read_eps);
-      r[0] *= inv;
-      r[1] *= inv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[k] *= inv;
     }
     if (a.read_out && p < L) {
       float* dst = a.read_out + (static_cast<int64_t>(b_row) * a.T + c0 + p) * static_cast<int64_t>(a.H) * a.dh +
                    static_cast<int64_t>(h) * a.dh + col0 + fcol;
-      store_vals<2, float>(dst, r);
+      store_vals<4, float>(dst, r);
     }
     if (norm) {
-      const float ss = pos_sum(fmaf(r[1], r[1], r[0] * r[0]));
+      const float ss = sum8(fmaf(r[3], r[3], fmaf(r[2], r[2], fmaf(r[1], r[1], r[0] * r[0]))));
       if (xnorm) {
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int k = 0; k < 4; ++k) {
           rq[2][k] = rq[1][k];
           rq[1][k] = rq[0][k];
           rq[0][k] = r[k];
@@ -353,14 +383,14 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         sq[2] = sq[1];
         sq[1] = sq[0];
         sq[0] = ss;
-        if (u == 0)
+        if (j == 0)
           __hip_atomic_store(xw + (c * G + g) * kChunk, (1ull << 32) | __float_as_uint(ss), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       } else if (p < L) {
         const float inv = fast_rsqrt(ss * inv_dh + a.out_eps);
-        float o[2];
+        float o[4];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) o[k] = r[k] * inv * onw[k];
+        for (int k = 0; k < 4; ++k) o[k] = r[k] * inv * onw[k];
         store_r(c, o);
       }
     } else if (p < L) {
@@ -372,47 +402,40 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
     const bool chunk_reset = reinterpret_cast<const uint32_t*>(varc)[1] & 0x80000000u;
     float mu_new = mu * (L == kChunk ? lam_chunk : pw[L]);
-    if (chunk_reset) {
+    if (chunk_reset) {   // the slab empties, the owners' loaded rows with it
       float4* a4 = reinterpret_cast<float4*>(A);
-      for (int i = tid; i < (M + 1) * CW / 4; i += kPickThreads) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int i = tid; i <= M; i += kPickThreads) cnt[i] = 0.f;
+      for (int i = tid; i < (M + 1) * CW / 4; i += NT) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = tid; i <= M; i += NT) cnt[i] = 0.f;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) y[k] = 0.f;
+      cw_old = 0.f;
       mu_new = 1.f;
       lds_barrier();
-    } else if (!(mu_new >= kMuFloor)) {
-      for (int i = tid; i < (M + 1) * CW; i += kPickThreads) A[i] *= mu_new;
-      for (int i = tid; i <= M; i += kPickThreads) cnt[i] *= mu_new;
+    } else if (!(mu_new >= kMuFloor)) {   // the slab is rescaled, the owners' loaded rows with it
+      float4* a4 = reinterpret_cast<float4*>(A);
+      for (int i = tid; i < (M + 1) * CW / 4; i += NT) {
+        const float4 t = a4[i];
+        a4[i] = make_float4(t.x * mu_new, t.y * mu_new, t.z * mu_new, t.w * mu_new);
+      }
+      for (int i = tid; i <= M; i += NT) cnt[i] *= mu_new;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) y[k] *= mu_new;
+      cw_old *= mu_new;
       mu_new = 1.f;
       lds_barrier();
     }
     // ---- write: the owner lanes add their faded values and those of the slot's later writers ----
     const float inv_mu = fast_rcp(mu_new);
-    const int wslot = static_cast<int>(wr.x & 0x7ffu);
     if (wslot != M) {
       const int n_l = static_cast<int>((wr.x >> 17) & 63u);
-      float y[16];
       unsigned char* row = A_w + wslot * (CW * 4);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float4 q4 = *reinterpret_cast<const float4*>(row + soff[t]);
-        y[4 * t] = q4.x;
-        y[4 * t + 1] = q4.y;
-        y[4 * t + 2] = q4.z;
-        y[4 * t + 3] = q4.w;
-      }
-      VPiece<float> vp[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) vp[t].load(s_vc + p * CW + soff[t] / 4);
       const float a0 = __uint_as_float(wr.y) * inv_mu;
-      float cw = cnt[wslot] + a0;
+      float cw = cw_old + a0;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) vp[t].fma4(a0, y + 4 * t);
+      for (int k = 0; k < 32; ++k) y[k] = fmaf(a0, vp[k], y[k]);
       if (n_l > 0) {
         const float a1 = __uint_as_float(wr.z) * inv_mu;
-        VPiece<float> vl[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) vl[t].load(s_vc + ((wr.x >> 11) & 63u) * CW + soff[t] / 4);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) vl[t].fma4(a1, y + 4 * t);
+        add_vrow(a1, static_cast<int>((wr.x >> 11) & 63u), y);
         cw += a1;
         if (n_l > 1) {   // later writers past the first, from the variable part
           const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
@@ -420,11 +443,7 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
             for (int e = 0; e < n_l - 1; ++e) {
               const uint2 en = ent_at(w_e0 + e, st);
               const float ae = __uint_as_float(en.x) * inv_mu;
-              VPiece<float> ve[4];
-#pragma unroll
-              for (int t = 0; t < 4; ++t) ve[t].load(s_vc + (en.y & 63u) * CW + soff[t] / 4);
-#pragma unroll
-              for (int t = 0; t < 4; ++t) ve[t].fma4(ae, y + 4 * t);
+              add_vrow(ae, static_cast<int>(en.y & 63u), y);
               cw += ae;
             }
           };
@@ -433,13 +452,14 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
         }
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        *reinterpret_cast<float4*>(row + soff[t]) = make_float4(y[4 * t], y[4 * t + 1], y[4 * t + 2], y[4 * t + 3]);
-      if (hh == 0) cnt[wslot] = cw;   // one of the two half lanes of the pick
+      for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+      cnt[wslot] = cw;
     }
     mu = mu_new;
     rr = rr_n;
     wr = wr_n;
+    v_cur = v_n;
     stage(c + 1, v_n, var_n);   // buffer (c + 1) & 1 held chunk c - 1, done before the last barrier
     if (fin2) finish(c - 2, rq[2], sq[2], xo);
     lds_barrier();
@@ -451,14 +471,14 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   }
 
   if (a.state_out_mem) {
-    for (int i = tid; i < M * CW; i += kPickThreads) {
+    for (int i = tid; i < M * CW; i += NT) {
       const int m = i / CW;
       const int cc = i - m * CW;
       a.state_out_mem[(static_cast<int64_t>(s) * M + m) * a.dh + col0 + cc] = mu * A[i];
     }
   }
   if (a.state_out_cnt && g == 0) {
-    for (int m = tid; m < M; m += kPickThreads) a.state_out_cnt[static_cast<int64_t>(s) * M + m] = mu * cnt[m];
+    for (int m = tid; m < M; m += NT) a.state_out_cnt[static_cast<int64_t>(s) * M + m] = mu * cnt[m];
   }
 }
 

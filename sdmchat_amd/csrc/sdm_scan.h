@@ -41,9 +41,13 @@ struct ScanArgs {
   int sync_stride;             // progress counters per slab in sync (at least groups)
   int v_direct;                // 1: value rows are 16-byte aligned and copied into LDS directly
   float read_eps, out_eps;
+  uint32_t spin_limit;         // polls of a partner's progress before a wait gives up (0: give up at once)
 };
 
-constexpr uint32_t kSpinLimit = 1u << 20;   // polls of a partner's progress before the wait gives up
+constexpr uint32_t kSpinLimit = 1u << 20;   // the default polls of a partner's progress before a wait gives up
+
+// the polls a wait makes before it gives up, process-wide (sdm_rt_set_wait_limit)
+uint32_t wait_limit();
 
 // CPL consecutive float values from LDS in one access
 template <int CPL>
@@ -263,22 +267,27 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
   auto poll = [&]() { return (lane < G && lane != g) ? load_sync(my_sync + lane) : 0xffffffffu; };
   auto wait_published = [&](uint32_t got, int c) {
     const uint32_t need = static_cast<uint32_t>(c) + 1u;
+    if (a.spin_limit == 0) got = 0u;   // waits give up at once (the error path's test)
+    bool ok = true;
     if (__ballot(got < need)) {   // the first check outside the spin loop, whose own waits are for everything
       for (uint32_t it = 0;; ++it) {
+        if (it >= a.spin_limit) {
+          if (lane == 0) store_sync(a.sync + static_cast<int64_t>(a.S) * a.sync_stride, 1u);
+          ok = false;
+          break;
+        }
         __builtin_amdgcn_s_sleep(2);
         got = poll();
         if (!__ballot(got < need)) break;
-        if (it >= kSpinLimit) {
-          if (lane == 0) store_sync(a.sync + static_cast<int64_t>(a.S) * a.sync_stride, 1u);
-          break;
-        }
       }
     }
     asm volatile("" ::: "memory");
+    return ok;
   };
   auto xch_at = [&](int c) { return a.xch + (static_cast<int64_t>(s) * a.n_chunks + c) * G * kChunk + p; };
   auto gather = [&](int c) { return G == 2 ? load_xch(xch_at(c) + (1 - g) * kChunk) : 0.f; };
-  auto finish = [&](int c, const float (&x)[CPL], float ss, float xo) {
+  // ok = false: the wait for the other groups gave up, and the chunk's read-outs are NaN
+  auto finish = [&](int c, const float (&x)[CPL], float ss, float xo, bool ok) {
     const int L = min(kChunk, a.T - c * kChunk);
     if (p < L) {
       float tot;
@@ -288,6 +297,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
         tot = 0.f;
         for (int gg = 0; gg < G; ++gg) tot += gg == g ? ss : load_xch(xch_at(c) + gg * kChunk);
       }
+      if (!ok) tot = __builtin_nanf("");
       const float inv = fast_rsqrt(tot * (1.f / static_cast<float>(a.dh)) + a.out_eps);
       float o[CPL];
 #pragma unroll
@@ -436,8 +446,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     const Seg<CPL> vown = lds_seg<CPL>(&s_vc[p * CW + cl]);
     lds_barrier();
     float xo = 0.f;
+    bool xok = true;
     if (fin2) {
-      wait_published(got, c - 2);
+      xok = wait_published(got, c - 2);
       xo = gather(c - 2);
     }
     // the next chunk's records, values and variable part stream into LDS while this chunk writes
@@ -529,15 +540,15 @@ __global__ void __launch_bounds__(kScanThreads) scan_kernel(ScanArgs a) {
     // they were issued a whole write phase ago
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
-    if (fin2) finish(c - 2, rq[2], sq[2], xo);
+    if (fin2) finish(c - 2, rq[2], sq[2], xo, xok);
     lds_barrier();
   }
   if (xnorm) {   // the last two chunks (or one)
     const int n = a.n_chunks;
     if (tid == 0) store_sync(my_sync + g, static_cast<uint32_t>(n));
-    wait_published(poll(), n - 1);
-    if (n >= 2) finish(n - 2, rq[1], sq[1], gather(n - 2));
-    finish(n - 1, rq[0], sq[0], gather(n - 1));
+    const bool ok = wait_published(poll(), n - 1);
+    if (n >= 2) finish(n - 2, rq[1], sq[1], gather(n - 2), ok);
+    finish(n - 1, rq[0], sq[0], gather(n - 1), ok);
   }
 
   if (a.state_out_mem) {

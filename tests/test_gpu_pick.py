@@ -222,3 +222,31 @@ def test_bench_shape_slabs_bf16():
     kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
     flips = check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, rescaled=True)
     say("bench-shape picks that differ from the oracle (all at near-ties):", flips)
+
+
+@pytest.mark.parametrize("k,what", [(8, "pick scan"), (16, "chunk scan")])
+def test_a_wait_that_gives_up_is_reported(k, what):
+    """The out-norm's wait for the other column group of a slab is bounded; when it gives up the chunk's read-outs
+    are NaN and sdm_rt_status reports SDM_RT_ETIMEOUT.  The test makes every wait give up at once from the host
+    (sdm_rt_set_wait_limit(0): the waits do not even look at the partner's sum), so every kernel still runs to its
+    end; then the default limit is restored and the same call is clean.  k = 8 runs the pick scan, k = 16 (pitch
+    16) the chunk scan; head_dim 64 gives two column groups in both."""
+    from sdmchat_amd import _lib, core
+    kz, qz, V, g, p = core_inputs(2, 200, 4, 64, 32, 16, seed=211)
+    tp = {n: torch.from_numpy(v).cuda() for n, v in p.items()}
+    args = [torch.from_numpy(a).cuda() for a in (kz, qz, V, g)]
+    kw = dict(keys1=tp["keys1"], keys2=tp["keys2"], log_scale=tp["log_scale"], decay=tp["decay"], addr_b=tp["addr_b"],
+              onorm_w=tp["onorm_w"], gate_bias=tp["gate_bias"], k=k, check=True)
+    core.set_wait_limit(0)
+    try:
+        out = torch.zeros(2, 200, 4 * 64, device="cuda")
+        with pytest.raises(_lib.SdmRtError, match="gave up"):
+            core.core_forward(*args, out=out, **kw)
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(out).all()), f"{what}: a given-up wait must leave NaN read-outs"
+    finally:
+        core.set_wait_limit(None)
+    r = core.core_forward(*args, **kw)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(r).all())
+    assert_close(r.cpu().numpy(), gpu_core(kz, qz, V, g, p, k), 0.0, msg=f"{what}: clean call after the error path")
