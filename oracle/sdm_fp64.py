@@ -132,10 +132,25 @@ def sigmoid(x):
     return 1.0 / (1.0 + np.exp(-x))
 
 
-def rms_norm(x, w, eps=1e-6):
-    """RMSNorm (SM:63-71): x * rsqrt(mean(x^2) + eps) * w, in float64."""
+def rms_norm(x, w, eps=1e-6, rnd=None):
+    """RMSNorm (SM:63-71): x * rsqrt(mean(x^2) + eps) * w, in float64.  rnd: the rounding of a reduced-precision
+    evaluation (bf16 below), applied where the module casts: ``(x_f * rsqrt(...)).to(x.dtype) * w`` (SM:69-71)."""
     x = np.asarray(x, np.float64)
-    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+    n = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return n * w if rnd is None else rnd(rnd(n) * w)
+
+
+def bf16(a):
+    """The nearest bfloat16 (ties to even) of each value, as float64: what a bfloat16 tensor holds after a result is
+    cast to it.  float64 values are rounded to float32 first (the GPU computes in float32, then casts)."""
+    a32 = np.asarray(a, np.float32)
+    u = a32.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    return np.where(np.isfinite(a32), r, a32).astype(np.float64)
+
+
+def _no_round(a):
+    return a
 
 
 def address_weights(sv, log_scale, gate=None):
@@ -298,21 +313,26 @@ def layer_forward(x, p, cfg, reset=None, forced=None):
     """Whole RunTimeSdm.forward in float64 (OM:195-213 prepare, OM:249-274 forward, OM:243-247 finish).
 
     x (B, T, d); p holds the module's parameters under their state_dict names ('norm.w', 'wk.weight', ...,
-    'decays_fixed' as 'decay').  Returns y (B, T, d)."""
+    'decays_fixed' as 'decay').  cfg["round"] (default none): the rounding of a bfloat16 evaluation (``bf16``),
+    applied where a bfloat16 layer casts: the input norm, each projection (the gate logit with its bias), the
+    read-out and the output map (the core computes in float32 between its bfloat16 inputs and output).  Returns
+    y (B, T, d)."""
     x = np.asarray(x, np.float64)
     B, T, d = x.shape
     H = cfg["heads"]
     d_a = cfg["d_a"]
     dh = d // H
-    hx = rms_norm(x, p["norm.w"])
-    kz = (hx @ p["wk.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
-    qz = (hx @ p["wq.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
-    V = (hx @ p["wv.weight"].T).reshape(B, T, H, dh)
-    g = (hx @ p["wg.weight"].T + p["wg.bias"]) if cfg.get("write_gate", True) else None
+    rnd = cfg.get("round")
+    r_ = rnd or _no_round
+    hx = rms_norm(x, p["norm.w"], rnd=rnd)
+    kz = r_(hx @ p["wk.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
+    qz = r_(hx @ p["wq.weight"].T).reshape(B, T, H, d_a) + p["addr_b"]
+    V = r_(hx @ p["wv.weight"].T).reshape(B, T, H, dh)
+    g = r_(hx @ p["wg.weight"].T + p["wg.bias"]) if cfg.get("write_gate", True) else None
     core_p = dict(keys1=p["keys1"], keys2=p["keys2"], log_scale=p["log_scale"], decay=p["decay"],
                   onorm_w=p.get("onorm_w"))
     r = core_forward(kz, qz, V, g, core_p, cfg, reset=reset, forced=forced)
-    return r.reshape(B, T, d) @ p["wo.weight"].T
+    return r_(r_(r.reshape(B, T, d)) @ p["wo.weight"].T)
 
 
 def table_read(si, w, values):
@@ -330,15 +350,17 @@ def trained_sdm_forward(x, p, cfg, return_parts=False, forced=None):
     log_scale, wo.weight.  cfg: heads, d_a, k."""
     B, T, d = x.shape
     H, d_a, k = cfg["heads"], cfg["d_a"], cfg["k"]
-    hx = rms_norm(np.asarray(x, np.float64), p["norm.w"])
-    q = (hx @ np.asarray(p["wq.weight"], np.float64).T).reshape(B * T, H, d_a)
+    rnd = cfg.get("round")
+    r_ = rnd or _no_round
+    hx = rms_norm(np.asarray(x, np.float64), p["norm.w"], rnd=rnd)
+    q = r_(hx @ np.asarray(p["wq.weight"], np.float64).T).reshape(B * T, H, d_a)
     sv, si = pk_address(q, p["keys1"], p["keys2"], k)
     if forced is not None:
         sv, si = adopt_picks(q, p["keys1"], p["keys2"], sv, si, forced, cfg.get("adopt_tol", 1e-5),
                              cfg.get("adopt_log"))
     w = address_weights(sv, p["log_scale"])
-    r = table_read(si, w, p["values"]).reshape(B, T, d)
-    y = r @ np.asarray(p["wo.weight"], np.float64).T
+    r = r_(table_read(si, w, p["values"]).reshape(B, T, d))
+    y = r_(r @ np.asarray(p["wo.weight"], np.float64).T)
     if return_parts:
         return y, dict(q=q, sv=sv, si=si, w=w, r=r)
     return y
@@ -348,12 +370,15 @@ def silu(x):
     return x / (1.0 + np.exp(-x))
 
 
-def swiglu(x, gate_w, up_w, down_w):
-    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97)."""
-    return (silu(x @ gate_w.T) * (x @ up_w.T)) @ down_w.T
+def swiglu(x, gate_w, up_w, down_w, rnd=None):
+    """down(silu(gate x) * up x) (track4_sdmllm_models.py:89-97).  rnd: a bfloat16 evaluation's casts, after each
+    map, after silu and after the product (torch's bfloat16 ops compute in float32 and cast each result)."""
+    if rnd is None:
+        return (silu(x @ gate_w.T) * (x @ up_w.T)) @ down_w.T
+    return rnd(rnd(rnd(silu(rnd(x @ gate_w.T))) * rnd(x @ up_w.T)) @ down_w.T)
 
 
-def model_forward(idx, p, cfg, margins=None, forced=None):
+def model_forward(idx, p, cfg, margins=None, forced=None, return_hidden=False):
     """OneSdmLM.forward (OM:471-555, archive off) in float64: embedding, per layer x + RunTimeSdm(x, reset) and
     x + SwiGLU(RMSNorm x) (ffn 'mlp') or x + TrainedSdm(x) (ffn 'sdm'), final RMSNorm, tied head.
 
@@ -361,10 +386,16 @@ def model_forward(idx, p, cfg, margins=None, forced=None):
     reset_at_bos, bos_id, sdm_heads, sdm_d_a, sdm_k and the mixer options of core_forward.  When ``margins`` is a
     list, the smallest fp64 top-k margin of every addressing is appended to it.  forced: None or a dict of another
     implementation's picks, {("mem", i): (siw, sir), ("sdm", i): si} as (N, H, kk) arrays, taken at ties
-    (adopt_picks, cfg["adopt_tol"]; the adopted counts go to cfg["adopt_log"]).  Returns logits (B, T, V)."""
+    (adopt_picks, cfg["adopt_tol"]; the adopted counts go to cfg["adopt_log"]).  cfg["round"]: the rounding of a
+    bfloat16 model (``bf16``; p then holds the bfloat16 weights), applied at every cast of a bfloat16 forward: each
+    layer's (layer_forward, trained_sdm_forward, swiglu), each residual sum, the final norm and the logits.  Returns
+    logits (B, T, V), or with return_hidden the normalised hidden state (B, T, d) the tied head reads (the logits
+    are then that times emb.weight^T, rounded like them)."""
     E = p["emb.weight"]
     x = E[np.asarray(idx)]
     B, T, d = x.shape
+    rnd = cfg.get("round")
+    r_ = rnd or _no_round
     reset = (np.asarray(idx) == cfg.get("bos_id", 0)) if cfg.get("reset_at_bos") else None
     for i in range(cfg["layers"]):
         if cfg.get("mem", True):
@@ -377,19 +408,21 @@ def model_forward(idx, p, cfg, margins=None, forced=None):
                 for wn in ("wk.weight", "wq.weight"):
                     z = (hx @ lp[wn].T).reshape(B * T, H, d_a) + lp["addr_b"]
                     margins.append(float(topk_margin(z, lp["keys1"], lp["keys2"], cfg["k"]).min()))
-            x = x + layer_forward(x, lp, cfg, reset, None if forced is None else forced[("mem", i)])
+            x = r_(x + layer_forward(x, lp, cfg, reset, None if forced is None else forced[("mem", i)]))
         if cfg.get("ffn", "mlp") == "mlp":
-            x = x + swiglu(rms_norm(x, p[f"mnorms.{i}.w"]), p[f"mlps.{i}.gate.weight"], p[f"mlps.{i}.up.weight"],
-                           p[f"mlps.{i}.down.weight"])
+            x = r_(x + swiglu(rms_norm(x, p[f"mnorms.{i}.w"], rnd=rnd), p[f"mlps.{i}.gate.weight"],
+                              p[f"mlps.{i}.up.weight"], p[f"mlps.{i}.down.weight"], rnd=rnd))
         elif cfg["ffn"] == "sdm":
             pre = f"sdms.{i}."
             sp = {n[len(pre):]: v for n, v in p.items() if n.startswith(pre)}
             scfg = dict(heads=cfg["sdm_heads"], d_a=cfg["sdm_d_a"], k=cfg["sdm_k"], adopt_tol=cfg.get("adopt_tol", 1e-5),
-                        adopt_log=cfg.get("adopt_log"))
+                        adopt_log=cfg.get("adopt_log"), round=rnd)
             y, parts = trained_sdm_forward(x, sp, scfg, return_parts=True,
                                            forced=None if forced is None else forced[("sdm", i)])
             if margins is not None:
                 margins.append(float(topk_margin(parts["q"], sp["keys1"], sp["keys2"], scfg["k"]).min()))
-            x = x + y
-    h = rms_norm(x, p["nf.w"])
-    return h @ (E.T if cfg.get("tie", True) else p["head.weight"].T)
+            x = r_(x + y)
+    h = rms_norm(x, p["nf.w"], rnd=rnd)
+    if return_hidden:
+        return h
+    return r_(h @ (E.T if cfg.get("tie", True) else p["head.weight"].T))

@@ -25,6 +25,22 @@ static bool pick_enabled() {
   return on;
 }
 
+// dst[i] = src ? src[i] : 0 for n floats: the state of a call with no positions (a kernel, not a memset or copy
+// node, so that it may be captured in a graph)
+__global__ void __launch_bounds__(256) state_copy_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                         int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[i] = src ? src[i] : 0.f;
+}
+
+static int state_copy(float* dst, const float* src, int64_t n, hipStream_t st) {
+  if (n <= 0) return SDM_RT_OK;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(state_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, dst, src, n);
+  return check_launch("state copy");
+}
+
 int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, const CoreIO& io, void* workspace,
              hipStream_t st) {
   char* ws = static_cast<char*>(workspace);
@@ -180,15 +196,11 @@ int sdm_rt_forward(const sdm_rt_dims* dims, const sdm_rt_params* params, const v
     return set_err(SDM_RT_ENOSPACE, "workspace %zu bytes < required %zu", workspace_bytes, p.total);
   if (p.B == 0) return SDM_RT_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (p.T == 0) {
+  if (p.T == 0) {   // no positions: the state out is the state in (or empty)
     if (state_out_mem) {
-      const size_t mem_b = sizeof(float) * p.B * p.H * static_cast<size_t>(p.M) * p.dh;
-      const size_t cnt_b = sizeof(float) * p.B * p.H * static_cast<size_t>(p.M);
-      hipError_t e1 = state_in_mem ? hipMemcpyAsync(state_out_mem, state_in_mem, mem_b, hipMemcpyDeviceToDevice, st)
-                                   : hipMemsetAsync(state_out_mem, 0, mem_b, st);
-      hipError_t e2 = state_in_cnt ? hipMemcpyAsync(state_out_cnt, state_in_cnt, cnt_b, hipMemcpyDeviceToDevice, st)
-                                   : hipMemsetAsync(state_out_cnt, 0, cnt_b, st);
-      if (e1 != hipSuccess || e2 != hipSuccess) return set_err(SDM_RT_ELAUNCH, "state copy failed");
+      const int64_t n_cnt = static_cast<int64_t>(p.B) * p.H * p.M;
+      if ((rc = state_copy(state_out_mem, state_in_mem, n_cnt * p.dh, st))) return rc;
+      if ((rc = state_copy(state_out_cnt, state_in_cnt, n_cnt, st))) return rc;
     }
     return SDM_RT_OK;
   }

@@ -234,6 +234,17 @@ class OneSdmLM(nn.Module):
     def forward(self, idx, sequential=False):
         return self.project(self.hidden(idx, sequential))
 
+    def memory_parameters(self):
+        """Names of the memories' parameters (track4_onesdm_models.py:557-558): the mixers' (``mems.``); the
+        reference also lists its archive's (``arcs.``), which this model does not build."""
+        return {n for n, _ in self.named_parameters() if n.startswith("mems.") or n.startswith("arcs.")}
+
+    def set_leak(self, on):
+        """The reference self-test's causality control (track4_onesdm_models.py:560-564): sets every mixer's
+        ``_leak``.  The HIP mixers compute only the causal recurrence, so a forward with the control on raises."""
+        for m in self.mems:
+            m._leak = on
+
     # -- decoding ----------------------------------------------------------------------------------------------------
     def decode_state(self, batch, device=None):
         """An empty decode state for ``batch`` streams."""

@@ -65,9 +65,11 @@ class RunTimeSdm(nn.Module):
         self.write_gate, self.out_norm, self.learn_decay = write_gate, out_norm, learn_decay
         self.out_norm_eps = out_norm_eps
         self.enabled = True
+        self._leak = False        # the reference's test-only causality control (OM:165, 223); see forward
         self.keep_state = False   # set True to fill last_state (costs one state write per call)
-        self.keep_picks = False   # set True to fill last_picks and last_addresses (an extra addressing per call)
-        self.last_picks = self.last_addresses = None
+        self.keep_picks = False   # set True to fill last_picks, last_addresses and last_projections (an extra
+                                  # addressing per call, forward and step)
+        self.last_picks = self.last_addresses = self.last_projections = None
         self.norm = RMSNorm(d)
         self.wk = nn.Linear(d, heads * d_a, bias=False)
         self.wq = nn.Linear(d, heads * d_a, bias=False)
@@ -88,7 +90,8 @@ class RunTimeSdm(nn.Module):
         self.gate_bias0 = gate_bias
         self._gate_src = None
         self.last_gate = None
-        self.last_state = None
+        self._last_state = None
+        self._state_skipped = False
         self._fused = None
         self._ws = core.CoreWorkspace()
         self._prm = core.ParamCache()
@@ -216,7 +219,7 @@ class RunTimeSdm(nn.Module):
         y = self.wo(r).to(x.dtype)
         self._gate_src = (g.detach().contiguous() if g is not None else None, None, (B, T, H), x.device)
         self._last_gate = None
-        self.last_state = None
+        self._last_state, self._state_skipped = None, False
         return y
 
     def forward(self, x, reset=None, hx=None):
@@ -228,6 +231,11 @@ class RunTimeSdm(nn.Module):
         B, T, _ = x.shape
         if not self.enabled:
             return torch.zeros_like(x)
+        if self._leak:
+            raise NotImplementedError(
+                "RunTimeSdm._leak (set_leak) is the reference self-test's causality control, a mask of its dense "
+                "chunk algorithm (track4_onesdm_models.py:223) that lets a position read later writes of its chunk; "
+                "the HIP kernels compute only the causal recurrence")
         self._check(x, reset)
         if self._training(x):
             return self._forward_train(x, reset)
@@ -247,15 +255,32 @@ class RunTimeSdm(nn.Module):
             if self.keep_picks:   # the same addressing kernels as the core's, on the same projections
                 prm = self._core_params(x.device)
                 self.last_addresses = (kz, qz)   # before addr_b
+                self.last_projections = (kz, qz, V, g)
                 self.last_picks = tuple(
                     core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
                                  params=prm)[0] for z in (kz, qz))
-        # the gate logits as a view of the projection buffer ([B, T, H], strided): a copy costs a launch per layer,
-        # the view keeps the buffer until the next forward (the whole fused projection, ~84 MB at B=8, T=2048)
-        self._gate_src = (g, None, (B, T, H), x.device)
+            # the gate logits copied out of the projection buffer ([B, T, H]; a view would keep the whole buffer,
+            # ~59 MB at B=8, T=2048, until the next forward); last_gate applies the sigmoid when first read
+            g_keep = None if g is None else g.contiguous()
+        self._gate_src = (g_keep, None, (B, T, H), x.device)
         self._last_gate = None
-        self.last_state = state
+        self._last_state, self._state_skipped = state, not self.keep_state
         return y
+
+    @property
+    def last_state(self):
+        """(mem [B, H, M, dh], cnt [B, H, M]) float32 after the last forward's final position, as the reference
+        sets it on every call (track4_onesdm_models.py:273).  Writing it costs a state write per call (25.6 MB at
+        B=8, T=2048), so the forward writes it only with ``keep_state`` set; reading it after a forward that skipped
+        it raises instead of returning a stale or missing value."""
+        if self._state_skipped:
+            raise RuntimeError("RunTimeSdm.last_state: set keep_state = True before the forward to receive the final "
+                               "state (it is not written by default: 25.6 MB per call at B=8, T=2048)")
+        return self._last_state
+
+    @last_state.setter
+    def last_state(self, value):
+        self._last_state, self._state_skipped = value, False
 
     @property
     def last_gate(self):
@@ -303,6 +328,13 @@ class RunTimeSdm(nn.Module):
                 out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
                 params=self._core_params(x.device))
             y = core.linear(r, wo, as_matmul=True).to(x.dtype)
+            if self.keep_picks:   # the addressing kernels on the step's rows: the decode step's own picks
+                prm = self._core_params(x.device)
+                self.last_addresses = (kz, qz)
+                self.last_projections = (kz, qz, V, g)
+                self.last_picks = tuple(
+                    core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
+                                 params=prm)[0] for z in (kz, qz))
         return y.reshape(x.shape)
 
     def forward_sequential(self, x, reset=None):

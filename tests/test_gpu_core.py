@@ -100,6 +100,12 @@ def test_zero_length_and_empty_batch():
     assert r.shape == (2, 0, 32) and np.all(m == 0) and np.all(c == 0)
     kz, qz, V, g, p = core_inputs(0, 5, 4, 8, 8, 4, seed=50)
     assert gpu_core(kz, qz, V, g, p, 4).shape == (0, 5, 32)
+    # no positions with a state in: the state out is that state (copied by a kernel, no memset or copy node)
+    kz, qz, V, g, p = core_inputs(2, 0, 4, 8, 8, 4, seed=51)
+    rng = np.random.default_rng(51)
+    st = (rng.standard_normal((2, 4, 16, 8)).astype(np.float32), rng.random((2, 4, 16)).astype(np.float32))
+    r, (m, c) = gpu_core(kz, qz, V, g, p, 4, state_in=st, want_state=True)
+    assert r.shape == (2, 0, 32) and np.array_equal(m, st[0]) and np.array_equal(c, st[1])
 
 
 def test_bench_shape_bf16():

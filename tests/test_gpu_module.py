@@ -228,3 +228,26 @@ def test_last_state_matches_oracle():
     np.testing.assert_allclose(mem.cpu().numpy(), parts["mem"], atol=1e-5, rtol=1e-5)
     np.testing.assert_allclose(cnt.cpu().numpy(), parts["cnt"], atol=1e-5, rtol=1e-5)
     np.testing.assert_allclose(y.cpu().numpy(), O.layer_forward(x, pp, cfg), atol=1e-5, rtol=1e-5)
+
+
+def test_last_gate_is_kept_apart_and_last_state_is_loud():
+    """After an inference forward the gate logits are a small contiguous [B, T, H] tensor (not a view that keeps
+    the fused projection's buffer alive), last_gate is their sigmoid, and reading last_state after a forward that
+    did not write it (keep_state unset) raises instead of returning None; with keep_state it holds the state."""
+    cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8)
+    p = S.layer_params(cfg, seed=70)
+    m = build(cfg, p)
+    x = torch.from_numpy(S.layer_input(2, 50, 64, seed=1070)).cuda()
+    with torch.no_grad():
+        m(x)
+    g = m._gate_src[0]
+    assert g.is_contiguous() and tuple(g.shape) == (2, 50, 4) and g.untyped_storage().nbytes() == g.numel() * g.element_size()
+    gate = m.last_gate
+    assert tuple(gate.shape) == (2, 50, 4) and float(gate.min()) >= 0 and float(gate.max()) <= 1
+    with pytest.raises(RuntimeError, match="keep_state"):
+        _ = m.last_state
+    m.keep_state = True
+    with torch.no_grad():
+        m(x)
+    mem, cnt = m.last_state
+    assert tuple(mem.shape) == (2, 4, 64, 16) and tuple(cnt.shape) == (2, 4, 64)

@@ -74,3 +74,21 @@ def test_disabled_returns_zeros_without_the_library():
     m.enabled = False
     x = torch.randn(2, 3, 768)
     assert torch.equal(m(x), torch.zeros_like(x))
+
+
+def test_memory_parameters_and_the_leak_control():
+    """OneSdmLM.memory_parameters (track4_onesdm_models.py:557-558) names the mixers' parameters; set_leak
+    (:560-564) sets every mixer's _leak, and a mixer forward with the control on raises (the kernels compute only
+    the causal recurrence) instead of returning a causal result the control expects to differ."""
+    from sdmchat_amd.model import OneSdmLM
+    lm = OneSdmLM(64, d=32, layers=2, mlp_f=48, heads=2, n_sub=4, d_a=8, k=4, decays=(0.5, 0.9))
+    names = lm.memory_parameters()
+    want = {n for n, _ in lm.named_parameters() if n.startswith("mems.")}
+    assert names == want and "mems.0.keys1" in names and "mems.1.onorm_w" in names
+    assert not any(n.startswith("mlps.") or n.startswith("emb") for n in names)
+    lm.set_leak(True)
+    assert all(m._leak for m in lm.mems)
+    with pytest.raises(NotImplementedError, match="causality control"):
+        lm.mems[0](torch.zeros(1, 3, 32))
+    lm.set_leak(False)
+    assert not any(m._leak for m in lm.mems)

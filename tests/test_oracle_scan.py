@@ -228,3 +228,25 @@ def test_planted_scan_mistakes_fail_the_closed_form():
     np.testing.assert_allclose(_closed_variant(siw, ww, sir, wr, V, lam, 1, False), num, atol=1e-12)
     assert np.abs(_closed_variant(siw, ww, sir, wr, V, lam, 0, False) - num).max() > 1e-3
     assert np.abs(_closed_variant(siw, ww, sir, wr, V, lam, 1, True) - num).max() > 1e-3
+
+
+def test_bf16_rounding_equals_torch_cast():
+    """oracle.sdm_fp64.bf16 (the casts of the bfloat16 model restatement) equals torch's float32 -> bfloat16 cast on
+    random values, exact ties (round half to even, both directions), values one float32 ulp either side of a tie,
+    subnormals, zeros and infinities; float64 inputs round through float32."""
+    import torch
+
+    from oracle import sdm_fp64 as O
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(10000) * 10.0 ** rng.integers(-30, 30, 10000),
+                        [0.0, -0.0, np.inf, -np.inf, 1e-40, -3e-39, 3.0e38]]).astype(np.float32)
+    u = rng.integers(0, 2 ** 31, 2000, dtype=np.uint64).astype(np.uint32)
+    ties = ((u & 0xFFFF0000) | 0x8000).view(np.float32)           # exactly halfway between two bfloat16 values
+    near = np.concatenate([ties, np.nextafter(ties, np.inf), np.nextafter(ties, -np.inf)])
+    for v in (x, near[np.isfinite(near)]):
+        want = torch.from_numpy(v).to(torch.bfloat16).float().numpy().astype(np.float64)
+        got = O.bf16(v)
+        assert np.array_equal(got, want) or np.allclose(got, want, rtol=0, atol=0, equal_nan=True)
+        assert np.array_equal(np.signbit(got), np.signbit(want))
+    d = rng.standard_normal(1000)
+    assert np.array_equal(O.bf16(d), torch.from_numpy(d.astype(np.float32)).to(torch.bfloat16).double().numpy())
