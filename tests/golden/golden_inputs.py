@@ -41,6 +41,24 @@ def layer_addresses(seed=21, N=2048, d=768, H=12, d_a=64, n_sub=32):
     return z, k1, k2
 
 
+# --- the addresses of the bench workload ------------------------------------------------------------------------
+def bench_addresses():
+    """The write keys and read queries of the layer bench workload (B=8, T=2048, d=768, 12 heads of M=1,024, d_a 64,
+    k=8; parameters sdmchat_amd.synthetic.layer_params(seed=0), input layer_input(seed=1)) as a bfloat16 layer forms
+    them: x rounded to bfloat16, the input norm x rsqrt(mean x^2 + 1e-6) rounded to bfloat16 (norm.w is 1), the
+    wk and wq maps summed in float64 and rounded to bfloat16 (addr_b is 0).  Returns zw, zr (16,384, 12, 64) float32
+    and keys1, keys2 (12, 32, 32) float32.  (The GPU's own float32 maps may round an occasional value the other
+    way; these are the fixture's addresses, fed as they are to every implementation.)"""
+    from sdmchat_amd import synthetic as S
+    cfg = S.layer_cfg()
+    p = S.layer_params(cfg, seed=0)
+    x = bf16_round(S.layer_input(8, 2048, 768, seed=1)).astype(np.float64).reshape(8 * 2048, 768)
+    hx = bf16_round((x / np.sqrt(np.mean(x * x, -1, keepdims=True) + 1e-6)).astype(np.float32)).astype(np.float64)
+    zw = bf16_round((hx @ p["wk.weight"].astype(np.float64).T).astype(np.float32)).reshape(-1, 12, 64)
+    zr = bf16_round((hx @ p["wq.weight"].astype(np.float64).T).astype(np.float32)).reshape(-1, 12, 64)
+    return zw, zr, p["keys1"], p["keys2"]
+
+
 # --- one RunTimeSdm layer ----------------------------------------------------------------------------------------
 def layer_case(name, seed):
     """(constructor kwargs, state dict of float32 arrays, x (B, T, d) float32) of a named layer case:

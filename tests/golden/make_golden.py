@@ -24,6 +24,14 @@ PCG64; only seeds and a checksum of each input are stored, the tests regenerate 
              a top-k margin above 2e-6, so the picks are the same in any correct float32 or float64 evaluation.
   model_mlp.*, model_sdm.*   the logits of a tiny OneSdmLM of each arm (golden_inputs.MODEL_KW, reset at BOS), with
              the same margin search.
+
+``python tests/golden/make_golden.py bench`` writes tests/golden/bench_ties_golden.npz: the reference's ordered picks
+(si int16, sv float32) at every address of the bench workload (golden_inputs.bench_addresses: the 393,216 write keys
+and read queries of B=8, T=2048, 12 heads) where two consecutive of its 9 best fp64 scores lie within 1e-5 (the
+pick or the order of the picks is a near-tie), their flat (token, head) indices (near_w, near_r), a checksum of
+each address set, and a checksum of the reference's whole ordered pick array of each set (int16, (393,216 / 2, 8)):
+a test that splices the recorded near-tie rows into its own picks reproduces that checksum exactly when every other
+address's picks equal the reference's.
 """
 import os
 import sys
@@ -188,8 +196,55 @@ def runtime_main():
     print("wrote", out, os.path.getsize(out), "bytes")
 
 
+def _order_gap(O, z, keys1, keys2, k):
+    """Per address, the smallest fp64 gap between consecutive scores among its kk + 1 best locations: below it, a
+    float32 evaluation may pick (the kk-th against the next) or order (two picks) differently from float64.  The
+    kk + 1 best lie in the grid of each half's kk + 1 best sub-keys (oracle.sdm_fp64.topk_margin_pruned)."""
+    n_sub = keys1.shape[1]
+    kk = min(k, min(k, n_sub) ** 2)
+    s1, s2 = O.half_scores(z, keys1, keys2)
+    c = min(kk + 1, n_sub)
+    v1 = -np.sort(-s1, axis=-1)[..., :c]
+    v2 = -np.sort(-s2, axis=-1)[..., :c]
+    g = -np.sort(-((v1[..., :, None] + v2[..., None, :]) * 0.5).reshape(*v1.shape[:-1], c * c), axis=-1)[..., :kk + 1]
+    return (g[..., :-1] - g[..., 1:]).min(-1)
+
+
+def bench_main(margin=1e-5):
+    """The reference's picks at the near-ties of the bench workload's 393,216 addresses (golden_inputs.
+    bench_addresses: write keys and read queries of B=8, T=2048, 12 heads): every address where two consecutive of
+    its kk + 1 best fp64 scores lie within ``margin`` (where a float32 evaluation may order or pick differently from
+    float64), with the reference's ordered picks si and scores sv there."""
+    sys.path.insert(0, REF_DIR)
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+    import track4_onesdm_models as ref  # noqa: E402  (reference checkout, this container only)
+    from oracle import sdm_fp64 as O  # noqa: E402
+    from tests.golden import golden_inputs as G  # noqa: E402
+
+    torch.set_num_threads(8)
+    zw, zr, k1, k2 = G.bench_addresses()
+    blob = {"bench.k": np.int64(8), "bench.margin": np.float64(margin)}
+    for name, z in (("w", zw), ("r", zr)):
+        mg = _order_gap(O, z.astype(np.float64), k1.astype(np.float64), k2.astype(np.float64), 8)
+        near = np.flatnonzero(mg.reshape(-1) < margin)   # flat (token, head) indices
+        with torch.no_grad():
+            sv, si = ref.pk_address(torch.from_numpy(z), torch.from_numpy(k1), torch.from_numpy(k2), 8)
+        H = z.shape[1]
+        blob[f"bench.digest_{name}"] = G.digest(z)
+        blob[f"bench.near_{name}"] = near.astype(np.int32)
+        blob[f"bench.si_{name}"] = si.numpy().reshape(-1, H, 8).reshape(-1, 8)[near].astype(np.int16)
+        blob[f"bench.sv_{name}"] = sv.numpy().reshape(-1, 8)[near].astype(np.float32)
+        blob[f"bench.all_digest_{name}"] = G.digest(si.numpy().reshape(-1, 8).astype(np.int16))
+        print(name, z.shape, "near-ties below", margin, ":", len(near), flush=True)
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "bench_ties_golden.npz")
+    np.savez_compressed(out, **blob)
+    print("wrote", out, os.path.getsize(out), "bytes")
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["runtime"]:
         runtime_main()
+    elif sys.argv[1:] == ["bench"]:
+        bench_main()
     else:
         main()

@@ -82,3 +82,56 @@ def test_oracle_model_logits_equal_reference(ffn):
     want = GOLD[f"model_{ffn}.logits"].astype(np.float64)
     np.testing.assert_allclose(logits, want, atol=2e-5 * np.abs(want).max(), rtol=0)
     del torch
+
+
+BENCH = np.load(os.path.join(os.path.dirname(__file__), "golden", "bench_ties_golden.npz"))
+
+
+def bench_near_ties():
+    """The bench workload's addresses (regenerated, checked against the recorded checksums) and, per address set,
+    the flat (token, head) indices of its near-ties with the reference's picks there."""
+    zw, zr, k1, k2 = G.bench_addresses()
+    assert G.digest(zw) == BENCH["bench.digest_w"] and G.digest(zr) == BENCH["bench.digest_r"], \
+        "regenerated bench addresses differ from the recorded ones"
+    return {"w": zw, "r": zr}, k1, k2
+
+
+def spliced_digest(si, s):
+    """The checksum of a whole ordered pick array (flat (token, head), 8) with the reference's near-tie rows of set s
+    spliced in: the reference's own checksum exactly when every other row equals the reference's."""
+    full = np.asarray(si).astype(np.int16).copy()
+    full[BENCH[f"bench.near_{s}"]] = BENCH[f"bench.si_{s}"]
+    return G.digest(full)
+
+
+def bench_pick_diffs(z, k1, k2, near, si, ref):
+    """Flat near-tie addresses whose ordered picks si differ from the reference's ref (both (n, 8)), after checking
+    that every difference is a tie: at each differing position the two slots' fp64 scores agree within TIE."""
+    H = z.shape[1]
+    diff = si != ref
+    rows = np.flatnonzero(diff.any(-1))
+    for i in rows:
+        tok, h = divmod(int(near[i]), H)
+        g = O.full_grid(z[tok:tok + 1, h:h + 1].astype(np.float64), k1[h:h + 1], k2[h:h + 1])[0, 0]
+        gap = np.abs(g[ref[i]] - g[si[i]])[diff[i]]
+        assert np.all(gap < TIE), f"address {int(near[i])}: a pick differs from the reference's at an fp64 gap of " \
+                                  f"{float(gap.max()):.3e}"
+    return len(rows)
+
+
+def test_oracle_picks_equal_reference_at_bench_near_ties():
+    """At every address of the bench workload (B=8, T=2048, 12 heads, both sets) where two of its 9 best fp64 scores
+    lie within 1e-5 (a near-tie of the pick or of the order), the oracle's ordered picks against the reference's own
+    (make_golden.py bench): they differ only where the two slots' fp64 scores are within TIE, and the count is
+    printed; at every other address the oracle's ordered picks equal the reference's exactly (the oracle's whole pick
+    array with the recorded near-tie rows spliced in has the checksum of the reference's)."""
+    zs, k1, k2 = bench_near_ties()
+    k1d, k2d = k1.astype(np.float64), k2.astype(np.float64)
+    for s in ("w", "r"):
+        near = BENCH[f"bench.near_{s}"]
+        _, si = O.pk_address(zs[s].astype(np.float64), k1d, k2d, int(BENCH["bench.k"]))
+        si = si.reshape(-1, si.shape[-1])
+        n = bench_pick_diffs(zs[s], k1d, k2d, near, si[near], BENCH[f"bench.si_{s}"].astype(np.int64))
+        assert spliced_digest(si, s) == BENCH[f"bench.all_digest_{s}"], "picks away from the near-ties differ"
+        print(f"bench near-ties ({s}): {n} of {len(near)} addresses order or pick differently from the reference, "
+              f"all at fp64 gaps < {TIE}")
