@@ -1,88 +1,7 @@
-// sdm_address_bf16.hip -- product-key addressing kernels for bf16 addresses (pk_address,
-// experiments/track4/sdmllm/track4_onesdm_models.py:134-148, with the softmax weights and gate of prepare :203-207).
-// The kernels are instantiated per input type in their own translation unit so the builds run in parallel.
-#include "sdm_common.h"
+// sdm_address_bf16.hip -- the addressing kernels of sdm_address.h instantiated for bf16 addresses.
+#include "sdm_address.h"
 
 namespace sdmrt {
-
-// sdm_rt_address: one thread per (token, head).  Grid: x = token tiles of 64, y = head.  MODE 1 and 2: the tile is
-// addressed by the wave on the matrix cores (address_wave; 2 = no masked candidate), MODE 3 and 4 likewise with 64
-// sub-keys per half (two sub-key tiles; 4 = no masked candidate), MODE 0: per thread with the sub-keys staged in
-// LDS (address_one).
-template <int HALF, int CAP, typename InT, int MODE>
-__global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
-  extern __shared__ float kn[];   // [2][n_sub][HALF] (per-thread path)
-  const int h = blockIdx.y;
-  const int64_t N = static_cast<int64_t>(a.B) * a.T;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int64_t n = n0 + threadIdx.x;
-  if (blockIdx.z == 1) {   // the second address set
-    a.z = a.z2;
-    a.z_stride = a.z2_stride;
-    a.gl = nullptr;
-    a.slot_out = a.slot_out2;
-    a.w_out = a.w_out2;
-    a.s_out = a.s_out2;
-  }
-  const float gate =
-      (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
-  int slot[CAP];
-  float w[CAP], sc[CAP];
-  if constexpr (MODE > 0) {
-    address_wave<HALF, CAP, InT, MODE == 2 || MODE == 4, (MODE >= 3 ? 64 : 32)>(
-        a.g, h, static_cast<const InT*>(a.z) + n0 * a.z_stride, a.z_stride,
-                                     static_cast<int>(min<int64_t>(64, N - n0)), gate, slot, w, sc);
-    if (n >= N) return;
-  } else {
-    stage_keys<HALF>(a.g, h, kn, threadIdx.x, 64);
-    __syncthreads();
-    if (n >= N) return;
-    const InT* zrow = static_cast<const InT*>(a.z) + n * a.z_stride + static_cast<int64_t>(h) * 2 * HALF;
-    address_one<HALF, CAP, InT>(a.g, h, kn, zrow, gate, slot, w, sc);
-  }
-  const int b = static_cast<int>(n / a.T);
-  const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
-  const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
-#pragma unroll
-  for (int p = 0; p < CAP; ++p) {
-    if (p < a.pitch) {
-      const bool live = p < a.g.kk;
-      a.slot_out[base + p] = live ? slot[p] : -1;
-      if (a.w_out) a.w_out[base + p] = w[p];
-      if (a.s_out) a.s_out[base + p] = sc[p];
-    }
-  }
-}
-
-template <int HALF, typename InT>
-struct AddressLaunch {
-  template <int CAP, int MODE>
-  static void go(const Plan& p, const AddrArgs& a, hipStream_t st) {
-    const int64_t N = static_cast<int64_t>(p.B) * p.T;
-    dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H, a.z2 ? 2 : 1);
-    const size_t lds = MODE > 0 ? 0 : sizeof(float) * 2 * p.n_sub * HALF;
-    hipLaunchKernelGGL((address_kernel<HALF, CAP, InT, MODE>), grid, dim3(64), lds, st, a);
-  }
-  static int run(const Plan& p, const AddrArgs& a, hipStream_t st) {
-    if constexpr (mf_half(HALF)) {
-      if (use_mf(p)) {
-        if (full_grid(p)) go<8, 2>(p, a, st);
-        else if (p.cap == 8) go<8, 1>(p, a, st);
-        else go<16, 1>(p, a, st);
-        return check_launch("address");
-      }
-      if (use_mf64(p)) {   // 64 sub-keys per half: no masked candidate when n_sub = 64 and c1 = kk = CAP
-        const bool full = p.n_sub == 64 && p.c1 == p.cap && p.kk == p.cap;
-        if (p.cap == 8) full ? go<8, 4>(p, a, st) : go<8, 3>(p, a, st);
-        else full ? go<16, 4>(p, a, st) : go<16, 3>(p, a, st);
-        return check_launch("address");
-      }
-    }
-    if (p.cap == 8) go<8, 0>(p, a, st);
-    else go<16, 0>(p, a, st);
-    return check_launch("address");
-  }
-};
 
 int launch_address_bf16(const Plan& p, const AddrArgs& a, hipStream_t st) {
   return by_half<AddressLaunch, bf16_t>(p.half, p, a, st);

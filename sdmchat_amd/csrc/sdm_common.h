@@ -647,69 +647,71 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
   }
 }
 
-// Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
-// clamped; their lanes' outputs are unspecified): the selection of address_one on offset keys, scores within 2^-31
-// of float rounding (2^-29 with NS = 64).  NS: 32 sub-keys per half (n_sub <= 32) or 64 (n_sub <= 64: two sub-key
-// tiles scored in turn, each tile's CAP best merged into the half's).  FULL: n_sub = NS and c1 = kk = CAP (no
-// candidate is masked).  All 64 lanes of the wave must call it.
-template <int HALF, int CAP, typename InT, bool FULL, int NS = 32>
-__device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
-                                             float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
+// The CAP best offset keys (descending) of half hf of the wave's 64 addresses over sub-key tile `tile` (sub-keys
+// 32 tile ... 32 tile + 31), lane l holding address row l of z0 (rows past `rows` are clamped).  The tile's 32 keys
+// are taken CAP at a time (sub-keys 2 GR grp ... 2 GR grp + 2 GR - 1), each group sorted and merged into the best:
+// the same top CAP as one 32-key selection (the keys are distinct), with a quarter of the keys live at once.
+// (best is merged into when merge_into is set: the keys of an earlier tile of the same half.)
+template <int HALF, int CAP, typename InT, bool FULL, int NS>
+__device__ __forceinline__ void tile_best(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows, int hf,
+                                          int tile, bool merge_into, double (&best)[CAP]) {
   using KL = KeyLayout<NS>;
   const int kb = (threadIdx.x & 63) >> 5;
-  double hk[2][CAP];   // ranked half keys
+  floatx16 acc[2];
+  float inv[2];
+  if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
+  else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
+  // after the swap below lane l holds every score of address row l
+  const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
+  constexpr int GR = CAP / 2;   // score registers per group
 #pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    double best[CAP];   // the half's CAP best keys so far, descending
+  for (int grp = 0; grp < 16 / GR; ++grp) {
+    double c[CAP];
 #pragma unroll
-    for (int tile = 0; tile < NS / 32; ++tile) {   // sub-keys 32 tile ... 32 tile + 31
-      floatx16 acc[2];
-      float inv[2];
-      if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
-      else half_scores_f32<HALF, InT, FULL>(g, h, hf, z0, zstride, rows, acc, inv, 32 * tile);
-      // after the swap below lane l holds every score of address row l.  The tile's 32 keys are taken CAP at a
-      // time (sub-keys 2 GR grp ... 2 GR grp + 2 GR - 1), each group sorted and merged into the half's best: the
-      // same top CAP as one 32-key selection (the keys are distinct), with a quarter of the keys live at once.
-      const double dinv = static_cast<double>(kb ? inv[1] : inv[0]);
-      constexpr int GR = CAP / 2;   // score registers per group
-#pragma unroll
-      for (int grp = 0; grp < 16 / GR; ++grp) {
-        double c[CAP];
-#pragma unroll
-        for (int rr = 0; rr < GR; ++rr) {
-          const int r = GR * grp + rr;
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]),
-                                                           false, false);
-          const int i0 = 32 * tile + 8 * (r / 4) + (r % 4);
-          if (hf == 0) {
-            c[rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[0]), dinv, i0);
-            c[GR + rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
-          } else {
-            c[rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[0]), dinv, i0);
-            c[GR + rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
-          }
-          if (!FULL) {   // sub-keys past n_sub are never picked
-            if (i0 >= g.n_sub) c[rr] = key_invalid(c[rr]);
-            if (i0 + 4 >= g.n_sub) c[GR + rr] = key_invalid(c[GR + rr]);
-          }
-        }
-        if constexpr (CAP == 8) sort8_desc(c);
-        else bitonic_sort_desc<CAP>(c);
-        if (tile == 0 && grp == 0) {
-#pragma unroll
-          for (int r = 0; r < CAP; ++r) best[r] = c[r];
-        } else {
-          merge_top_desc<CAP>(best, c);
-        }
+    for (int rr = 0; rr < GR; ++rr) {
+      const int r = GR * grp + rr;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][r]), __float_as_uint(acc[1][r]),
+                                                       false, false);
+      const int i0 = 32 * tile + 8 * (r / 4) + (r % 4);
+      if (hf == 0) {
+        c[rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[0]), dinv, i0);
+        c[GR + rr] = half_key<KL::FS1, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+      } else {
+        c[rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[0]), dinv, i0);
+        c[GR + rr] = half_key<KL::FS2, NS>(__uint_as_float(sw[1]), dinv, i0 + 4);
+      }
+      if (!FULL) {   // sub-keys past n_sub are never picked
+        if (i0 >= g.n_sub) c[rr] = key_invalid(c[rr]);
+        if (i0 + 4 >= g.n_sub) c[GR + rr] = key_invalid(c[GR + rr]);
       }
     }
+    if constexpr (CAP == 8) sort8_desc(c);
+    else bitonic_sort_desc<CAP>(c);
+    if (!merge_into && grp == 0) {
 #pragma unroll
-    for (int r = 0; r < CAP; ++r)
-      hk[hf][r] = key_or(best[r], static_cast<uint32_t>(15 - r) << (hf == 0 ? KL::RS1 : KL::RS2));
+      for (int r = 0; r < CAP; ++r) best[r] = c[r];
+    } else {
+      merge_top_desc<CAP>(best, c);
+    }
   }
-  // combine over the dominance-pruned grid (see address_one)
+}
+
+// the half's best keys tagged with their rank within the half (the grid key's rank fields)
+template <int CAP, int NS>
+__device__ __forceinline__ void rank_half(int hf, const double (&best)[CAP], double (&hk)[CAP]) {
+  using KL = KeyLayout<NS>;
+#pragma unroll
+  for (int r = 0; r < CAP; ++r) hk[r] = key_or(best[r], static_cast<uint32_t>(15 - r) << (hf == 0 ? KL::RS1 : KL::RS2));
+}
+
+// The picks of one address from its two ranked halves: the combine over the dominance-pruned grid (see
+// address_one), the slots, the mean scores and the softmax weights (times the gate).
+template <int CAP, bool FULL, int NS>
+__device__ __forceinline__ void grid_pick(const AddrGeom& g, int h, const double (&hk0)[CAP], const double (&hk1)[CAP],
+                                          float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
+  using KL = KeyLayout<NS>;
   auto cell = [&](int ra, int rb) {
-    const double k = hk[0][ra] + hk[1][rb];
+    const double k = hk0[ra] + hk1[rb];
     if (FULL) return k;
     return (ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk) ? k : key_invalid(k);
   };
@@ -777,6 +779,26 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
     w[p] = live ? e[p] * wscale : 0.f;
     score[p] = live ? cv[p] : 0.f;
   }
+}
+
+// Picks of address l (lane l) of the 64 rows z0[r * zstride + h * 2 * HALF ...], r < rows (rows past `rows` are
+// clamped; their lanes' outputs are unspecified): the selection of address_one on offset keys, scores within 2^-31
+// of float rounding (2^-29 with NS = 64).  NS: 32 sub-keys per half (n_sub <= 32) or 64 (n_sub <= 64: two sub-key
+// tiles scored in turn, each tile's CAP best merged into the half's).  FULL: n_sub = NS and c1 = kk = CAP (no
+// candidate is masked).  All 64 lanes of the wave must call it.
+template <int HALF, int CAP, typename InT, bool FULL, int NS = 32>
+__device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT* z0, int64_t zstride, int rows,
+                                             float gate, int (&slot)[CAP], float (&w)[CAP], float (&score)[CAP]) {
+  double hk[2][CAP];   // ranked half keys
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    double best[CAP];   // the half's CAP best keys so far, descending
+#pragma unroll
+    for (int tile = 0; tile < NS / 32; ++tile)
+      tile_best<HALF, CAP, InT, FULL, NS>(g, h, z0, zstride, rows, hf, tile, tile > 0, best);
+    rank_half<CAP, NS>(hf, best, hk[hf]);
+  }
+  grid_pick<CAP, FULL, NS>(g, h, hk[0], hk[1], gate, slot, w, score);
 }
 
 struct AddrArgs {

@@ -28,12 +28,18 @@ __device__ __forceinline__ void gemm_step(const bf16_t* a0, const bf16_t* a1, co
 // step; the accumulators hold column n0 + l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 (r < 16) of each 32-row half.
 // The four partial tiles meet in LDS; thread (g, l) adds registers 8 g .. 8 g + 7 of lane l over the waves in order,
 // adds the bias and rounds to bfloat16.  STEPS: 16-deep steps per wave (K / 64) when unrolled, 0 for a loop.
-template <int STEPS>
+// Rows of the x tile staged in LDS (STAGE: k = 768): 64 rows of 768 bfloat16 plus 16 bytes, so that the 32 rows a
+// matrix-core operand load reads fall on different banks
+constexpr int kStageK = 768;
+constexpr int kStageRow = kStageK * 2 + 16;   // bytes
+
+template <int STEPS, bool STAGE>
 __global__ void __launch_bounds__(256) gemm_rows_kernel(const bf16_t* __restrict__ x, int64_t xs,
                                                         const bf16_t* __restrict__ w, int64_t ws,
                                                         const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
                                                         int64_t ys, int rows, int k) {
   __shared__ float part[4][32][64];   // [wave][accumulator register][lane]
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs_lds[];   // STAGE: the x tile [64][kStageRow]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * kGemmCols, m0 = blockIdx.y * kGemmRows;
   const int kq = k / 4;
@@ -43,7 +49,42 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const bf16_t* __restrict
   const bf16_t* a1 = x + static_cast<int64_t>(min(m0 + 32 + r, rows - 1)) * xs + kb;   // their sums unused
   const bf16_t* b = w + static_cast<int64_t>(n0 + r) * ws + kb;
   floatx16 acc0 = {}, acc1 = {};
-  if constexpr (STEPS > 0) {   // every operand of the wave loaded before the first product: one memory round trip
+  if constexpr (STAGE) {
+    // The x tile is the same for every column tile, and the operand layout (lane l: row l % 32) makes each direct
+    // load touch 32 rows; staged, each load instruction reads 1 KB of consecutive row bytes (thread t: the 16-byte
+    // pieces t, t + 256, ...), and the operands come from LDS.  The weights' loads are issued first.  (Staging the
+    // weight tile the same way gains under 0.1 us.)
+    static_assert(STEPS == kStageK / 64, "the staged tile holds k = 768");
+    uint4 wv[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) wv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
+    constexpr int kPieces = kGemmRows * kStageK / 8;   // 16-byte pieces of the tile: 6,144
+    uint4 xv[kPieces / 256];
+#pragma unroll
+    for (int j = 0; j < kPieces / 256; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      const int row = i / (kStageK / 8), col8 = i - row * (kStageK / 8);
+      xv[j] = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(min(m0 + row, rows - 1)) * xs + 8 * col8);
+    }
+#pragma unroll
+    for (int j = 0; j < kPieces / 256; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      const int row = i / (kStageK / 8), col8 = i - row * (kStageK / 8);
+      *reinterpret_cast<uint4*>(xs_lds + row * kStageRow + 16 * col8) = xv[j];
+    }
+    __syncthreads();
+    const unsigned char* l0 = xs_lds + r * kStageRow + 2 * kb;
+    const unsigned char* l1 = xs_lds + (32 + r) * kStageRow + 2 * kb;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const uint4 x0 = *reinterpret_cast<const uint4*>(l0 + 32 * s);
+      const uint4 x1 = *reinterpret_cast<const uint4*>(l1 + 32 * s);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x0), __builtin_bit_cast(bf16x8, wv[s]),
+                                                     acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x1), __builtin_bit_cast(bf16x8, wv[s]),
+                                                     acc1, 0, 0, 0);
+    }
+  } else if constexpr (STEPS > 0) {   // every operand of the wave loaded before the first product: one round trip
     uint4 x0[STEPS], x1[STEPS], wv[STEPS];
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
@@ -109,12 +150,23 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
   const bf16_t* wb = static_cast<const bf16_t*>(w);
   const bf16_t* bb = static_cast<const bf16_t*>(bias);
   bf16_t* yb = static_cast<bf16_t*>(y);
-  if (k == 768)
-    hipLaunchKernelGGL((gemm_rows_kernel<12>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb, yb,
-                       y_row_stride, static_cast<int>(rows), k);
-  else
-    hipLaunchKernelGGL((gemm_rows_kernel<0>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb, yb,
-                       y_row_stride, static_cast<int>(rows), k);
+  // k = 768 with few column tiles (the maps of a decode step's layers): the x tile staged in LDS; the wide maps (the
+  // tied head) keep the direct loads, with several workgroups per compute unit
+  if (k == kStageK && grid.x * grid.y <= 256) {
+    constexpr int kStageBytes = kGemmRows * kStageRow;   // 99,328
+    static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_rows_kernel<12, true>),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   kStageBytes) == hipSuccess;
+    if (!lds_ok) return set_err(SDM_RT_ELAUNCH, "gemm_rows: cannot enable %d bytes of LDS", kStageBytes);
+    hipLaunchKernelGGL((gemm_rows_kernel<12, true>), grid, dim3(256), kStageBytes, st, xb, x_row_stride, wb,
+                       w_row_stride, bb, yb, y_row_stride, static_cast<int>(rows), k);
+  } else if (k == kStageK) {
+    hipLaunchKernelGGL((gemm_rows_kernel<12, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+                       yb, y_row_stride, static_cast<int>(rows), k);
+  } else {
+    hipLaunchKernelGGL((gemm_rows_kernel<0, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+                       yb, y_row_stride, static_cast<int>(rows), k);
+  }
   return check_launch("gemm_rows");
 }
 

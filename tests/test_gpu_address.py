@@ -114,3 +114,29 @@ def test_64_subkey_addressing_matches_oracle(n_sub, k, H, half, dtype):
     np.testing.assert_allclose(_as_tokens(scores), sv, atol=1e-6)
     w = O.address_weights(sv, p["log_scale"].astype(np.float64))
     np.testing.assert_allclose(_as_tokens(weights)[same], w[same], atol=2e-6, rtol=2e-6)
+
+
+@pytest.mark.parametrize("n_sub,d_a,k,H,addr_bias,dtype", [(32, 64, 8, 12, 0.0, torch.bfloat16),
+                                                           (32, 64, 8, 12, 0.0, torch.float32),
+                                                           (64, 32, 16, 1, 0.0, torch.bfloat16),
+                                                           (64, 32, 16, 1, 0.0, torch.float32),
+                                                           (20, 32, 12, 3, 0.4, torch.bfloat16),
+                                                           (48, 16, 8, 2, 0.4, torch.float32)])
+def test_few_token_split_path_equals_wave_path(n_sub, d_a, k, H, addr_bias, dtype):
+    """Up to 1,024 tokens the addressing splits every address over the block's waves (one per half and sub-key tile,
+    then a wave for the grid: a decode step's path); beyond, one wave addresses 64 tokens.  The same tokens give the
+    same picks, weights and scores, bit for bit, on both paths (32 and 64 sub-keys per half, full and masked grids,
+    gate and address bias), and the picks agree with the oracle."""
+    from tests._gpu_util import core_inputs
+    kz, _, _, g, p = core_inputs(1, 1100, H, 8, d_a, n_sub, seed=231 + n_sub, addr_bias=addr_bias)
+    if dtype == torch.bfloat16:
+        kz, g = bf16_round(kz), bf16_round(g)
+    say("split vs wave addressing", n_sub, d_a, k, H, dtype)
+    s_all, v_all, w_all = gpu_address(kz, p, k, dtype=dtype, gate=g)                           # 1,100: wave path
+    s_few, v_few, w_few = gpu_address(kz[:, :500], p, k, dtype=dtype, gate=g[:, :500])         # 500: split path
+    assert np.array_equal(s_few, s_all[:, :, :500])
+    assert np.array_equal(w_few, w_all[:, :, :500]) and np.array_equal(v_few, v_all[:, :, :500])
+    zz = kz[:, :500].astype(np.float64).reshape(500, H, d_a) + p["addr_b"]
+    _, osi = O.pk_address(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), k)
+    n = int(pick_diffs(zz, p["keys1"].astype(np.float64), p["keys2"].astype(np.float64), osi, _as_tokens(s_few)).sum())
+    say(f"  {n} of {500 * H} addresses differ from the oracle (ties)")
