@@ -63,6 +63,7 @@ struct VPiece<float> {
 };
 
 constexpr int kPickThreads = 512;    // 64 positions x 8 picks
+constexpr int kTeamWriters = 12;     // a wave with a slot of this many later writers in a chunk writes in teams
 
 template <typename VT, typename OutT>
 __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
@@ -303,12 +304,17 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
       const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
-      auto over = [&](auto st) {
-        for (int jj = 8 + j; jj < n_in; jj += 8) {
-          const uint2 e = ent_at(e0 + jj - 8, st);
-          const float ce = __uint_as_float(e.x);
-          add_vrow(ce, static_cast<int>(e.y & 63u), acc);
-          dl += ce;
+      auto over = [&](auto st) {   // contributions 8 + j, 16 + j, ... (at most 7: n_in < 64), entries loaded first
+        uint2 ev[7];
+#pragma unroll
+        for (int t = 0; t < 7; ++t) ev[t] = 8 + j + 8 * t < n_in ? ent_at(e0 + j + 8 * t, st) : make_uint2(0u, 0u);
+#pragma unroll
+        for (int t = 0; t < 7; ++t) {
+          if (8 + j + 8 * t < n_in) {
+            const float ce = __uint_as_float(ev[t].x);
+            add_vrow(ce, static_cast<int>(ev[t].y & 63u), acc);
+            dl += ce;
+          }
         }
       };
       if (all_staged) over(std::true_type{});
@@ -426,35 +432,110 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     // ---- write: the owner lanes add their faded values and those of the slot's later writers ----
     const float inv_mu = fast_rcp(mu_new);
+    // every owner adds its own faded value to its loaded row
+    float cw = cw_old;
     if (wslot != M) {
-      const int n_l = static_cast<int>((wr.x >> 17) & 63u);
-      unsigned char* row = A_w + wslot * (CW * 4);
       const float a0 = __uint_as_float(wr.y) * inv_mu;
-      float cw = cw_old + a0;
 #pragma unroll
       for (int k = 0; k < 32; ++k) y[k] = fmaf(a0, vp[k], y[k]);
-      if (n_l > 0) {
-        const float a1 = __uint_as_float(wr.z) * inv_mu;
-        add_vrow(a1, static_cast<int>((wr.x >> 11) & 63u), y);
-        cw += a1;
-        if (n_l > 1) {   // later writers past the first, from the variable part
-          const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
-          auto later = [&](auto st) {
-            for (int e = 0; e < n_l - 1; ++e) {
-              const uint2 en = ent_at(w_e0 + e, st);
-              const float ae = __uint_as_float(en.x) * inv_mu;
-              add_vrow(ae, static_cast<int>(en.y & 63u), y);
-              cw += ae;
-            }
-          };
-          if (all_staged) later(std::true_type{});
-          else later(std::false_type{});
+      cw += a0;
+    }
+    const int n_l_own = wslot != M ? static_cast<int>((wr.x >> 17) & 63u) : 0;
+    if (!__ballot(n_l_own >= kTeamWriters)) {
+      if (wslot != M) {   // the owner adds the slot's later writers and stores the row
+        const int n_l = n_l_own;
+        unsigned char* row = A_w + wslot * (CW * 4);
+        if (n_l > 0) {
+          const float a1 = __uint_as_float(wr.z) * inv_mu;
+          add_vrow(a1, static_cast<int>((wr.x >> 11) & 63u), y);
+          cw += a1;
+          if (n_l > 1) {   // later writers past the first, from the variable part
+            const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
+            auto later = [&](auto st) {
+              for (int e = 0; e < n_l - 1; ++e) {
+                const uint2 en = ent_at(w_e0 + e, st);
+                const float ae = __uint_as_float(en.x) * inv_mu;
+                add_vrow(ae, static_cast<int>(en.y & 63u), y);
+                cw += ae;
+              }
+            };
+            if (all_staged) later(std::true_type{});
+            else later(std::false_type{});
+          }
         }
-      }
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
-      cnt[wslot] = cw;
+        for (int k = 0; k < 8; ++k)
+          *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+        cnt[wslot] = cw;
+      }
+    } else {
+      // A wave with a slot of many later writers (crowded addresses) writes as eight teams: team j, the lanes of
+      // pick j of the wave's eight positions, takes the owned slots of its members one after another; the member's
+      // row (its own value added) and the slot's later writers (every eighth, from the member's index in the team)
+      // are summed per lane, then over the team (lanes 8 apart) by a fixed butterfly that leaves each lane one
+      // four-column piece of the row, which it stores.
+      const unsigned long long owners = __ballot(wslot != M);
+      const int mi = lane >> 3;   // the lane's member index in its team
+      auto team = [&](auto st) {
+        for (int k = 0; k < 8; ++k) {
+          if (!((owners >> (8 * k)) & 0xffull)) continue;   // no owner among the teams' members k
+          const int src = 8 * k + j;
+          const uint32_t mx = static_cast<uint32_t>(__shfl(static_cast<int>(wr.x), src));
+          const uint32_t mz = static_cast<uint32_t>(__shfl(static_cast<int>(wr.z), src));
+          const int mslot = static_cast<int>(mx & 0x7ffu);
+          float part[32];
+          float cwp = 0.f;
+          const bool self = mi == k && mslot != M;   // the member itself: its row with its own value added
+#pragma unroll
+          for (int q = 0; q < 32; ++q) part[q] = self ? y[q] : 0.f;
+          if (self) cwp = cw;
+          if (mslot != M) {   // later writers mi, mi + 8, ...: 0 is the inline one, i > 0 entry w_e0 + i - 1
+            const int n_l = static_cast<int>((mx >> 17) & 63u);
+            const int w_e0 = static_cast<int>(mx >> 23);
+            for (int i = mi; i < n_l; i += 8) {
+              const uint2 it = i == 0 ? make_uint2(mz, (mx >> 11) & 63u) : ent_at(w_e0 + i - 1, st);
+              const float ae = __uint_as_float(it.x) * inv_mu;
+              add_vrow(ae, static_cast<int>(it.y & 63u), part);
+              cwp += ae;
+            }
+          }
+          // over the team: lanes 32 apart (32 -> 16 values), 16 apart (-> 8), 8 apart (-> 4)
+          float h16[16];
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[q]), __float_as_uint(part[16 + q]),
+                                                             false, false);
+            h16[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);   // lane < 32: values q, else 16 + q
+          }
+          const bool b4 = lane & 16, b3 = lane & 8;
+          float h8[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float keep = b4 ? h16[8 + q] : h16[q];
+            h8[q] = keep + __shfl_xor(b4 ? h16[q] : h16[8 + q], 16);
+          }
+          float h4[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float keep = b3 ? h8[4 + q] : h8[q];
+            h4[q] = keep + __int_as_float(__builtin_amdgcn_update_dpp(
+                               0, __float_as_int(b3 ? h8[q] : h8[4 + q]), 0x128, 0xf, 0xf, false));   // row_ror:8
+          }
+          float ct = cwp;
+          ct += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ct), 0x128, 0xf, 0xf, false));
+          ct += __shfl_xor(ct, 16);
+          {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
+            ct = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+          }
+          if (mslot != M) {   // the lane's piece: number mi of the read order
+            const int piece = j ^ (mi < 4 ? mi : 11 - mi);
+            *reinterpret_cast<float4*>(A_w + mslot * (CW * 4) + 16 * piece) = make_float4(h4[0], h4[1], h4[2], h4[3]);
+            if (mi == k) cnt[mslot] = ct;
+          }
+        }
+      };
+      team(std::false_type{});   // rare: one instance, the entries staged or not
     }
     mu = mu_new;
     rr = rr_n;

@@ -205,6 +205,58 @@ def test_bench_shape_crowded_bf16():
     assert int(sizes.max()) > 4096
 
 
+def _repeat(a, pattern):
+    """Positions that repeat tokens: 'same' one token per batch row, 'cycle3' three tokens in turn, 'alternate' one
+    token at the even positions and fresh ones at the odd."""
+    out = a.copy()
+    T = a.shape[1]
+    if pattern == "same":
+        out[:] = a[:, :1]
+    elif pattern == "cycle3":
+        out[:] = a[:, np.arange(T) % 3]
+    else:
+        out[:, 0::2] = a[:, :1]
+    return out
+
+
+@pytest.mark.parametrize("pattern", ["same", "cycle3", "alternate"])
+def test_repeated_tokens_crowd_every_chunk(pattern):
+    """Addresses of repeated tokens, the scan's slowest input: the first positions of every chunk own slots with up
+    to 63 later writers (waves with such a slot write in teams of eight lanes, which also take the wave's other
+    owned slots: 'alternate' mixes them with fresh tokens' slots), and positions have up to 63 in-chunk read
+    contributions.  With resets, fades 0 ... 1 and a fade that rescales the slab every chunk: read-out and final
+    state against the fp64 recurrence on the kernel's picks."""
+    from oracle import sdm_fp64 as O
+    B, T, H, dh, n_sub = 3, 200, 4, 64, 8
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 16, n_sub, seed=301, decays=(0.0, 0.3, 0.97, 1.0))
+    kz, qz, g = _repeat(kz, pattern), _repeat(qz, pattern), _repeat(g, pattern)
+    reset = np.zeros((B, T), bool)
+    reset[1, [5, 64, 100]] = True
+    reset[2, [63, 130, 131]] = True
+    r, (mem, cnt) = gpu_core(kz, qz, V, g, p, 8, want_state=True, reset=reset)
+    siw, _, ww = gpu_address(kz, p, 8, gate=g)
+    sir, _, wr = gpu_address(qz, p, 8)
+    Vb = V.astype(np.float64).reshape(B, T, H, dh).transpose(0, 2, 1, 3)
+    num, den, m64, c64 = O.scan_recurrence(siw.astype(np.int64), ww.astype(np.float64), sir.astype(np.int64),
+                                           wr.astype(np.float64), Vb, p["decay"].astype(np.float64),
+                                           (np.zeros((B, H, n_sub ** 2, dh)), np.zeros((B, H, n_sub ** 2))),
+                                           reset=reset)
+    r64 = O.finish(num, den, "mean", 1e-3, True, p["onorm_w"].astype(np.float64), 1e-2)
+    assert_close(r, r64.transpose(0, 2, 1, 3).reshape(B, T, H * dh), 1e-5, msg=f"read-out, {pattern} tokens")
+    np.testing.assert_allclose(mem, m64, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
+
+
+def test_bench_shape_one_repeated_token_bf16():
+    """The bench shape with one repeated token per batch row (every chunk: 8 slots of 63 later writers, positions of
+    up to 63 in-chunk contributions, variable parts past the staged 4 KB), bf16: every pick against the oracle and
+    every slab's read-out against the fp64 recurrence on the kernel's picks."""
+    kz, qz, V, g, p = core_inputs(8, 2048, 12, 64, 64, 32, seed=303)
+    kz, qz, g = (_repeat(a, "same") for a in (kz, qz, g))
+    kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    check_core(kz, qz, V, g, p, 8, dtype=torch.bfloat16, tol=2e-3, rescaled=True)
+
+
 def test_long_sequence_32k_positions_bf16():
     """T = 32,768 positions in one call (512 chunks per slab: the scan's table of plan sizes near the end of its LDS),
     one batch row, 12 heads, bf16: every pick against the oracle and the read-out of every slab against the fp64
