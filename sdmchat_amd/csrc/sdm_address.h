@@ -59,20 +59,23 @@ __global__ void __launch_bounds__(64) address_kernel(AddrArgs a) {
 }
 
 
-// sdm_rt_address for few tokens (a decode step): the addressing of one address is the longest dependent chain of
-// a step, so it is split over the waves of a block.  Block (64-address tile, head, set), 64 * NW threads, NW = 2 *
-// NS / 32: wave q scores half q / (NS / 32) against sub-key tile q % (NS / 32) on the matrix cores and selects its
-// CAP best keys (tile_best); wave 0 then merges each half's tiles, ranks the halves and picks from the grid
-// (grid_pick).  The keys are those of address_wave, so the picks are the same.
+// sdm_rt_address for few tokens (a decode step), where one wave per 64 addresses leaves the GPU idle and the
+// selection of an address is the longest chain: block (4 addresses, head, set), 4 waves.  Wave q < 2 NS / 32 scores
+// half q / (NS / 32) of the block's addresses against sub-key tile q % (NS / 32) on the matrix cores (half_scores, the
+// scoring of address_wave); through LDS, wave j then selects address j across its lanes (select_lanes: the same keys,
+// so the same picks, order, weights and scores as address_wave) and its lanes p < pitch store pick p.
 template <int HALF, int CAP, typename InT, int MODE>
-__global__ void __launch_bounds__(256) address_split_kernel(AddrArgs a) {
+__global__ void __launch_bounds__(256) address_lanes_kernel(AddrArgs a) {
   constexpr int NS = MODE >= 3 ? 64 : 32;
   constexpr int NT = NS / 32;          // sub-key tiles per half
   constexpr bool FULL = MODE == 2 || MODE == 4;
-  __shared__ double best_l[2 * NT][CAP][64];
+  constexpr int kGroup = 4;
+  __shared__ float s_sc[kGroup][2][NS];   // [address][half][sub-key] raw scores
+  __shared__ float s_inv[kGroup][2];
   const int h = blockIdx.y;
   const int64_t N = static_cast<int64_t>(a.B) * a.T;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kGroup;
+  const int nb = static_cast<int>(min<int64_t>(kGroup, N - n0));
   const int lane = threadIdx.x & 63;
   const int q = threadIdx.x >> 6;
   if (blockIdx.z == 1) {   // the second address set
@@ -83,53 +86,40 @@ __global__ void __launch_bounds__(256) address_split_kernel(AddrArgs a) {
     a.w_out = a.w_out2;
     a.s_out = a.s_out2;
   }
-  const int rows = static_cast<int>(min<int64_t>(64, N - n0));
-  const InT* z0 = static_cast<const InT*>(a.z) + n0 * a.z_stride;
-  {
-    double best[CAP];
-    tile_best<HALF, CAP, InT, FULL, NS>(a.g, h, z0, a.z_stride, rows, q / NT, q % NT, false, best);
+  if (q < 2 * NT) {
+    const int hf = q / NT, tile = q % NT;
+    const InT* z0 = static_cast<const InT*>(a.z) + n0 * a.z_stride;
+    floatx16 acc[2];
+    float inv[2];
+    if constexpr (sizeof(InT) == 2) half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, a.z_stride, nb, acc, inv, 32 * tile);
+    else half_scores_f32<HALF, InT, FULL>(a.g, h, hf, z0, a.z_stride, nb, acc, inv, 32 * tile);
+    // lane l: address l % 32 of tile 0, sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
+    const int row = lane & 31;
+    if (row < nb) {
 #pragma unroll
-    for (int r = 0; r < CAP; ++r) best_l[q][r][lane] = best[r];
+      for (int r = 0; r < 16; ++r) s_sc[row][hf][32 * tile + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3)] = acc[0][r];
+      if (lane < 32 && tile == 0) s_inv[row][hf] = inv[0];
+    }
   }
   __syncthreads();
-  if (q != 0) return;
-  const int64_t n = n0 + lane;
-  double hk[2][CAP];
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    double best[CAP];
-#pragma unroll
-    for (int r = 0; r < CAP; ++r) best[r] = best_l[hf * NT][r][lane];
-#pragma unroll
-    for (int t = 1; t < NT; ++t) {
-      double other[CAP];
-#pragma unroll
-      for (int r = 0; r < CAP; ++r) other[r] = best_l[hf * NT + t][r][lane];
-      merge_top_desc<CAP>(best, other);
-    }
-    rank_half<CAP, NS>(hf, best, hk[hf]);
-  }
-  const float gate =
-      (a.gl && n < N) ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
-  int slot[CAP];
-  float w[CAP], sc[CAP];
-  grid_pick<CAP, FULL, NS>(a.g, h, hk[0], hk[1], gate, slot, w, sc);
-  if (n >= N) return;
+  if (q >= nb) return;
+  const int64_t n = n0 + q;
+  const float gate = a.gl ? gate_of(static_cast<const InT*>(a.gl) + n * a.g_stride, h, a.g.gate_bias) : 1.f;
+  int slot;
+  float w, sc;
+  select_lanes<CAP, FULL, NS>(a.g, a.g.log_scale[h], &s_sc[q][0][0], &s_inv[q][0], gate, slot, w, sc);
   const int b = static_cast<int>(n / a.T);
   const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
   const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
-#pragma unroll
-  for (int p = 0; p < CAP; ++p) {
-    if (p < a.pitch) {
-      const bool live = p < a.g.kk;
-      a.slot_out[base + p] = live ? slot[p] : -1;
-      if (a.w_out) a.w_out[base + p] = w[p];
-      if (a.s_out) a.s_out[base + p] = sc[p];
-    }
+  if (lane < CAP && lane < a.pitch) {
+    const bool live = lane < a.g.kk;
+    a.slot_out[base + lane] = live ? slot : -1;
+    if (a.w_out) a.w_out[base + lane] = w;
+    if (a.s_out) a.s_out[base + lane] = sc;
   }
 }
 
-// token counts up to this take address_split_kernel (the wave-per-tile split pays when few blocks fill the GPU)
+// token counts up to this take address_lanes_kernel (a block per 4 addresses pays when few blocks fill the GPU)
 constexpr int64_t kSplitAddressTokens = 1024;
 
 template <int HALF, typename InT>
@@ -139,9 +129,9 @@ struct AddressLaunch {
     const int64_t N = static_cast<int64_t>(p.B) * p.T;
     dim3 grid(static_cast<unsigned>((N + 63) / 64), p.H, a.z2 ? 2 : 1);
     if constexpr (MODE > 0) {
-      if (N <= kSplitAddressTokens) {   // few tokens: every address's selection split over the block's waves
-        constexpr int NW = 2 * (MODE >= 3 ? 2 : 1);
-        hipLaunchKernelGGL((address_split_kernel<HALF, CAP, InT, MODE>), grid, dim3(64 * NW), 0, st, a);
+      if (N <= kSplitAddressTokens) {   // few tokens: a block per 4 addresses, each selected across a wave
+        hipLaunchKernelGGL((address_lanes_kernel<HALF, CAP, InT, MODE>), dim3(static_cast<unsigned>((N + 3) / 4), p.H,
+                           a.z2 ? 2 : 1), dim3(256), 0, st, a);
         return;
       }
     }

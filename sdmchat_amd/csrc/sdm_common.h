@@ -801,6 +801,124 @@ __device__ __forceinline__ void address_wave(const AddrGeom& g, int h, const InT
   grid_pick<CAP, FULL, NS>(g, h, hk[0], hk[1], gate, slot, w, score);
 }
 
+// the value of lane (lane ^ j) of the wave (j < 64 a power of two): DPP within rows of 16 lanes (quad_perm for 1
+// and 2, row_shl/row_shr by 4, row_ror by 8), lane permutes across rows
+__device__ __forceinline__ int xor_lanes32(int v, int j, int lane) {
+  if (j == 1) return __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);    // quad_perm [1,0,3,2]
+  if (j == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);    // quad_perm [2,3,0,1]
+  if (j == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);   // row_ror:8
+  if (j == 4) {   // lanes with bit 2 clear read lane + 4 (row_shl:4), the others lane - 4 (row_shr:4)
+    const int u = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xf, 0xf, false);
+    const int d = __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false);
+    return (lane & 4) ? d : u;
+  }
+  return __shfl_xor(v, j);
+}
+
+// Descending bitonic sort of one selection key per lane over aligned groups of N lanes (N a power of two <= 64):
+// lane i of a group ends with the group's i-th largest key.  The keys are non-negative doubles (their order is the
+// unsigned order of their bits) and are compared as 64-bit integers.  Every lane of the wave takes part.
+template <int N>
+__device__ __forceinline__ unsigned long long sort_lanes_desc(unsigned long long x, int lane) {
+  const int idx = lane & (N - 1);
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int ylo = xor_lanes32(static_cast<int>(x), j, lane);
+      const int yhi = xor_lanes32(static_cast<int>(x >> 32), j, lane);
+      const unsigned long long y = (static_cast<unsigned long long>(static_cast<uint32_t>(yhi)) << 32) |
+                                   static_cast<uint32_t>(ylo);
+      const bool keep_max = ((idx & j) == 0) == ((idx & k) == 0);
+      x = ((x > y) == keep_max) ? x : y;
+    }
+  }
+  return x;
+}
+
+// The picks of one address by a whole wave: address_wave's selection (the same keys, so the same picks, order,
+// weights and scores) with the candidates spread over the lanes instead of sorted per lane.  sc: the NS raw sub-key
+// scores of each half ([2][NS], as half_scores leaves them: score * inv = cosine), inv: the two halves' factors.
+// NS = 32: lanes 32 hf + i key sub-key i of half hf and each half sorts across its 32 lanes; NS = 64: lane i keys
+// sub-key i of each half in turn, each sorted across the wave.  Lane x < n_pairs(CAP) then keys grid pair x of the
+// dominance-pruned grid (address_one) and the 64 lanes sort.  Lane p < CAP returns pick p.
+template <int CAP, bool FULL, int NS = 32>
+__device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale, const float* sc, const float* inv,
+                                             float gate, int& slot, float& w, float& score) {
+  static_assert(NS == 32 || NS == 64, "32 or 64 sub-keys per half");
+  const int lane = threadIdx.x & 63;
+  using KL = KeyLayout<NS>;
+  auto sort64 = [&](double v, auto n) {
+    return __longlong_as_double(static_cast<long long>(
+        sort_lanes_desc<decltype(n)::value>(static_cast<unsigned long long>(__double_as_longlong(v)), lane)));
+  };
+  double hk0, hk1;   // lane r < 16: the rank-r key of half 0 and of half 1, ranked
+  if constexpr (NS == 32) {
+    const int hf = lane >> 5, i = lane & 31;
+    double c = hf == 0 ? half_key<KL::FS1>(sc[i], static_cast<double>(inv[0]), i)
+                       : half_key<KL::FS2>(sc[32 + i], static_cast<double>(inv[1]), i);
+    if (!FULL && i >= g.n_sub) c = key_invalid(c);   // sub-keys past n_sub are never picked
+    c = sort64(c, std::integral_constant<int, 32>{});
+    const double hk = i < 16 ? key_or(c, static_cast<uint32_t>(15 - i) << (hf == 0 ? KL::RS1 : KL::RS2)) : c;
+    hk0 = hk;
+    hk1 = __shfl(hk, (lane & 31) + 32);
+  } else {
+    double c0 = half_key<KL::FS1, NS>(sc[lane], static_cast<double>(inv[0]), lane);
+    double c1 = half_key<KL::FS2, NS>(sc[NS + lane], static_cast<double>(inv[1]), lane);
+    if (!FULL && lane >= g.n_sub) {
+      c0 = key_invalid(c0);
+      c1 = key_invalid(c1);
+    }
+    c0 = sort64(c0, std::integral_constant<int, 64>{});
+    c1 = sort64(c1, std::integral_constant<int, 64>{});
+    hk0 = lane < 16 ? key_or(c0, static_cast<uint32_t>(15 - lane) << KL::RS1) : c0;
+    hk1 = lane < 16 ? key_or(c1, static_cast<uint32_t>(15 - lane) << KL::RS2) : c1;
+  }
+  // grid pair of this lane: pairs (ra, rb) with (ra + 1)(rb + 1) <= CAP, row by row
+  int x = lane, ra = -1, rb = 0;
+#pragma unroll
+  for (int a = 0; a < CAP; ++a) {
+    const int n_a = CAP / (a + 1);
+    if (ra < 0) {
+      if (x < n_a) {
+        ra = a;
+        rb = x;
+      } else {
+        x -= n_a;
+      }
+    }
+  }
+  const double k0 = __shfl(hk0, max(ra, 0));
+  const double k1 = __shfl(hk1, rb);
+  double k = k0 + k1;
+  if (ra < 0) k = 0.0;   // no candidate: below every key
+  else if (!FULL && !(ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk)) k = key_invalid(k);
+  // the candidates sit in lanes < n_pairs(CAP)
+  k = sort64(k, std::integral_constant<int, (n_pairs(CAP) <= 32 ? 32 : 64)>{});
+  const float cv = grid_score<NS>(k);
+  const uint32_t f = static_cast<uint32_t>(__double_as_longlong(k));
+  int si;
+  if (FULL) {   // (NS - 1 - i1) * NS + (NS - 1 - i2) = NS^2 - 1 - slot
+    si = NS * NS - 1 - static_cast<int>(f & static_cast<uint32_t>(NS * NS - 1));
+  } else {
+    const int i1 = NS - 1 - static_cast<int>((f >> KL::IB) & static_cast<uint32_t>(NS - 1));
+    const int i2 = NS - 1 - static_cast<int>(f & static_cast<uint32_t>(NS - 1));
+    si = min(i1 * g.n_sub + i2, g.n_sub * g.n_sub - 1);
+  }
+  const float scale = expf(log_scale);
+  const float x0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), 0)) * scale;
+  const bool live = lane < CAP && (FULL || lane < g.kk);
+  const float e = live ? expf(cv * scale - x0) : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int p = 0; p < CAP; ++p)   // in pick order, as address_wave sums
+    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
+  const float wscale = gate / sum;
+  slot = live ? si : 0;
+  w = live ? e * wscale : 0.f;
+  score = live ? cv : 0.f;
+}
+
 struct AddrArgs {
   AddrGeom g;
   const void* z;              // address rows

@@ -268,101 +268,6 @@ __global__ void __launch_bounds__(64) decode_kernel(DecodeArgs a) {
   decode_one<VT, KP, C>(a, b, h, threadIdx.x, pre, rsl, rwv, wsl, wwv);
 }
 
-// the value of lane (lane ^ j) of the wave (j < 64 a power of two): DPP within rows of 16 lanes (quad_perm for 1
-// and 2, row_shl/row_shr by 4, row_ror by 8), lane permutes across rows
-__device__ __forceinline__ int xor_lanes32(int v, int j, int lane) {
-  if (j == 1) return __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);    // quad_perm [1,0,3,2]
-  if (j == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);    // quad_perm [2,3,0,1]
-  if (j == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);   // row_ror:8
-  if (j == 4) {   // lanes with bit 2 clear read lane + 4 (row_shl:4), the others lane - 4 (row_shr:4)
-    const int u = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xf, 0xf, false);
-    const int d = __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false);
-    return (lane & 4) ? d : u;
-  }
-  return __shfl_xor(v, j);
-}
-
-// Descending bitonic sort of one selection key per lane over aligned groups of N lanes (N a power of two <= 64):
-// lane i of a group ends with the group's i-th largest key.  The keys are non-negative doubles (their order is the
-// unsigned order of their bits) and are compared as 64-bit integers.  Every lane of the wave takes part.
-template <int N>
-__device__ __forceinline__ unsigned long long sort_lanes_desc(unsigned long long x, int lane) {
-  const int idx = lane & (N - 1);
-#pragma unroll
-  for (int k = 2; k <= N; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const int ylo = xor_lanes32(static_cast<int>(x), j, lane);
-      const int yhi = xor_lanes32(static_cast<int>(x >> 32), j, lane);
-      const unsigned long long y = (static_cast<unsigned long long>(static_cast<uint32_t>(yhi)) << 32) |
-                                   static_cast<uint32_t>(ylo);
-      const bool keep_max = ((idx & j) == 0) == ((idx & k) == 0);
-      x = ((x > y) == keep_max) ? x : y;
-    }
-  }
-  return x;
-}
-
-// The picks of one address by a whole wave: address_wave's selection (the same keys, so the same picks, order and
-// weights) with the candidates spread over the lanes instead of sorted per lane.  sc: the 32 raw sub-key scores of
-// each half ([2][32], as half_scores leaves them: score * inv = cosine), inv: the two halves' factors.  Lanes
-// 32 hf + i key sub-key i of half hf; each half sorts across its 32 lanes; lane x < n_pairs(CAP) then keys grid
-// pair x of the dominance-pruned grid (address_one) and the 64 lanes sort.  Lane p < CAP returns pick p.
-template <int CAP, bool FULL>
-__device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale, const float* sc, const float* inv,
-                                             float gate, int& slot, float& w) {
-  const int lane = threadIdx.x & 63;
-  const int hf = lane >> 5, i = lane & 31;
-  using KL = KeyLayout<32>;
-  double c = hf == 0 ? half_key<KL::FS1>(sc[i], static_cast<double>(inv[0]), i)
-                     : half_key<KL::FS2>(sc[32 + i], static_cast<double>(inv[1]), i);
-  if (!FULL && i >= g.n_sub) c = key_invalid(c);   // sub-keys past n_sub are never picked
-  c = __longlong_as_double(static_cast<long long>(sort_lanes_desc<32>(static_cast<unsigned long long>(__double_as_longlong(c)), lane)));
-  const double hk = i < 16 ? key_or(c, static_cast<uint32_t>(15 - i) << (hf == 0 ? KL::RS1 : KL::RS2)) : c;   // ranked
-  // grid pair of this lane: pairs (ra, rb) with (ra + 1)(rb + 1) <= CAP, row by row
-  int x = lane, ra = -1, rb = 0;
-#pragma unroll
-  for (int a = 0; a < CAP; ++a) {
-    const int n_a = CAP / (a + 1);
-    if (ra < 0) {
-      if (x < n_a) {
-        ra = a;
-        rb = x;
-      } else {
-        x -= n_a;
-      }
-    }
-  }
-  const double k0 = __shfl(hk, max(ra, 0));
-  const double k1 = __shfl(hk, 32 + rb);
-  double k = k0 + k1;
-  if (ra < 0) k = 0.0;   // no candidate: below every key
-  else if (!FULL && !(ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk)) k = key_invalid(k);
-  // the candidates sit in lanes < n_pairs(CAP)
-  k = __longlong_as_double(static_cast<long long>(
-      sort_lanes_desc<(n_pairs(CAP) <= 32 ? 32 : 64)>(static_cast<unsigned long long>(__double_as_longlong(k)), lane)));
-  const float cv = grid_score(k);
-  const uint32_t f = static_cast<uint32_t>(__double_as_longlong(k));
-  int si;
-  if (FULL) {
-    si = 1023 - static_cast<int>(f & 1023u);   // (31 - i1) * 32 + (31 - i2) = 1023 - slot
-  } else {
-    const int i1 = 31 - static_cast<int>((f >> 5) & 31u), i2 = 31 - static_cast<int>(f & 31u);
-    si = min(i1 * g.n_sub + i2, g.n_sub * g.n_sub - 1);
-  }
-  const float scale = expf(log_scale);
-  const float x0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), 0)) * scale;
-  const bool live = lane < CAP && (FULL || lane < g.kk);
-  const float e = live ? expf(cv * scale - x0) : 0.f;
-  float sum = 0.f;
-#pragma unroll
-  for (int p = 0; p < CAP; ++p)   // in pick order, as address_wave sums
-    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
-  const float wscale = gate / sum;
-  slot = live ? si : 0;
-  w = live ? e * wscale : 0.f;
-}
-
 // One launch: block (head, group of 4 streams), 8 waves.  Wave 2 s + hf scores half hf of the group's addresses of
 // set s (0: write keys, 1: read queries) against the head's sub-keys on the matrix cores (half_scores, the forward's
 // scoring); through LDS, wave 4 s + j then selects address j of set s across its lanes (select_lanes), so the picks
@@ -406,8 +311,8 @@ __global__ void __launch_bounds__(512) decode_fused_kernel(DecodeArgs a) {
   if (jg < nb) {
     const float gate = gated ? 1.f / (1.f + expf(-(glog + gbias))) : 1.f;   // gate_of
     int slot;
-    float w;
-    select_lanes<CAP, FULL>(a.g, log_scale, &s_sc[set][jg][0][0], &s_inv[set][jg][0], gate, slot, w);
+    float w, score;
+    select_lanes<CAP, FULL>(a.g, log_scale, &s_sc[set][jg][0][0], &s_inv[set][jg][0], gate, slot, w, score);
     if (lane < CAP) {
       s_slot[set][jg][lane] = slot;
       s_w[set][jg][lane] = w;
