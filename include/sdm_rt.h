@@ -193,6 +193,24 @@ int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float
                       const void* values, sdm_rt_dtype values_dtype,
                       void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype, void* stream);
 
+/* TrainedSdm's read for a few tokens in one launch (a decode step): the query map q = hx Wq^T, the addressing of q
+ * and the weighted read of the picked rows, each as its own entry point computes it (sdm_rt_gemm_rows for the map,
+ * sdm_rt_address, sdm_rt_table_read), so the three calls and this one give the same bits.  No single counterpart in
+ * the reference: it is TrainedSdm.forward's F.linear, pk_address and embedding_bag (track4_onesdm_models.py:438-455)
+ * for at most 256 tokens.  All arrays bfloat16 except the picks.
+ *   hx       [B*T rows] of d (the layer width, a multiple of 64), row stride hx_row_stride
+ *   wq       [H * addr_dim][d] (addr_dim 32 or 64), row stride wq_row_stride
+ *   values   [H][M][head_dim] (head_dim a multiple of 8), rows contiguous
+ *   q_out    [B*T rows] of H * addr_dim, or NULL
+ *   slot_out, score_out, weight_out   [B][H][T][pitch] as sdm_rt_address writes them (score_out, weight_out may be
+ *            NULL)
+ *   out      [B*T rows] of H * head_dim
+ * hx, wq, values and out rows 16-byte aligned; params: keys, addr_b, log_scale (no fade, no gate). */
+int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* hx, int64_t hx_row_stride,
+                      int32_t d, const void* wq, int64_t wq_row_stride, const void* values, void* q_out,
+                      int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
+                      int64_t out_row_stride, void* stream);
+
 /* The input norm of RunTimeSdm (RMSNorm, experiments/track4/sdmllm/track4_sdmllm_models.py:63-71) with the
  * reference's rounding: out = cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), the mean and product in float32,
  * cast_in rounding to the input dtype and cast_out to out_dtype.

@@ -261,6 +261,57 @@ def table_read(slots, weights, values, k, out_dtype=torch.float32, out=None):
     return out
 
 
+TABLE_STEP_MAX = 256   # token counts up to this take sdm_rt_table_step (the query map's sums as sdm_rt_gemm_rows')
+
+
+def table_step_fits(hx, wq, values, d_a):
+    """Whether sdm_rt_table_step serves this TrainedSdm read: bfloat16 inputs, map and tables, at most
+    TABLE_STEP_MAX tokens, d_a 32 or 64, the layer width a multiple of 64, head_dim a multiple of 8, no autograd."""
+    d = hx.shape[-1]
+    rows = hx.numel() // d if d else 0
+    return (hx.is_cuda and hx.dtype == torch.bfloat16 and wq.dtype == torch.bfloat16
+            and values.dtype == torch.bfloat16 and 0 < rows <= TABLE_STEP_MAX and d % 64 == 0 and d_a in (32, 64)
+            and values.shape[-1] % 8 == 0
+            and not (torch.is_grad_enabled() and any(t.requires_grad for t in (hx, wq, values))))
+
+
+def table_step(hx, wq, keys1, keys2, log_scale, values, k, params=None, want_q=False):
+    """TrainedSdm's read for a few tokens in one launch (sdm_rt_table_step): q = hx wq^T, its product-key picks and
+    the weighted read of the picked rows, bit for bit what linear(), address(padded=True) and table_read() give.
+    hx [B, T, d] bf16, wq [H * d_a, d] bf16, values [H, M, dh] bf16.  Returns (r [B, T, H * dh] bf16, slots, scores,
+    weights [B, H, T, pitch], q [B, T, H * d_a] or None)."""
+    lib = _lib.load()
+    B, T, d = hx.shape
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dh = values.shape[-1]
+    dims = make_dims(B, T, H, dh, d_a, n_sub, k, out_norm=False, write_gate=False)
+    x2 = hx.reshape(B * T, d)
+    if not _rows16(x2):
+        x2 = x2.contiguous()
+    wq = wq if _rows16(wq) else wq.contiguous()
+    vals = values.detach().contiguous()
+    dev = hx.device
+    if params is None:
+        params = _params(dev, keys1, keys2, None, log_scale, None, None, None)
+    prm, held = params
+    pitch = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
+    if pitch <= 0:
+        raise _lib.SdmRtError(lib.sdm_rt_last_error().decode() or "invalid dimensions")
+    slots = torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev)
+    scores = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    weights = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    out = torch.empty(B, T, H * dh, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(B, T, H * d_a, dtype=torch.bfloat16, device=dev) if want_q else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_table_step(ctypes.byref(dims), ctypes.byref(prm), _ptr(x2), x2.stride(0), d, _ptr(wq), wq.stride(0),
+                               _ptr(vals), _ptr(q), H * d_a, _ptr(slots), _ptr(scores), _ptr(weights), _ptr(out),
+                               H * dh, ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    del held
+    return out, slots, scores, weights, q
+
+
 class DecodeState:
     """State of B decode streams: the true memory is ``scale * mem`` and the true counts ``scale * cnt``
     (mem [B, H, M, dh], cnt [B, H, M], scale [B, H], float32, on the device).  Keeping the scale apart lets a decode

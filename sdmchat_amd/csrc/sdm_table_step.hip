@@ -1,0 +1,231 @@
+// sdm_table_step.hip -- sdm_rt_table_step: TrainedSdm's read for a few tokens (a decode step) in one launch: the
+// query map q = hx Wq^T, the product-key addressing of q and the weighted read of the picked table rows
+// (TrainedSdm.forward, experiments/track4/sdmllm/track4_onesdm_models.py:438-455: F.linear, pk_address :134-148 with
+// the softmax weights, embedding_bag).  Each stage is computed as its own entry point computes it (the query map as
+// sdm_rt_gemm_rows sums it, the addressing as sdm_rt_address, the read as sdm_rt_table_read), so the three calls and
+// this one give the same bits; between the stages the data stay in LDS and registers.
+#include "sdm_common.h"
+
+namespace sdmrt {
+
+struct TableStepArgs {
+  AddrGeom g;
+  const bf16_t* hx;        // [N][d] normed inputs
+  int64_t hx_stride;
+  int d;
+  const bf16_t* wq;        // [H * d_a][d]
+  int64_t wq_stride;
+  const bf16_t* values;    // [H][M][dh]
+  int M, dh, pitch, B, T;
+  bf16_t* q_out;           // [N][H * d_a] or nullptr
+  int64_t q_stride;
+  int32_t* slot_out;       // [B][H][T][pitch]
+  float* w_out;            // same layout or nullptr
+  float* s_out;            // same layout or nullptr
+  bf16_t* r_out;           // [N][H * dh]
+  int64_t r_stride;
+};
+
+constexpr int kStepGroup = 4;          // tokens per block
+constexpr int kTableStepTokens = 256;  // at most this many tokens (sdm_rt_gemm_rows' row range, whose sums it repeats)
+
+// Block (4 tokens, head), 4 waves.
+//  1. the head's d_a query columns of the block's rows: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
+//     with the operand layout of gemm_rows_kernel (rows 0..3 of a 32-row tile: accumulator registers 0..3 of lanes
+//     0..31), the four partial sums are added in wave order and rounded to bfloat16 once;
+//  2. wave q < 2 NS / 32 scores half q / (NS / 32) of the block's queries against sub-key tile q % (NS / 32)
+//     (half_scores, reading the queries from LDS), and wave j selects token j across its lanes (select_lanes);
+//  3. wave j reads its token's picked rows, 16 bytes of a row per lane, and sums them in pick order over the pitch
+//     (pads: slot 0, weight 0) in float32, as the table read does.
+template <int HALF, int CAP, int MODE>
+__global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
+  constexpr int NS = MODE >= 3 ? 64 : 32;
+  constexpr int NT = NS / 32;
+  constexpr bool FULL = MODE == 2 || MODE == 4;
+  constexpr int DA = 2 * HALF;   // query columns of a head
+  constexpr int NCT = DA / 32;   // 32-column tiles of the query map per head
+  static_assert(DA % 32 == 0, "the query map runs on 32-column tiles");
+  __shared__ float s_part[4][NCT][kStepGroup][32];   // [wave][column tile][row][column]
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[kStepGroup][DA];
+  __shared__ float s_sc[kStepGroup][2][NS];
+  __shared__ float s_inv[kStepGroup][2];
+  const int h = blockIdx.y;
+  const int64_t N = static_cast<int64_t>(a.B) * a.T;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStepGroup;
+  const int nb = static_cast<int>(min<int64_t>(kStepGroup, N - n0));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  {
+    const int kq = a.d / 4;
+    const int kb = wave * kq + 8 * (lane >> 5);
+    const int r = lane & 31;
+    const bf16_t* xr = a.hx + (n0 + min(r, nb - 1)) * a.hx_stride + kb;   // rows past the block: clamped, unused
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + r) * a.wq_stride + kb;
+      floatx16 acc = {};
+      for (int s = 0; s < kq / 16; ++s) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + 16 * s);
+        const uint4 wv = *reinterpret_cast<const uint4*>(wr + 16 * s);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv), __builtin_bit_cast(bf16x8, wv),
+                                                      acc, 0, 0, 0);
+      }
+      if (lane < 32) {
+#pragma unroll
+        for (int i = 0; i < kStepGroup; ++i) s_part[wave][ct][i][lane] = acc[i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < kStepGroup * DA; t += 256) {
+    const int i = t / DA, c = t - i * DA;
+    const int ct = c >> 5, cl = c & 31;
+    float v = s_part[0][ct][i][cl];
+    v += s_part[1][ct][i][cl];
+    v += s_part[2][ct][i][cl];
+    v += s_part[3][ct][i][cl];
+    const uint16_t bits = static_cast<uint16_t>(pack_bf16(v + 0.f, 0.f));   // as gemm_rows adds a zero bias
+    s_q[i][c] = bits;
+    if (a.q_out && i < nb) reinterpret_cast<uint16_t*>(a.q_out)[(n0 + i) * a.q_stride + h * DA + c] = bits;
+  }
+  __syncthreads();
+  if (wave < 2 * NT) {
+    const int hf = wave / NT, tile = wave % NT;
+    // half_scores reads row r of head h at z0 + r * DA + h * DA: the LDS rows hold head h's columns only
+    const bf16_t* z0 = reinterpret_cast<const bf16_t*>(&s_q[0][0]) - h * DA;
+    floatx16 acc[2];
+    float inv[2];
+    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile);
+    // lane l: token l % 32 of tile 0, sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
+    const int row = lane & 31;
+    if (row < nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_sc[row][hf][32 * tile + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3)] = acc[0][r];
+      if (lane < 32 && tile == 0) s_inv[row][hf] = inv[0];
+    }
+  }
+  __syncthreads();
+  if (wave >= nb) return;
+  const int64_t n = n0 + wave;
+  int slot;
+  float w, sc;
+  select_lanes<CAP, FULL, NS>(a.g, a.g.log_scale[h], &s_sc[wave][0][0], &s_inv[wave][0], 1.f, slot, w, sc);
+  const int b = static_cast<int>(n / a.T);
+  const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
+  const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
+  if (lane < CAP && lane < a.pitch) {
+    const bool live = lane < a.g.kk;
+    a.slot_out[base + lane] = live ? slot : -1;
+    if (a.w_out) a.w_out[base + lane] = w;
+    if (a.s_out) a.s_out[base + lane] = sc;
+  }
+  const bf16_t* tab = a.values + static_cast<int64_t>(h) * a.M * a.dh;
+  for (int c0 = 8 * lane; c0 < a.dh; c0 += 512) {
+    uint4 raw[CAP];
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      const int sj = __builtin_amdgcn_readlane(slot, j);   // lanes past kk: slot 0 (weight 0)
+      raw[j] = j < a.pitch ? *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(sj) * a.dh + c0)
+                           : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      if (j < a.pitch) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+        const uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = fmaf(wj, __uint_as_float(wd[q] << 16), acc[2 * q]);
+          acc[2 * q + 1] = fmaf(wj, __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
+        }
+      }
+    }
+    store_vals<8, bf16_t>(a.r_out + n * a.r_stride + static_cast<int64_t>(h) * a.dh + c0, acc);
+  }
+}
+
+template <int HALF>
+struct TableStepLaunch {
+  template <int CAP, int MODE>
+  static int go(const Plan& p, const TableStepArgs& a, hipStream_t st) {
+    const int64_t N = static_cast<int64_t>(p.B) * p.T;
+    hipLaunchKernelGGL((table_step_kernel<HALF, CAP, MODE>), dim3(static_cast<unsigned>((N + kStepGroup - 1) / kStepGroup), p.H),
+                       dim3(256), 0, st, a);
+    return check_launch("table_step");
+  }
+  // the addressing mode of sdm_rt_address for this shape (AddressLaunch::run)
+  static int run(const Plan& p, const TableStepArgs& a, hipStream_t st) {
+    if (use_mf(p)) {
+      if (full_grid(p)) return go<8, 2>(p, a, st);
+      return p.cap == 8 ? go<8, 1>(p, a, st) : go<16, 1>(p, a, st);
+    }
+    if (use_mf64(p)) {
+      const bool full = p.n_sub == 64 && p.c1 == p.cap && p.kk == p.cap;
+      if (p.cap == 8) return full ? go<8, 4>(p, a, st) : go<8, 3>(p, a, st);
+      return full ? go<16, 4>(p, a, st) : go<16, 3>(p, a, st);
+    }
+    return set_err(SDM_RT_EUNSUPPORTED, "table_step: n_sub = %d: at most 64 sub-keys per half", p.n_sub);
+  }
+};
+
+}  // namespace sdmrt
+
+using namespace sdmrt;
+
+extern "C" {
+
+int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* hx, int64_t hx_row_stride,
+                      int32_t d, const void* wq, int64_t wq_row_stride, const void* values, void* q_out,
+                      int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
+                      int64_t out_row_stride, void* stream) {
+  g_err[0] = 0;
+  Plan p;
+  int rc = make_plan(dims, &p, false);
+  if (rc) return rc;
+  if ((rc = check_params(params, false, false))) return rc;
+  const int64_t N = static_cast<int64_t>(p.B) * p.T;
+  if (N == 0) return SDM_RT_OK;
+  if (N > kTableStepTokens)
+    return set_err(SDM_RT_EUNSUPPORTED, "table_step: %lld tokens, at most %d", (long long)N, kTableStepTokens);
+  if (d <= 0 || d % 64 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: d = %d must be a positive multiple of 64", d);
+  if (p.d_a % 32 != 0 || p.d_a > 64)
+    return set_err(SDM_RT_EUNSUPPORTED, "table_step: addr_dim = %d must be 32 or 64", p.d_a);
+  if (p.dh % 8 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: head_dim = %d must be a multiple of 8", p.dh);
+  if (p.pitch != p.cap) return set_err(SDM_RT_EUNSUPPORTED, "table_step: pick pitch %d", p.pitch);
+  if (!hx || !wq || !values || !slot_out || !out)
+    return set_err(SDM_RT_EINVAL, "hx, wq, values, slot_out and out must not be NULL");
+  if (hx_row_stride < d || wq_row_stride < d || out_row_stride < static_cast<int64_t>(p.H) * p.dh ||
+      (q_out && q_row_stride < static_cast<int64_t>(p.H) * p.d_a))
+    return set_err(SDM_RT_EINVAL, "table_step: a row stride is smaller than its row");
+  auto al16 = [](const void* ptr, int64_t stride) {
+    return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && (stride * 2) % 16 == 0;
+  };
+  if (!al16(hx, hx_row_stride) || !al16(wq, wq_row_stride) || !al16(values, p.dh) || !al16(out, out_row_stride))
+    return set_err(SDM_RT_EINVAL, "table_step: hx, wq, values and out rows must be 16-byte aligned");
+  TableStepArgs a{};
+  a.g = addr_geom(p, params);
+  a.hx = static_cast<const bf16_t*>(hx);
+  a.hx_stride = hx_row_stride;
+  a.d = d;
+  a.wq = static_cast<const bf16_t*>(wq);
+  a.wq_stride = wq_row_stride;
+  a.values = static_cast<const bf16_t*>(values);
+  a.M = p.M;
+  a.dh = p.dh;
+  a.pitch = p.pitch;
+  a.B = p.B;
+  a.T = p.T;
+  a.q_out = static_cast<bf16_t*>(q_out);
+  a.q_stride = q_row_stride;
+  a.slot_out = slot_out;
+  a.w_out = weight_out;
+  a.s_out = score_out;
+  a.r_out = static_cast<bf16_t*>(out);
+  a.r_stride = out_row_stride;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return p.d_a == 32 ? TableStepLaunch<16>::run(p, a, st) : TableStepLaunch<32>::run(p, a, st);
+}
+
+}  // extern "C"

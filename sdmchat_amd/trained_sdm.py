@@ -114,9 +114,19 @@ class TrainedSdm(nn.Module):
         B, T, _ = x.shape
         dt = self._compute_dtype(x)
         with torch.autocast("cuda", enabled=False):
-            si, _, w = self._picks(x, dt, hx)
-            r = core.table_read(si, w, self.values, self.k, out_dtype=dt)
-            y = core.linear(r, self._weights(dt)[1], as_matmul=True).to(x.dtype)
+            if hx is None:
+                hx = core.rms_norm(x, self.norm.w, self.norm.eps, out_dtype=dt)
+            wq, wo = self._weights(dt)
+            if core.table_step_fits(hx, wq, self.values, self.d_a):   # a few tokens: the read in one launch
+                prm = self._prm.get(x.device, self.keys1, self.keys2, None, self.log_scale, None, None, None)
+                r, si, _, _, q = core.table_step(hx, wq, self.keys1, self.keys2, self.log_scale, self.values, self.k,
+                                                 params=prm, want_q=self.keep_picks)
+                if self.keep_picks:
+                    self.last_q = q
+            else:
+                si, _, w = self._picks(x, dt, hx)
+                r = core.table_read(si, w, self.values, self.k, out_dtype=dt)
+            y = core.linear(r, wo, as_matmul=True).to(x.dtype)
         kk = min(self.k, min(self.k, self.n_sub) ** 2)
         self.last_si = si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
         return y

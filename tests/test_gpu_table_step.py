@@ -1,0 +1,69 @@
+"""GPU tests of sdm_rt_table_step (core.table_step), TrainedSdm's read for a few tokens in one launch
+(track4_onesdm_models.py:438-455: the query map, pk_address :134-148 and the weighted read): it must give, bit for
+bit, what the three separate entry points give (sdm_rt_gemm_rows for the query map, sdm_rt_address, sdm_rt_table_read),
+whose parity with the oracle the other tests check.  Shapes cover every addressing mode (32 and 64 sub-keys per half,
+full and masked grids, 8 and 16 picks), d_a 32 and 64 and 1 ... 256 tokens."""
+import pytest
+import torch
+
+from sdmchat_amd import TrainedSdm, core
+from tests._gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("H,n_sub,d_a,k,d,rows", [(1, 64, 32, 16, 768, 64),    # the FULL model's table layer
+                                                  (1, 64, 32, 16, 768, 1),
+                                                  (1, 64, 32, 16, 768, 256),
+                                                  (2, 32, 32, 8, 256, 37),     # full 32 x 32 grid
+                                                  (3, 20, 64, 12, 192, 5),     # masked grid, 16 picks
+                                                  (2, 48, 64, 8, 128, 64),     # 64 sub-keys, masked
+                                                  (1, 64, 64, 8, 64, 9)])      # 64 sub-keys, full, 8 picks
+def test_table_step_equals_map_address_and_read(H, n_sub, d_a, k, d, rows):
+    g = torch.Generator(device="cpu").manual_seed(H * 1000 + n_sub + d_a + k + rows)
+    dh = d // H
+    hx = torch.randn(1, rows, d, generator=g).to(torch.bfloat16).cuda()
+    wq = (torch.randn(H * d_a, d, generator=g) * d ** -0.5).to(torch.bfloat16).cuda()
+    keys1 = torch.randn(H, n_sub, d_a // 2, generator=g).cuda()
+    keys2 = torch.randn(H, n_sub, d_a // 2, generator=g).cuda()
+    log_scale = (torch.full((H,), 2.0) + torch.rand(H, generator=g) * 0.5).cuda()
+    values = torch.randn(H, n_sub * n_sub, dh, generator=g).to(torch.bfloat16).cuda()
+    say("table_step", H, n_sub, d_a, k, d, rows)
+    with torch.no_grad():
+        r, si, sc, w, q = core.table_step(hx, wq, keys1, keys2, log_scale, values, k, want_q=True)
+        q_ref = core.linear(hx, wq, as_matmul=True)
+        si_ref, sc_ref, w_ref = core.address(q_ref, keys1, keys2, k, log_scale, padded=True)
+        r_ref = core.table_read(si_ref, w_ref, values, k, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref)
+    assert torch.equal(si, si_ref)
+    assert torch.equal(sc, sc_ref) and torch.equal(w, w_ref)
+    assert torch.equal(r, r_ref)
+
+
+def test_trained_sdm_decode_shape_takes_the_one_launch_read():
+    """TrainedSdm.forward on a few bfloat16 tokens (a decode step) runs the read in one launch and gives the same
+    output, picks and queries as the separate calls (a forward of more tokens than the one-launch read takes)."""
+    torch.manual_seed(5)
+    m = TrainedSdm(768, 64, heads=1, d_a=32, k=16).cuda().to(torch.bfloat16).eval()
+    with torch.no_grad():
+        m.values.normal_()
+        m.wo.weight.normal_(std=0.03)
+    x = torch.randn(1, 300, 768, device="cuda").to(torch.bfloat16)   # 300 tokens: the separate calls
+    m.keep_picks = True
+    with torch.no_grad():
+        y_all = m(x)
+        si_all, q_all = m.last_si.clone(), m.last_q.clone()
+        y_few = m(x[:, :64])                                           # 64 tokens: one launch
+        assert core.table_step_fits(x[:, :64], m.wq.weight, m.values, 32)
+    # the query map of more than 256 rows is the GEMM library's: compare the one-launch read with the separate
+    # calls on the same 64 rows instead
+    with torch.no_grad():
+        hx = core.rms_norm(x[:, :64], m.norm.w, m.norm.eps, out_dtype=torch.bfloat16)
+        q_ref = core.linear(hx, m.wq.weight, as_matmul=True)
+        si_ref, _, w_ref = core.address(q_ref, m.keys1, m.keys2, m.k, m.log_scale, padded=True)
+        r_ref = core.table_read(si_ref, w_ref, m.values, m.k, out_dtype=torch.bfloat16)
+        y_ref = core.linear(r_ref, m.wo.weight, as_matmul=True)
+    assert torch.equal(m.last_q, q_ref)
+    assert torch.equal(y_few, y_ref)
+    assert y_all.shape == (1, 300, 768) and si_all.shape[0] == 300 and q_all.shape == (1, 300, 32)
