@@ -1,6 +1,6 @@
 """Throughput of the run-time SDM mixer forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--core-only] [--copy-probe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--core-only [--core-input repeated]] [--copy-probe]
 
 Workload: one RunTimeSdm layer forward at B=8, T=2048, d=768, 12 heads of width 64, 1,024 product-key locations
 per head, k=8, bf16 activations and weights, float32 memory state, synthetic seeded inputs and Xavier weights.  A
@@ -49,6 +49,8 @@ and one RunTimeSdm layer training step (forward + backward under bf16 autocast),
 layer of the FULL model (addressing + table read, and sdm_rt_table_backward), median of 20.  --no-train skips it.
 
 --copy-probe runs one 256 MiB device copy before the core calls (the calibration kernel for the traffic counters).
+--core-only --core-input repeated times the core on the projections of one repeated token per batch row (the core's
+slowest input: every chunk's positions pick the same locations), for profiler runs.
 """
 import argparse
 import json
@@ -392,6 +394,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--core-only", action="store_true", help="time only the SDM core (for profiler runs)")
+    ap.add_argument("--core-input", choices=("varied", "repeated"), default="varied",
+                    help="with --core-only: the layer input, or one repeated token per batch row")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter calibration)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step measurement")
     ap.add_argument("--decode-replays", type=int, default=513, help="graph replays of the decode-step measurement")
@@ -426,6 +430,10 @@ def main():
     m.load_state_dict({n: torch.from_numpy(v) for n, v in params.items()}, strict=True)
     m = m.to(dev).eval()
     x = torch.from_numpy(S.layer_input(B, T, D, seed=1)).to(dev).to(torch.bfloat16)
+    if a.core_input == "repeated":
+        if not a.core_only:
+            sys.exit("--core-input repeated times the core only (--core-only)")
+        x = x[:, :1].expand(B, T, D).contiguous()
 
     with torch.no_grad():
         kz, qz, V, g = m._project(x, torch.bfloat16)

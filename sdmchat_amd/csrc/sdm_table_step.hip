@@ -28,6 +28,7 @@ struct TableStepArgs {
 
 constexpr int kStepGroup = 4;          // tokens per block
 constexpr int kTableStepTokens = 256;  // at most this many tokens (sdm_rt_gemm_rows' row range, whose sums it repeats)
+constexpr int kStepK = 12;             // 16-deep steps per wave of the query map when d = 768
 
 // Block (4 tokens, head), 4 waves.
 //  1. the head's d_a query columns of the block's rows: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
@@ -63,11 +64,25 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
     for (int ct = 0; ct < NCT; ++ct) {
       const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + r) * a.wq_stride + kb;
       floatx16 acc = {};
-      for (int s = 0; s < kq / 16; ++s) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xr + 16 * s);
-        const uint4 wv = *reinterpret_cast<const uint4*>(wr + 16 * s);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv), __builtin_bit_cast(bf16x8, wv),
-                                                      acc, 0, 0, 0);
+      if (kq == 16 * kStepK) {   // d = 768: every operand of the wave loaded before the first product
+        uint4 xv[kStepK], wv[kStepK];
+#pragma unroll
+        for (int s = 0; s < kStepK; ++s) {
+          xv[s] = *reinterpret_cast<const uint4*>(xr + 16 * s);
+          wv[s] = *reinterpret_cast<const uint4*>(wr + 16 * s);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the scheduler from moving loads below the products
+#pragma unroll
+        for (int s = 0; s < kStepK; ++s)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[s]),
+                                                        __builtin_bit_cast(bf16x8, wv[s]), acc, 0, 0, 0);
+      } else {
+        for (int s = 0; s < kq / 16; ++s) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xr + 16 * s);
+          const uint4 wv = *reinterpret_cast<const uint4*>(wr + 16 * s);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv), __builtin_bit_cast(bf16x8, wv),
+                                                        acc, 0, 0, 0);
+        }
       }
       if (lane < 32) {
 #pragma unroll
