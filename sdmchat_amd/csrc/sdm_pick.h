@@ -63,7 +63,8 @@ struct VPiece<float> {
 };
 
 constexpr int kPickThreads = 512;    // 64 positions x 8 picks
-constexpr int kTeamWriters = 12;     // a wave with a slot of this many later writers in a chunk writes in teams
+constexpr int kTeamWriters = 32;     // a wave with a slot of this many later writers in a chunk writes in teams
+constexpr int kPrefetchContribs = 40;  // a wave with a position of more contributions loads their entries together
 
 template <typename VT, typename OutT>
 __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
@@ -304,15 +305,24 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
     }
     if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
       const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
-      auto over = [&](auto st) {   // contributions 8 + j, 16 + j, ... (at most 7: n_in < 64), entries loaded first
-        uint2 ev[7];
+      auto over = [&](auto st) {
+        if (__ballot(n_in > kPrefetchContribs)) {   // crowded: contributions 8 + j, 16 + j, ... (at most 7: n_in <
+          uint2 ev[7];                                // 64), their entries loaded together first
 #pragma unroll
-        for (int t = 0; t < 7; ++t) ev[t] = 8 + j + 8 * t < n_in ? ent_at(e0 + j + 8 * t, st) : make_uint2(0u, 0u);
+          for (int t = 0; t < 7; ++t) ev[t] = 8 + j + 8 * t < n_in ? ent_at(e0 + j + 8 * t, st) : make_uint2(0u, 0u);
 #pragma unroll
-        for (int t = 0; t < 7; ++t) {
-          if (8 + j + 8 * t < n_in) {
-            const float ce = __uint_as_float(ev[t].x);
-            add_vrow(ce, static_cast<int>(ev[t].y & 63u), acc);
+          for (int t = 0; t < 7; ++t) {
+            if (8 + j + 8 * t < n_in) {
+              const float ce = __uint_as_float(ev[t].x);
+              add_vrow(ce, static_cast<int>(ev[t].y & 63u), acc);
+              dl += ce;
+            }
+          }
+        } else {
+          for (int jj = 8 + j; jj < n_in; jj += 8) {
+            const uint2 e = ent_at(e0 + jj - 8, st);
+            const float ce = __uint_as_float(e.x);
+            add_vrow(ce, static_cast<int>(e.y & 63u), acc);
             dl += ce;
           }
         }
