@@ -15,6 +15,9 @@ events on the stream the kernels run on).  traffic = measured HBM bytes per call
 WRITE_SIZE summed over the core's kernels, scaled by the same counters' reading for a device copy of known size),
 read from profiles/sdm_core_traffic_b8_t2048.txt when present (null otherwise).
 
+config1: the same layer forward at B=1, T=256 in float32 (the reference's CPU-runnable configuration), median of 50
+calls.
+
 module: the whole layer is MFMA-bound (79.6 GFLOP per call against 55.2 MB): module.frac = max(bytes / 8 TB/s,
 FLOPs / 2.5 PFLOP/s) / module time.  copy_gbs: a 1 GiB device-to-device copy, for context.
 
@@ -307,13 +310,43 @@ def decode_model_bench(dev, streams=64, graph_steps=64, total=32768):
     us = np.array([e0.elapsed_time(e1) * 1e3 / graph_steps for e0, e1 in evs])
     by_pos = {str(p): round(float(us[p // graph_steps]), 1) for p in (0, 1024, 8192, 32768) if p <= total}
     steps = replays * graph_steps
+    floor = graph_kernel_floor_us(dev)
     log(f"decode (FULL model): {np.median(us):.1f} us per step, {streams * 1e6 / np.median(us):.0f} tokens/s, by "
-        f"position {by_pos}; {steps} steps in {wall:.1f} s")
+        f"position {by_pos}; {steps} steps in {wall:.1f} s; a kernel of no work costs {floor:.2f} us in a graph")
     return {"workload": f"FULL OneSdmLM (trained_sdm arm) decode: {streams} streams, one fresh random token per "
                         f"stream per step, {steps} steps, bf16, float32 state ({st.nbytes() / 2 ** 30:.2f} GiB)",
             "us_per_step": round(float(np.median(us)), 1), "tokens_per_s": round(streams * 1e6 / float(np.median(us)), 1),
             "us_per_step_by_position": by_pos, "wall_s": round(wall, 2),
-            "method": f"HIP graph of {graph_steps} steps (DecodeGraph), replay time / {graph_steps}"}
+            "method": f"HIP graph of {graph_steps} steps (DecodeGraph), replay time / {graph_steps}",
+            "graph_kernel_floor_us": round(floor, 2)}
+
+
+def graph_kernel_floor_us(dev, n=64, replays=200):
+    """The cost of one kernel of (almost) no work inside a HIP graph: n one-element adds captured in one graph,
+    replay time / n, best of three runs of `replays` replays (what every launch of a graph-replayed step pays)."""
+    import torch
+
+    t = torch.zeros(1, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        t.add_(1.0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            t.add_(1.0)
+    g.replay()
+    torch.cuda.synchronize()
+    best = 1e9
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for _ in range(replays):
+            g.replay()
+        torch.cuda.synchronize()
+        best = min(best, (time.perf_counter() - t0) / (replays * n))
+    return best * 1e6
 
 
 def train_bench(m, dev, x, kz, qz, V, g, prm, median_call_ms):
@@ -485,6 +518,8 @@ def main():
             return
         mod_ms = median_call_ms(lambda: m(x))
         wall = timed(lambda: m(x), a.steps, a.warmup)
+        x1 = torch.from_numpy(S.layer_input(1, 256, D, seed=2)).to(dev)   # config 1: B=1, T=256, float32
+        c1_ms = median_call_ms(lambda: m(x1))
         big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         big2 = torch.empty_like(big)
         copy_ms = median_call_ms(lambda: big2.copy_(big), n=10, warm=2)
@@ -523,6 +558,8 @@ def main():
                    "frac": round(max(MODULE_BYTES / (HBM_PEAK_GBS * 1e9), MODULE_FLOPS / BF16_PEAK_FLOPS)
                                  / (mod_ms * 1e-3), 4)},
         "copy_gbs": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
+        "config1": {"workload": "RunTimeSdm layer forward, B=1 T=256, float32 activations and weights",
+                    "ms": round(c1_ms, 5), "tokens_per_s": round(256 / (c1_ms * 1e-3), 1)},
     }
     if decode is not None:
         rec["decode"] = decode

@@ -85,6 +85,12 @@ typedef struct {
  * head and group). */
 size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims);
 
+/* With the write gate, sdm_rt_forward (and sdm_rt_forward_noalloc, in its scratch) leaves in its workspace a copy
+ * of the gate logits it read, [B*T][H] in the input dtype, from this byte offset; it stays there until the
+ * workspace is next used.  0 without the write gate or on invalid dims.  No reference counterpart: it lets a caller
+ * keep RunTimeSdm.last_gate's logits (track4_onesdm_models.py:205, 212) without a copy of its own. */
+size_t sdm_rt_gate_copy_offset(const sdm_rt_dims* dims);
+
 /* Row pitch (entries per token and head) of the pick arrays sdm_rt_address writes: kk rounded up to 8. */
 int32_t sdm_rt_pick_pitch(const sdm_rt_dims* dims);
 

@@ -106,6 +106,7 @@ SIGNATURES = {
                                           c_void_p, ctypes.c_size_t, c_void_p]),
     "sdm_rt_table_read": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), c_void_p, c_void_p, c_void_p, ctypes.c_int,
                                          c_void_p, c_i64, ctypes.c_int, c_void_p]),
+    "sdm_rt_gate_copy_offset": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
     "sdm_rt_table_step": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams), c_void_p, c_i64,
                                          ctypes.c_int32, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
                                          c_void_p, c_void_p, c_void_p, c_i64, c_void_p]),

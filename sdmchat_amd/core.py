@@ -130,6 +130,21 @@ def address(z, keys1, keys2, k, log_scale, addr_b=None, gate_logits=None, gate_b
     return slots[..., :kk], scores[..., :kk], weights[..., :kk]
 
 
+def gate_copy(workspace, B, T, H, dh, d_a, n_sub, k, dtype, read_mode="mean", out_norm=True, read_eps=1e-3,
+              out_norm_eps=1e-2):
+    """The gate logits that the last core_forward on ``workspace`` read, [B, T, H] in ``dtype`` (the projections'
+    dtype): a view of the copy sdm_rt_forward leaves in its workspace (sdm_rt_gate_copy_offset), valid until the
+    workspace is next used.  The dimensions must be those of that call."""
+    lib = _lib.load()
+    dims = make_dims(B, T, H, dh, d_a, n_sub, k, read_mode, out_norm, True, read_eps, out_norm_eps)
+    off = lib.sdm_rt_gate_copy_offset(ctypes.byref(dims))
+    n = B * T * H * torch.empty(0, dtype=dtype).element_size()
+    buf = workspace.buf
+    if off == 0 or buf is None or buf.numel() < off + n:
+        raise RuntimeError("gate_copy: the workspace holds no gate copy for these dimensions")
+    return buf[off:off + n].view(dtype).view(B, T, H)
+
+
 class CoreWorkspace:
     """A reusable device workspace (grows on demand)."""
 

@@ -1078,7 +1078,7 @@ struct Plan {
   int cw, cw32;     // scan: value columns per workgroup for bfloat16 and float32 values (0: does not fit)
   int groups;       // the most scan workgroups per (batch row, head) slab over both value types (workspace size)
   // forward workspace offsets
-  size_t off_sizes, off_plans, off_sync, off_xch, total;
+  size_t off_sizes, off_plans, off_sync, off_xch, off_gate, total;
 };
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -1120,7 +1120,7 @@ inline int make_plan(const sdm_rt_dims* d, Plan* p, bool core = true) {
   p->pitch = (p->kk + 7) / 8 * 8;
   p->n_chunks = (p->T + kChunk - 1) / kChunk;
   p->cw = p->cw32 = p->groups = 0;
-  p->off_sizes = p->off_plans = p->off_sync = p->off_xch = p->total = 0;
+  p->off_sizes = p->off_plans = p->off_sync = p->off_xch = p->off_gate = p->total = 0;
   if (!core) return SDM_RT_OK;
   // the column group of bfloat16 values (wider when it fits); float32 values may need a narrower one
   p->cw = scan_columns(p->M, p->dh, p->n_chunks, p->pitch, 2);
@@ -1147,6 +1147,9 @@ inline int make_plan(const sdm_rt_dims* d, Plan* p, bool core = true) {
   // sum with a flag that says it is written)
   p->off_xch = o;
   o = align_up(o + (d->out_norm && p->groups > 1 ? 8 * slabs * p->n_chunks * p->groups * kChunk : 0), 256);
+  // with the write gate, a copy of the gate logits the forward read, [B*T][H] in the input type (4 bytes reserved)
+  p->off_gate = o;
+  o = align_up(o + (d->write_gate ? sizeof(float) * static_cast<size_t>(p->B) * p->T * p->H : 0), 256);
   p->total = o;
   return SDM_RT_OK;
 }

@@ -60,6 +60,7 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   pa.qz = io.qz;
   pa.qz_stride = io.qz_stride;
   pa.gl = dims->write_gate ? io.gate_logits : nullptr;
+  pa.gate_copy = pa.gl ? ws + p.off_gate : nullptr;
   pa.g_stride = io.g_stride;
   pa.decay = prm->decay;
   pa.reset = io.reset;
@@ -127,6 +128,12 @@ size_t sdm_rt_workspace_bytes(const sdm_rt_dims* dims) {
   Plan p;
   if (make_plan(dims, &p) != SDM_RT_OK) return 0;
   return p.total;
+}
+
+size_t sdm_rt_gate_copy_offset(const sdm_rt_dims* dims) {
+  Plan p;
+  if (!dims || !dims->write_gate || make_plan(dims, &p) != SDM_RT_OK) return 0;
+  return p.off_gate;
 }
 
 void sdm_rt_set_wait_limit(int64_t polls) {

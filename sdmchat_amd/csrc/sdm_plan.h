@@ -43,6 +43,7 @@ struct PlanArgs {
   int32_t* sizes;          // [B][H][n_chunks] bytes of each plan's variable part
   uint32_t* sync;          // [B*H][groups] scan progress counters, then a status word: zeroed here, or nullptr
   unsigned long long* xch; // pick plans: [B*H][n_chunks][xgroups][64] out-norm partial sums, cleared here, or nullptr
+  void* gate_copy;         // [B*T][H] of the input type: the gate logits as read (rows of H), or nullptr
   int groups;
   int xgroups;             // column groups of the pick scan
   int row_bytes;           // bytes of a slab row in the scan's LDS (its column group width * 4)
@@ -244,6 +245,8 @@ __global__ void __launch_bounds__(128, 3) plan_kernel(PlanArgs a) {
     const float gate = (set == 0 && a.gl && p < L)
                            ? gate_of(static_cast<const InT*>(a.gl) + (row0 + p) * a.g_stride, h, a.g.gate_bias)
                            : 1.f;
+    if (set == 0 && a.gate_copy && p < L)   // the caller's compact copy of the logits (RunTimeSdm.last_gate)
+      static_cast<InT*>(a.gate_copy)[(row0 + p) * a.g.H + h] = static_cast<const InT*>(a.gl)[(row0 + p) * a.g_stride + h];
     const InT* zb = static_cast<const InT*>(set == 0 ? a.kz : a.qz);
     const int64_t zs = set == 0 ? a.kz_stride : a.qz_stride;
     if constexpr (MODE > 0) {

@@ -259,9 +259,13 @@ class RunTimeSdm(nn.Module):
                 self.last_picks = tuple(
                     core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
                                  params=prm)[0] for z in (kz, qz))
-            # the gate logits copied out of the projection buffer ([B, T, H]; a view would keep the whole buffer,
-            # ~59 MB at B=8, T=2048, until the next forward); last_gate applies the sigmoid when first read
-            g_keep = None if g is None else g.contiguous()
+            # the gate logits as the forward left them in its workspace ([B, T, H]: a view of the projection
+            # buffer would keep the whole buffer, ~59 MB at B=8, T=2048, until the next forward, and a copy costs a
+            # launch); the workspace is this module's, so the view holds until the next forward replaces it;
+            # last_gate applies the sigmoid when first read
+            g_keep = None if g is None else core.gate_copy(
+                self._ws, B, T, H, self.dh, self.d_a, self.n_sub, self.k, dt, self.read_mode, self.out_norm,
+                self.read_eps, self.out_norm_eps)
         self._gate_src = (g_keep, None, (B, T, H), x.device)
         self._last_gate = None
         self._last_state, self._state_skipped = state, not self.keep_state

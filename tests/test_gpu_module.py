@@ -230,19 +230,29 @@ def test_last_state_matches_oracle():
     np.testing.assert_allclose(y.cpu().numpy(), O.layer_forward(x, pp, cfg), atol=1e-5, rtol=1e-5)
 
 
-def test_last_gate_is_kept_apart_and_last_state_is_loud():
-    """After an inference forward the gate logits are a small contiguous [B, T, H] tensor (not a view that keeps
-    the fused projection's buffer alive), last_gate is their sigmoid, and reading last_state after a forward that
-    did not write it (keep_state unset) raises instead of returning None; with keep_state it holds the state."""
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_last_gate_is_kept_apart_and_last_state_is_loud(dt):
+    """After an inference forward the gate logits are the [B, T, H] copy the forward left in the module's own
+    workspace (sdm_rt_gate_copy_offset; not a view that keeps the fused projection's buffer alive), equal to the
+    projections' gate logits bit for bit, last_gate is their sigmoid, a second forward's gate replaces the first's,
+    and reading last_state after a forward that did not write it (keep_state unset) raises instead of returning
+    None; with keep_state it holds the state."""
     cfg = S.layer_cfg(d=64, heads=4, n_sub=8, d_a=16, k=8)
     p = S.layer_params(cfg, seed=70)
     m = build(cfg, p)
-    x = torch.from_numpy(S.layer_input(2, 50, 64, seed=1070)).cuda()
-    with torch.no_grad():
-        m(x)
+    x = torch.from_numpy(S.layer_input(2, 50, 64, seed=1070)).cuda().to(dt)
+    x2 = torch.from_numpy(S.layer_input(2, 50, 64, seed=1071)).cuda().to(dt)
+    for xx in (x2, x):
+        with torch.no_grad():
+            m(xx)
     g = m._gate_src[0]
-    assert g.is_contiguous() and tuple(g.shape) == (2, 50, 4) and g.untyped_storage().nbytes() == g.numel() * g.element_size()
+    assert tuple(g.shape) == (2, 50, 4) and g.dtype == dt
+    assert g.untyped_storage().data_ptr() == m._ws.buf.untyped_storage().data_ptr()   # the workspace's copy
+    with torch.no_grad():
+        g_ref = m._project(x, dt)[3]
+    assert torch.equal(g, g_ref)
     gate = m.last_gate
+    assert torch.equal(gate, torch.sigmoid(g_ref.float()))
     assert tuple(gate.shape) == (2, 50, 4) and float(gate.min()) >= 0 and float(gate.max()) <= 1
     with pytest.raises(RuntimeError, match="keep_state"):
         _ = m.last_state
