@@ -544,10 +544,11 @@ __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf
 // address values are bfloat16 already, so every product is exact in the float32 accumulation.  The address bias
 // enters through the accumulator's start value c_i = k_i . addr_b (one float32 matrix step: c_i x 1) and through
 // inv.  Lane l feeds dims 16q + 8(l/32) + e (e < 8) of sub-key row l%32 and of both address rows (HALF = 8: lanes
-// 32..63 feed zeros).
+// 32..63 feed zeros).  Head h's address columns start at column zcol of a row (h * 2 HALF when zcol < 0).
 template <int HALF, bool FULL>
 __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
-                                                 int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0) {
+                                                 int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0,
+                                                 int zcol = -1) {
   static_assert(HALF % 8 == 0, "bfloat16 scoring feeds 8 dims per lane");
   constexpr int Q = (HALF + 15) / 16;
   const int l = threadIdx.x & 63;
@@ -563,7 +564,8 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int row = min(32 * t + jl, rows - 1);
-      zr[t][q] = has ? load_raw8(z0 + row * zstride + static_cast<int64_t>(h) * 2 * HALF + d0 + 16 * q)
+      zr[t][q] = has ? load_raw8(z0 + row * zstride + (zcol >= 0 ? zcol : static_cast<int64_t>(h) * 2 * HALF) + d0 +
+                                 16 * q)
                      : make_uint4(0u, 0u, 0u, 0u);
     }
     if (has) {

@@ -105,11 +105,11 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   __syncthreads();
   if (wave < 2 * NT) {
     const int hf = wave / NT, tile = wave % NT;
-    // half_scores reads row r of head h at z0 + r * DA + h * DA: the LDS rows hold head h's columns only
-    const bf16_t* z0 = reinterpret_cast<const bf16_t*>(&s_q[0][0]) - h * DA;
+    // the LDS rows hold head h's columns only: they start at column 0
+    const bf16_t* z0 = reinterpret_cast<const bf16_t*>(&s_q[0][0]);
     floatx16 acc[2];
     float inv[2];
-    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile);
+    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile, 0);
     // lane l: token l % 32 of tile 0, sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
     const int row = lane & 31;
     if (row < nb) {
