@@ -217,6 +217,21 @@ int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, cons
                       int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
                       int64_t out_row_stride, void* stream);
 
+/* sdm_rt_table_step with the residual add and TrainedSdm's input norm folded in front: the stage before the table
+ * layer left y, OneSdmLM adds it to the residual stream x (x = x + layer(x), track4_onesdm_models.py:540-547) and the
+ * table layer normalises the sum (TrainedSdm.norm, :441; RMSNorm, track4_sdmllm_models.py:69-71).  Here
+ * sum_out = x + y (bfloat16) and hx = rms_norm(sum_out, norm_w, norm_eps) (bfloat16, kept on chip) feed the table
+ * step; bit for bit sdm_rt_add_rms_norm followed by sdm_rt_table_step, in one launch.  x, y and sum_out are [B*T rows]
+ * of d = 768 with the given row strides, 16-byte aligned; norm_w [d] float32, 16-byte aligned.  sum_out may be x
+ * (in place) when the table has one head.  hx_out [B*T rows] of d receives hx, or NULL.  The other arguments as
+ * sdm_rt_table_step's. */
+int sdm_rt_table_step_residual(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* x,
+                               int64_t x_row_stride, const void* y, int64_t y_row_stride, const float* norm_w,
+                               float norm_eps, void* sum_out, int64_t sum_row_stride, void* hx_out,
+                               int64_t hx_row_stride, int32_t d, const void* wq, int64_t wq_row_stride,
+                               const void* values, void* q_out, int64_t q_row_stride, int32_t* slot_out,
+                               float* score_out, float* weight_out, void* out, int64_t out_row_stride, void* stream);
+
 /* The input norm of RunTimeSdm (RMSNorm, experiments/track4/sdmllm/track4_sdmllm_models.py:63-71) with the
  * reference's rounding: out = cast_out(cast_in(x * rsqrt(mean(x^2) + eps)) * w), the mean and product in float32,
  * cast_in rounding to the input dtype and cast_out to out_dtype.

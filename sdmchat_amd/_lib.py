@@ -110,6 +110,11 @@ SIGNATURES = {
     "sdm_rt_table_step": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams), c_void_p, c_i64,
                                          ctypes.c_int32, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
                                          c_void_p, c_void_p, c_void_p, c_i64, c_void_p]),
+    "sdm_rt_table_step_residual": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams), c_void_p,
+                                                  c_i64, c_void_p, c_i64, c_void_p, ctypes.c_float, c_void_p, c_i64,
+                                                  c_void_p, c_i64, ctypes.c_int32, c_void_p, c_i64, c_void_p,
+                                                  c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_i64,
+                                                  c_void_p]),
     "sdm_rt_rms_norm": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p,
                                        ctypes.c_float, c_void_p, c_i64, ctypes.c_int, c_void_p]),
     "sdm_rt_add_rms_norm": (ctypes.c_int, [c_void_p, c_i64, c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32,

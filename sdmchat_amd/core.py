@@ -327,6 +327,56 @@ def table_step(hx, wq, keys1, keys2, log_scale, values, k, params=None, want_q=F
     return out, slots, scores, weights, q
 
 
+def table_step_residual_fits(x, y, wq, values, d_a):
+    """Whether sdm_rt_table_step_residual serves this residual add and TrainedSdm read: table_step_fits on x, y of
+    x's shape and dtype, both contiguous, and the layer width 768."""
+    return (x.shape[-1] == TABLE_STEP_FOLD_D and y.shape == x.shape and y.dtype == x.dtype and x.is_contiguous()
+            and y.is_contiguous() and y.is_cuda and table_step_fits(x, wq, values, d_a)
+            and not (torch.is_grad_enabled() and (x.requires_grad or y.requires_grad)))
+
+
+TABLE_STEP_FOLD_D = 768   # the layer width of sdm_rt_table_step_residual
+
+
+def table_step_residual(x, y, norm_w, eps, wq, keys1, keys2, log_scale, values, k, params=None, want_q=False,
+                        inplace=True, want_hx=False):
+    """The residual add, TrainedSdm's input norm and its read in one launch (sdm_rt_table_step_residual):
+    s = x + y, hx = rms_norm(s, norm_w, eps) in bf16, then table_step on hx; bit for bit add_rms_norm followed by
+    table_step.  x, y [B, T, 768] bf16, contiguous.  s is written into x when ``inplace`` (one head only; otherwise
+    into a new tensor).  Returns (s, r, slots, scores, weights, q, hx); q and hx are None unless asked for."""
+    lib = _lib.load()
+    B, T, d = x.shape
+    H, n_sub, half = keys1.shape
+    d_a = 2 * half
+    dh = values.shape[-1]
+    dims = make_dims(B, T, H, dh, d_a, n_sub, k, out_norm=False, write_gate=False)
+    wq = wq if _rows16(wq) else wq.contiguous()
+    vals = values.detach().contiguous()
+    dev = x.device
+    if params is None:
+        params = _params(dev, keys1, keys2, None, log_scale, None, None, None)
+    prm, held = params
+    pitch = lib.sdm_rt_pick_pitch(ctypes.byref(dims))
+    if pitch <= 0:
+        raise _lib.SdmRtError(lib.sdm_rt_last_error().decode() or "invalid dimensions")
+    s = x if (inplace and H == 1) else torch.empty_like(x)
+    wf = _f32_weight(norm_w, dev)
+    slots = torch.empty(B, H, T, pitch, dtype=torch.int32, device=dev)
+    scores = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    weights = torch.empty(B, H, T, pitch, dtype=torch.float32, device=dev)
+    out = torch.empty(B, T, H * dh, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(B, T, H * d_a, dtype=torch.bfloat16, device=dev) if want_q else None
+    hx = torch.empty(B, T, d, dtype=torch.bfloat16, device=dev) if want_hx else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.sdm_rt_table_step_residual(ctypes.byref(dims), ctypes.byref(prm), _ptr(x), d, _ptr(y), d, _ptr(wf),
+                                        float(eps), _ptr(s), d, _ptr(hx), d, d, _ptr(wq), wq.stride(0), _ptr(vals),
+                                        _ptr(q), H * d_a, _ptr(slots), _ptr(scores), _ptr(weights), _ptr(out), H * dh,
+                                        ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    del held
+    return s, out, slots, scores, weights, q, hx
+
+
 class DecodeState:
     """State of B decode streams: the true memory is ``scale * mem`` and the true counts ``scale * cnt``
     (mem [B, H, M, dh], cnt [B, H, M], scale [B, H], float32, on the device).  Keeping the scale apart lets a decode

@@ -1,55 +1,9 @@
 // sdm_misc.hip -- the input norm (sdm_rt_rms_norm, and with the residual add before it sdm_rt_add_rms_norm),
 // SwiGLU's gate (sdm_rt_silu_mul), the table read of TrainedSdm (sdm_rt_table_read) and the addressing entry point
 // (sdm_rt_address).
-#include "sdm_common.h"
+#include "sdm_norm.h"
 
 namespace sdmrt {
-
-// x rounded to T and back (bfloat16: the hardware conversion, nearest even)
-template <typename T>
-__device__ __forceinline__ float round_to(float x) {
-  if constexpr (sizeof(T) == 2) return __uint_as_float(pack_bf16(x, 0.f) << 16);
-  else return x;
-}
-// 8 values from / to T (16-byte pieces: p is 16-byte aligned, as the launchers check)
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
-  if constexpr (sizeof(T) == 2) {
-    const uint4 q = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = __uint_as_float(w[e] << 16);
-      v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-    }
-  } else {
-    const float4 q0 = reinterpret_cast<const float4*>(p)[0], q1 = reinterpret_cast<const float4*>(p)[1];
-    v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-    v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-  }
-}
-template <typename T>
-__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
-  if constexpr (sizeof(T) == 2) {
-    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
-                                              pack_bf16(v[6], v[7]));
-  } else {
-    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
-    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
-  }
-}
-// the sum over the 32 lanes of each half of the wave, in every lane of the half (DPP within rows of 16, then
-// rows 0 + 1 and 2 + 3, read back from lanes 31 and 63)
-__device__ __forceinline__ float half_wave_sum(float v, int lane) {
-  v += dpp_f<0xb1>(v);    // quad_perm [1,0,3,2]
-  v += dpp_f<0x4e>(v);    // quad_perm [2,3,0,1]
-  v += dpp_f<0x141>(v);   // row_half_mirror
-  v += dpp_f<0x140>(v);   // row_mirror: every lane of a row holds the row's sum
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));   // row_bcast:15
-  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
-  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-  return lane < 32 ? lo : hi;
-}
 
 // rms_norm: two rows per wave, 32 lanes per row, each lane taking 8 consecutive values at a time (KC pieces of 8
 // per lane, KC = ceil(d / 256)); the row, the residual and the weights are all loaded before any use.  ADD: the row
@@ -62,42 +16,10 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* x, int64_t x_s
                                                        int d, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6) * 2 + (lane >> 5);
-  const int hl = lane & 31;
   const bool live = row < rows;   // both halves of a wave take part in the sums
   const int64_t r = live ? row : 0;
-  float v[KC][8], wv[KC][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < KC; ++k) {
-    const int c = 8 * (hl + 32 * k);
-    if (c < d) {
-      load8<InT>(x + r * x_stride + c, v[k]);
-      load8<float>(w + c, wv[k]);
-      if constexpr (ADD) {
-        float u[8];
-        load8<InT>(y + r * y_stride + c, u);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[k][e] = round_to<InT>(v[k][e] + u[e]);   // x + y in the input type
-        if (live) store8<InT>(sum + r * sum_stride + c, v[k]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
-    }
-  }
-  ss = half_wave_sum(ss, lane);
-  const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
-  if (!live) return;
-  OutT* dst = out + r * out_stride;
-#pragma unroll
-  for (int k = 0; k < KC; ++k) {
-    const int c = 8 * (hl + 32 * k);
-    if (c < d) {
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = round_to<InT>(v[k][e] * rs) * wv[k][e];   // .to(x.dtype) * w
-      store8<OutT>(dst + c, o);
-    }
-  }
+  norm_row<InT, OutT, ADD, KC>(x + r * x_stride, ADD ? y + r * y_stride : nullptr, ADD ? sum + r * sum_stride : nullptr,
+                               out + r * out_stride, w, d, eps, lane, live, live);
 }
 
 // SwiGLU's gate: out = silu(g) * u with g, u the two halves of a row of the fused [gate | up] projection, each

@@ -4,7 +4,7 @@
 // the softmax weights, embedding_bag).  Each stage is computed as its own entry point computes it (the query map as
 // sdm_rt_gemm_rows sums it, the addressing as sdm_rt_address, the read as sdm_rt_table_read), so the three calls and
 // this one give the same bits; between the stages the data stay in LDS and registers.
-#include "sdm_common.h"
+#include "sdm_norm.h"
 
 namespace sdmrt {
 
@@ -24,11 +24,23 @@ struct TableStepArgs {
   float* s_out;            // same layout or nullptr
   bf16_t* r_out;           // [N][H * dh]
   int64_t r_stride;
+  // the residual add and the input norm folded in front (FOLD): hx = rms_norm(rx + ry), rsum = rx + ry
+  const bf16_t* rx;        // [N][d]
+  int64_t rx_stride;
+  const bf16_t* ry;        // [N][d]
+  int64_t ry_stride;
+  bf16_t* rsum;            // [N][d], written by head 0's blocks
+  int64_t rsum_stride;
+  const float* rw;         // [d] the norm's weight
+  float reps;
+  bf16_t* hx_out;          // [N][d] the normed rows (head 0's blocks), or nullptr
+  int64_t hx_out_stride;
 };
 
 constexpr int kStepGroup = 4;          // tokens per block
 constexpr int kTableStepTokens = 256;  // at most this many tokens (sdm_rt_gemm_rows' row range, whose sums it repeats)
 constexpr int kStepK = 12;             // 16-deep steps per wave of the query map when d = 768
+constexpr int kFoldD = 768;            // the layer width of the folded residual add and norm (FOLD)
 
 // Block (4 tokens, head), 4 waves.
 //  1. the head's d_a query columns of the block's rows: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
@@ -38,7 +50,10 @@ constexpr int kStepK = 12;             // 16-deep steps per wave of the query ma
 //     (half_scores, reading the queries from LDS), and wave j selects token j across its lanes (select_lanes);
 //  3. wave j reads its token's picked rows, 16 bytes of a row per lane, and sums them in pick order over the pitch
 //     (pads: slot 0, weight 0) in float32, as the table read does.
-template <int HALF, int CAP, int MODE>
+// FOLD (d = 768): before 1., half-wave i of waves 0 and 1 computes row i's residual sum rx + ry and its norm with the
+// norm kernel's own code (norm_row: the same bits as sdm_rt_add_rms_norm), writes the sum (head 0's blocks only)
+// and leaves the normed row in LDS, from which the query map reads it.
+template <int HALF, int CAP, int MODE, bool FOLD>
 __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   constexpr int NS = MODE >= 3 ? 64 : 32;
   constexpr int NT = NS / 32;
@@ -50,16 +65,37 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kStepGroup][DA];
   __shared__ float s_sc[kStepGroup][2][NS];
   __shared__ float s_inv[kStepGroup][2];
+  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? kStepGroup : 1][FOLD ? kFoldD : 8];
   const int h = blockIdx.y;
   const int64_t N = static_cast<int64_t>(a.B) * a.T;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStepGroup;
   const int nb = static_cast<int>(min<int64_t>(kStepGroup, N - n0));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if constexpr (FOLD) {
+    static_assert(kStepGroup == 4, "two rows per wave in waves 0 and 1");
+    if (wave < kStepGroup / 2) {
+      const int i = 2 * wave + (lane >> 5);
+      const bool live = i < nb;
+      const int64_t rr = n0 + (live ? i : 0);
+      norm_row<bf16_t, bf16_t, true, kFoldD / 256>(a.rx + rr * a.rx_stride, a.ry + rr * a.ry_stride,
+                                                   a.rsum + rr * a.rsum_stride, &s_hx[live ? i : 0][0], a.rw, kFoldD,
+                                                   a.reps, lane, live, live && h == 0);
+      if (a.hx_out && live && h == 0) {   // the lane's own pieces, as norm_row stored them
+#pragma unroll
+        for (int k = 0; k < kFoldD / 256; ++k) {
+          const int c = 8 * ((lane & 31) + 32 * k);
+          *reinterpret_cast<uint4*>(a.hx_out + rr * a.hx_out_stride + c) = *reinterpret_cast<const uint4*>(&s_hx[i][c]);
+        }
+      }
+    }
+    __syncthreads();
+  }
   {
     const int kq = a.d / 4;
     const int kb = wave * kq + 8 * (lane >> 5);
     const int r = lane & 31;
-    const bf16_t* xr = a.hx + (n0 + min(r, nb - 1)) * a.hx_stride + kb;   // rows past the block: clamped, unused
+    // rows past the block: clamped, unused; FOLD: the normed rows in LDS
+    const bf16_t* xr = FOLD ? &s_hx[min(r, nb - 1)][0] + kb : a.hx + (n0 + min(r, nb - 1)) * a.hx_stride + kb;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
       const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + r) * a.wq_stride + kb;
@@ -166,8 +202,11 @@ struct TableStepLaunch {
   template <int CAP, int MODE>
   static int go(const Plan& p, const TableStepArgs& a, hipStream_t st) {
     const int64_t N = static_cast<int64_t>(p.B) * p.T;
-    hipLaunchKernelGGL((table_step_kernel<HALF, CAP, MODE>), dim3(static_cast<unsigned>((N + kStepGroup - 1) / kStepGroup), p.H),
-                       dim3(256), 0, st, a);
+    const dim3 grid(static_cast<unsigned>((N + kStepGroup - 1) / kStepGroup), p.H);
+    if (a.rx)
+      hipLaunchKernelGGL((table_step_kernel<HALF, CAP, MODE, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((table_step_kernel<HALF, CAP, MODE, false>), grid, dim3(256), 0, st, a);
     return check_launch("table_step");
   }
   // the addressing mode of sdm_rt_address for this shape (AddressLaunch::run)
@@ -191,10 +230,25 @@ using namespace sdmrt;
 
 extern "C" {
 
-int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* hx, int64_t hx_row_stride,
-                      int32_t d, const void* wq, int64_t wq_row_stride, const void* values, void* q_out,
-                      int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
-                      int64_t out_row_stride, void* stream) {
+namespace {
+
+struct Residual {   // the folded residual add and norm of sdm_rt_table_step_residual
+  const void* x;
+  int64_t x_stride;
+  const void* y;
+  int64_t y_stride;
+  const float* w;
+  float eps;
+  void* sum;
+  int64_t sum_stride;
+  void* hx;
+  int64_t hx_stride;
+};
+
+int table_step_impl(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* hx, int64_t hx_row_stride,
+                    int32_t d, const void* wq, int64_t wq_row_stride, const void* values, void* q_out,
+                    int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
+                    int64_t out_row_stride, const Residual* res, void* stream) {
   g_err[0] = 0;
   Plan p;
   int rc = make_plan(dims, &p, false);
@@ -209,16 +263,33 @@ int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, cons
     return set_err(SDM_RT_EUNSUPPORTED, "table_step: addr_dim = %d must be 32 or 64", p.d_a);
   if (p.dh % 8 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: head_dim = %d must be a multiple of 8", p.dh);
   if (p.pitch != p.cap) return set_err(SDM_RT_EUNSUPPORTED, "table_step: pick pitch %d", p.pitch);
-  if (!hx || !wq || !values || !slot_out || !out)
+  if ((!res && !hx) || !wq || !values || !slot_out || !out)
     return set_err(SDM_RT_EINVAL, "hx, wq, values, slot_out and out must not be NULL");
-  if (hx_row_stride < d || wq_row_stride < d || out_row_stride < static_cast<int64_t>(p.H) * p.dh ||
+  if ((!res && hx_row_stride < d) || wq_row_stride < d || out_row_stride < static_cast<int64_t>(p.H) * p.dh ||
       (q_out && q_row_stride < static_cast<int64_t>(p.H) * p.d_a))
     return set_err(SDM_RT_EINVAL, "table_step: a row stride is smaller than its row");
   auto al16 = [](const void* ptr, int64_t stride) {
     return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && (stride * 2) % 16 == 0;
   };
-  if (!al16(hx, hx_row_stride) || !al16(wq, wq_row_stride) || !al16(values, p.dh) || !al16(out, out_row_stride))
+  if ((!res && !al16(hx, hx_row_stride)) || !al16(wq, wq_row_stride) || !al16(values, p.dh) ||
+      !al16(out, out_row_stride))
     return set_err(SDM_RT_EINVAL, "table_step: hx, wq, values and out rows must be 16-byte aligned");
+  if (res) {
+    if (d != kFoldD) return set_err(SDM_RT_EUNSUPPORTED, "table_step_residual: d = %d, must be %d", d, kFoldD);
+    if (!res->x || !res->y || !res->w || !res->sum)
+      return set_err(SDM_RT_EINVAL, "table_step_residual: x, y, norm_w and sum_out must not be NULL");
+    if (res->x_stride < d || res->y_stride < d || res->sum_stride < d)
+      return set_err(SDM_RT_EINVAL, "table_step_residual: a row stride is smaller than its row");
+    if (!al16(res->x, res->x_stride) || !al16(res->y, res->y_stride) || !al16(res->sum, res->sum_stride) ||
+        reinterpret_cast<uintptr_t>(res->w) % 16)
+      return set_err(SDM_RT_EINVAL, "table_step_residual: x, y, sum_out rows and norm_w must be 16-byte aligned");
+    // every head's blocks read x and y; head 0's write the sum: in place only with one head
+    if (p.H > 1 && (res->sum == res->x || res->sum == res->y))
+      return set_err(SDM_RT_EINVAL, "table_step_residual: sum_out may alias x only with one head");
+    if (res->sum == res->y) return set_err(SDM_RT_EINVAL, "table_step_residual: sum_out must not alias y");
+    if (res->hx && (res->hx_stride < d || !al16(res->hx, res->hx_stride)))
+      return set_err(SDM_RT_EINVAL, "table_step_residual: hx_out rows must be 16-byte aligned and >= d long");
+  }
   TableStepArgs a{};
   a.g = addr_geom(p, params);
   a.hx = static_cast<const bf16_t*>(hx);
@@ -239,8 +310,41 @@ int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, cons
   a.s_out = score_out;
   a.r_out = static_cast<bf16_t*>(out);
   a.r_stride = out_row_stride;
+  if (res) {
+    a.rx = static_cast<const bf16_t*>(res->x);
+    a.rx_stride = res->x_stride;
+    a.ry = static_cast<const bf16_t*>(res->y);
+    a.ry_stride = res->y_stride;
+    a.rsum = static_cast<bf16_t*>(res->sum);
+    a.rsum_stride = res->sum_stride;
+    a.rw = res->w;
+    a.reps = res->eps;
+    a.hx_out = static_cast<bf16_t*>(res->hx);
+    a.hx_out_stride = res->hx_stride;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   return p.d_a == 32 ? TableStepLaunch<16>::run(p, a, st) : TableStepLaunch<32>::run(p, a, st);
+}
+
+}  // namespace
+
+int sdm_rt_table_step(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* hx, int64_t hx_row_stride,
+                      int32_t d, const void* wq, int64_t wq_row_stride, const void* values, void* q_out,
+                      int64_t q_row_stride, int32_t* slot_out, float* score_out, float* weight_out, void* out,
+                      int64_t out_row_stride, void* stream) {
+  return table_step_impl(dims, params, hx, hx_row_stride, d, wq, wq_row_stride, values, q_out, q_row_stride, slot_out,
+                         score_out, weight_out, out, out_row_stride, nullptr, stream);
+}
+
+int sdm_rt_table_step_residual(const sdm_rt_dims* dims, const sdm_rt_params* params, const void* x,
+                               int64_t x_row_stride, const void* y, int64_t y_row_stride, const float* norm_w,
+                               float norm_eps, void* sum_out, int64_t sum_row_stride, void* hx_out,
+                               int64_t hx_row_stride, int32_t d, const void* wq, int64_t wq_row_stride,
+                               const void* values, void* q_out, int64_t q_row_stride, int32_t* slot_out,
+                               float* score_out, float* weight_out, void* out, int64_t out_row_stride, void* stream) {
+  const Residual res{x, x_row_stride, y, y_row_stride, norm_w, norm_eps, sum_out, sum_row_stride, hx_out, hx_row_stride};
+  return table_step_impl(dims, params, nullptr, 0, d, wq, wq_row_stride, values, q_out, q_row_stride, slot_out,
+                         score_out, weight_out, out, out_row_stride, &res, stream);
 }
 
 }  // extern "C"

@@ -184,22 +184,32 @@ class OneSdmLM(nn.Module):
     def _run(self, x, apply):
         """Inference: the residual stream through every stage with each residual add fused into the next stage's
         input norm (core.add_rms_norm: one kernel for x = x + y and its RMSNorm, the same roundings as the add and
-        the norm apart).  apply(kind, i, x, hx) gives a stage's output.  Returns nf(x)."""
+        the norm apart); in front of a TrainedSdm stage that takes it (a few tokens, TrainedSdm.residual_fits) the
+        add and the norm run inside that stage's table step instead (TrainedSdm.forward_residual, the same bits).
+        apply(kind, i, x, hx) gives a stage's output.  Returns nf(x)."""
         stages = self._stages()
         if not stages:
             return _norm(x, self.nf)
         kind, i, norm = stages[0]
         x = x.contiguous()   # the residual stream (enfold's fresh output), updated in place
         hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
+        pending = None       # the last stage's output, to be added in front of this (TrainedSdm) stage
         for n, (kind, i, norm) in enumerate(stages):
-            y = apply(kind, i, x, hx)
+            if pending is not None:
+                x, y = self.sdms[i].forward_residual(x, pending)
+                pending = None
+            else:
+                y = apply(kind, i, x, hx)
             nxt = stages[n + 1] if n + 1 < len(stages) else ("nf", 0, self.nf)
             if y.dtype != x.dtype:   # a stage wider than the stream: the add promotes, as x + y does
                 x = (x + y).contiguous()
                 hx = core.rms_norm(x, nxt[2].w, nxt[2].eps, out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
                 continue
-            x, hx = core.add_rms_norm(x, y.contiguous(), nxt[2].w, nxt[2].eps,
-                                      out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
+            y = y.contiguous()
+            if nxt[0] == "sdm" and self.sdms[nxt[1]].residual_fits(x, y):
+                pending = y
+                continue
+            x, hx = core.add_rms_norm(x, y, nxt[2].w, nxt[2].eps, out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
         return hx
 
     def residual(self, idx, sequential=False):

@@ -41,6 +41,7 @@ class TrainedSdm(nn.Module):
         self.last_si = None
         self.keep_picks = False   # set True to keep the last forward's queries in last_q
         self.last_q = None
+        self.last_hx = None
         self._cast = None
         self._prm = core.ParamCache()
 
@@ -130,3 +131,33 @@ class TrainedSdm(nn.Module):
         kk = min(self.k, min(self.k, self.n_sub) ** 2)
         self.last_si = si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
         return y
+
+    def residual_fits(self, x, y):
+        """Whether forward_residual serves x + y for this layer: inference, bfloat16, contiguous, width 768, at most
+        core.TABLE_STEP_MAX tokens (a decode step)."""
+        if not x.is_cuda or x.dtype != torch.bfloat16 or self._training(x) or torch.is_autocast_enabled("cuda"):
+            return False
+        wq, _ = self._weights(torch.bfloat16)
+        return core.table_step_residual_fits(x, y, wq, self.values, self.d_a)
+
+    def forward_residual(self, x, y):
+        """The residual add in front of this layer and the layer, inference only: s = x + y (OneSdmLM's
+        x = x + stage(x), track4_onesdm_models.py:540-547), then forward(s); the add, the input norm and the read in
+        one launch (core.table_step_residual).  x, y [..., d] bfloat16, contiguous (residual_fits).  s is written into
+        x with one head.  With keep_picks, last_hx keeps the normed input.  Returns (s, forward(s))."""
+        shape = x.shape
+        x3, y3 = x.reshape(-1, 1, shape[-1]) if x.dim() == 2 else x, y.reshape(-1, 1, shape[-1]) if y.dim() == 2 else y
+        B, T, _ = x3.shape
+        with torch.autocast("cuda", enabled=False):
+            wq, wo = self._weights(torch.bfloat16)
+            prm = self._prm.get(x.device, self.keys1, self.keys2, None, self.log_scale, None, None, None)
+            s, r, si, _, _, q, hx = core.table_step_residual(x3, y3, self.norm.w, self.norm.eps, wq, self.keys1,
+                                                             self.keys2, self.log_scale, self.values, self.k,
+                                                             params=prm, want_q=self.keep_picks,
+                                                             want_hx=self.keep_picks)
+            if self.keep_picks:
+                self.last_q, self.last_hx = q, hx
+            out = core.linear(r, wo, as_matmul=True)
+        kk = min(self.k, min(self.k, self.n_sub) ** 2)
+        self.last_si = si[..., :kk].permute(0, 2, 1, 3).reshape(B * T, self.h, kk)
+        return s.reshape(shape), out.reshape(shape)

@@ -96,6 +96,7 @@ class _Stages:
         for i, sd in enumerate(getattr(m, "sdms", [])):
             sd.keep_picks = True
             self._wrap(sd, "forward", ("sdm", i))
+            self._wrap_residual(sd, ("sdm", i))
         for i, ml in enumerate(getattr(m, "mlps", [])):
             self._wrap(ml, "forward", ("mlp", i))
 
@@ -117,6 +118,19 @@ class _Stages:
             self.rec.setdefault(key, []).append(r)
             return out
         setattr(mod, name, f)
+
+    def _wrap_residual(self, mod, key):
+        """TrainedSdm.forward_residual (the add in front of the layer folded into its table step): the layer's input
+        is the returned sum, its normed input the kernel's hx (last_hx)."""
+        orig = mod.forward_residual
+
+        def f(x, y):
+            s, out = orig(x, y)
+            r = dict(x=s.detach().clone(), hx=mod.last_hx.detach().clone().reshape(s.shape), y=out.detach().clone(),
+                     q=mod.last_q.detach().clone(), picks=mod.last_si)
+            self.rec.setdefault(key, []).append(r)
+            return s, out
+        mod.forward_residual = f
 
     def get(self, key, B):
         rec = self.rec[key]

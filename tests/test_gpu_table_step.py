@@ -67,3 +67,73 @@ def test_trained_sdm_decode_shape_takes_the_one_launch_read():
     assert torch.equal(m.last_q, q_ref)
     assert torch.equal(y_few, y_ref)
     assert y_all.shape == (1, 300, 768) and si_all.shape[0] == 300 and q_all.shape == (1, 300, 32)
+
+
+@pytest.mark.parametrize("H,n_sub,d_a,k,rows,inplace", [(1, 64, 32, 16, 64, True),    # the FULL model's table layer
+                                                        (1, 64, 32, 16, 1, True),
+                                                        (1, 64, 32, 16, 256, False),
+                                                        (1, 64, 32, 16, 7, True),     # a partial group
+                                                        (2, 32, 32, 8, 37, False),    # two heads: not in place
+                                                        (3, 20, 64, 12, 5, False)])
+def test_table_step_residual_equals_add_norm_then_table_step(H, n_sub, d_a, k, rows, inplace):
+    """sdm_rt_table_step_residual (the residual add and TrainedSdm's input norm folded in front of the table step)
+    gives, bit for bit, what sdm_rt_add_rms_norm and then sdm_rt_table_step give: the residual sum, the normed rows,
+    the queries, the picks, scores and weights and the read; x is summed in place only when asked, with one head."""
+    d = 768
+    g = torch.Generator(device="cpu").manual_seed(7 * H + n_sub + d_a + k + rows)
+    dh = d // H
+    x = torch.randn(1, rows, d, generator=g).to(torch.bfloat16).cuda()
+    y = (torch.randn(1, rows, d, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    nw = (1.0 + 0.2 * torch.randn(d, generator=g)).cuda()
+    wq = (torch.randn(H * d_a, d, generator=g) * d ** -0.5).to(torch.bfloat16).cuda()
+    keys1 = torch.randn(H, n_sub, d_a // 2, generator=g).cuda()
+    keys2 = torch.randn(H, n_sub, d_a // 2, generator=g).cuda()
+    log_scale = (torch.full((H,), 2.0) + torch.rand(H, generator=g) * 0.5).cuda()
+    values = torch.randn(H, n_sub * n_sub, dh, generator=g).to(torch.bfloat16).cuda()
+    say("table_step_residual", H, n_sub, d_a, k, rows, inplace)
+    with torch.no_grad():
+        x_ref = x.clone()
+        s_ref, hx_ref = core.add_rms_norm(x_ref, y, nw, 1e-6, out_dtype=torch.bfloat16)
+        r_ref, si_ref, sc_ref, w_ref, q_ref = core.table_step(hx_ref, wq, keys1, keys2, log_scale, values, k,
+                                                              want_q=True)
+        x_in = x.clone()
+        s, r, si, sc, w, q, hx = core.table_step_residual(x_in, y, nw, 1e-6, wq, keys1, keys2, log_scale, values, k,
+                                                          want_q=True, inplace=inplace, want_hx=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref) and torch.equal(hx, hx_ref) and torch.equal(q, q_ref)
+    assert torch.equal(si, si_ref) and torch.equal(sc, sc_ref) and torch.equal(w, w_ref)
+    assert torch.equal(r, r_ref)
+    if inplace and H == 1:
+        assert s.data_ptr() == x_in.data_ptr()
+    else:
+        assert torch.equal(x_in, x), "x changed although the sum was not asked in place"
+
+
+def test_onesdm_decode_with_the_folded_add_equals_the_separate_add():
+    """A OneSdmLM with TrainedSdm layers of width 768 decoding in bfloat16: the steps whose residual adds run inside
+    the table step (TrainedSdm.forward_residual) give the same logits, bit for bit, as the steps with the separate
+    add-and-norm kernel."""
+    from sdmchat_amd import OneSdmLM, TrainedSdm
+    torch.manual_seed(11)
+    m = OneSdmLM(512, d=768, layers=2, heads=4, n_sub=16, d_a=32, k=8, ffn="sdm", sdm_n_sub=32, sdm_heads=1,
+                 sdm_k=16).cuda().to(torch.bfloat16).eval()
+    with torch.no_grad():
+        for sd in m.sdms:
+            sd.values.normal_()
+            sd.wo.weight.normal_(std=0.03)
+        for mm in m.mems:
+            mm.wo.weight.normal_(std=0.03)
+    toks = torch.randint(0, 512, (6, 24), device="cuda")
+    say("onesdm decode, folded add against separate add")
+    outs = []
+    for fold in (True, False):
+        if not fold:
+            for sd in m.sdms:
+                sd.residual_fits = lambda x, y: False
+        st = m.decode_state(24)
+        with torch.no_grad():
+            outs.append(torch.stack([m.step(toks[t], st) for t in range(6)]))
+    for sd in m.sdms:
+        del sd.residual_fits
+    assert torch.equal(outs[0], outs[1])
+    assert torch.isfinite(outs[0].float()).all()

@@ -164,3 +164,20 @@ def test_backward_validation():
     rc = lib.sdm_rt_forward_train(ctypes.byref(dims), ctypes.byref(prm), fake, 768, fake, 768, fake, 768, fake, 12,
                                   F, None, fake, 768, F, None, fake, 1 << 30, None)
     assert rc == -1 and b"saved" in lib.sdm_rt_last_error()
+
+
+def test_table_step_residual_arguments_are_checked_before_launch():
+    """The folded table step takes the layer width 768 only, and sums in place only with one head."""
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    prm = _lib.SdmRtParams(one, one, None, one, None, None, None)
+
+    def call(dims, d, sum_out):
+        return lib.sdm_rt_table_step_residual(ctypes.byref(dims), ctypes.byref(prm), one, d, ctypes.c_void_p(32), d,
+                                              one, 1e-6, sum_out, d, None, 0, d, one, d, one, None, 0, one, None,
+                                              None, one, 4096, None)
+    dims1 = core.make_dims(1, 64, 1, 768, 32, 64, 16, out_norm=False, write_gate=False)
+    assert call(dims1, 512, one) != 0 and "768" in lib.sdm_rt_last_error().decode()
+    dims2 = core.make_dims(1, 64, 2, 384, 32, 32, 8, out_norm=False, write_gate=False)
+    assert call(dims2, 768, one) != 0 and "one head" in lib.sdm_rt_last_error().decode()
+    assert call(dims1, 768, ctypes.c_void_p(32)) != 0 and "alias y" in lib.sdm_rt_last_error().decode()
