@@ -252,309 +252,480 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   const unsigned char* A_b = reinterpret_cast<const unsigned char*>(A);
   unsigned char* A_w = reinterpret_cast<unsigned char*>(A);
 
-  for (int c = 0; c < a.n_chunks; ++c) {
-    const bool fin2 = xnorm && c >= 2;
-    // the next chunk's records, values and variable part are loaded into registers during this chunk (the last
-    // chunk loads its own again)
-    const int cn = min(c + 1, a.n_chunks - 1);
-    uint3 rr_n, wr_n;
-    load_recs(cn, rr_n, wr_n);
-    const VQuad v_n = load_v(cn);
-    const uint2 var_n = load_var(cn, s_sizes[cn]);
-    const int c0 = c * kChunk;
-    const int L = min(kChunk, a.T - c0);
-    const unsigned char* varc = var + (c & 1) * VS;
-    const float* s_vc = s_v + (c & 1) * kChunk * CW;
-    const int bytes = s_sizes[c];
-    const bool all_staged = bytes <= VS;
-    const unsigned char* gvar =
-        plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) + PickGeom::off_var();
-    auto ent_at = [&](int e, auto st) {
-      const int o = PickGeom::off_ent() + 8 * min(max(e, 0), PickGeom::max_entries() - 1);
-      if constexpr (decltype(st)::value) return *reinterpret_cast<const uint2*>(varc + o);
-      else return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
-    };
-    // row v of the staged values, scaled by cf, added to acc (the lane's read order)
-    auto add_vrow = [&](float cf, int v, float (&acc)[32]) {
-      const float* vrow = s_vc + v * CW;
-      VPiece<float> vq[8];
+  // A slab with crowded chunks (a chunk's variable part past the LDS staging area: most positions of the chunk
+  // write the same slots) runs the chunk step whose owners sum their writes before the read barrier (EARLY), so a
+  // crowded wave's writes overlap the other waves' reads; the other slabs the plain step, whose sums after the
+  // barrier hide the partner word's load (the early sums cost varied addresses ~5%).  Both give the same bits.
+  bool crowded = false;
+  for (int i = lane; i < a.n_chunks; i += 64) crowded |= s_sizes[i] > VS;
+  crowded = __ballot(crowded) != 0ull;
+  auto chunk_loop = [&](auto early_t) {
+    constexpr bool EARLY = decltype(early_t)::value;
+    for (int c = 0; c < a.n_chunks; ++c) {
+      const bool fin2 = xnorm && c >= 2;
+      // the next chunk's records, values and variable part are loaded into registers during this chunk (the last
+      // chunk loads its own again)
+      const int cn = min(c + 1, a.n_chunks - 1);
+      uint3 rr_n, wr_n;
+      load_recs(cn, rr_n, wr_n);
+      const VQuad v_n = load_v(cn);
+      const uint2 var_n = load_var(cn, s_sizes[cn]);
+      const int c0 = c * kChunk;
+      const int L = min(kChunk, a.T - c0);
+      const unsigned char* varc = var + (c & 1) * VS;
+      const float* s_vc = s_v + (c & 1) * kChunk * CW;
+      const int bytes = s_sizes[c];
+      const bool all_staged = bytes <= VS;
+      const unsigned char* gvar =
+          plans_s + static_cast<uint32_t>(c) * static_cast<uint32_t>(PickGeom::stride()) + PickGeom::off_var();
+      auto ent_at = [&](int e, auto st) {
+        const int o = PickGeom::off_ent() + 8 * min(max(e, 0), PickGeom::max_entries() - 1);
+        if constexpr (decltype(st)::value) return *reinterpret_cast<const uint2*>(varc + o);
+        else return o + 8 <= VS ? *reinterpret_cast<const uint2*>(varc + o) : *reinterpret_cast<const uint2*>(gvar + o);
+      };
+      // row v of the staged values, scaled by cf, added to acc (the lane's read order)
+      auto add_vrow = [&](float cf, int v, float (&acc)[32]) {
+        const float* vrow = s_vc + v * CW;
+        VPiece<float> vq[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) vq[k].load(vrow + soff[k] / 4);
+        for (int k = 0; k < 8; ++k) vq[k].load(vrow + soff[k] / 4);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) vq[k].fma4(cf, acc + 4 * k);
-    };
+        for (int k = 0; k < 8; ++k) vq[k].fma4(cf, acc + 4 * k);
+      };
 
-    // ---- read: the pick's row, scaled; the in-chunk contribution of this lane's record ----
-    const int rslot = static_cast<int>(rr.x & 0xffffu);
-    const int n_in = static_cast<int>(rr.x >> 24);
-    const float sw = __uint_as_float(rr.y) * (mu * pw[p]);
-    float acc[32];
+      // ---- read: the pick's row, scaled; the in-chunk contribution of this lane's record ----
+      const int rslot = static_cast<int>(rr.x & 0xffffu);
+      const int n_in = static_cast<int>(rr.x >> 24);
+      const float sw = __uint_as_float(rr.y) * (mu * pw[p]);
+      float acc[32];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float4 q4 = *reinterpret_cast<const float4*>(A_b + rslot * (CW * 4) + soff[k]);
-      acc[4 * k] = sw * q4.x;
-      acc[4 * k + 1] = sw * q4.y;
-      acc[4 * k + 2] = sw * q4.z;
-      acc[4 * k + 3] = sw * q4.w;
-    }
-    float dl = sw * cnt[rslot];
-    if (j < n_in) {   // contribution number j of the position
-      const float cc = __uint_as_float(rr.z);
-      add_vrow(cc, static_cast<int>((rr.x >> 16) & 63u), acc);
-      dl += cc;
-    }
-    if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
-      const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
-      auto over = [&](auto st) {
-        if (__ballot(n_in > kPrefetchContribs)) {   // crowded: contributions 8 + j, 16 + j, ... (at most 7: n_in <
-          uint2 ev[7];                                // 64), their entries loaded together first
+      for (int k = 0; k < 8; ++k) {
+        const float4 q4 = *reinterpret_cast<const float4*>(A_b + rslot * (CW * 4) + soff[k]);
+        acc[4 * k] = sw * q4.x;
+        acc[4 * k + 1] = sw * q4.y;
+        acc[4 * k + 2] = sw * q4.z;
+        acc[4 * k + 3] = sw * q4.w;
+      }
+      float dl = sw * cnt[rslot];
+      if (j < n_in) {   // contribution number j of the position
+        const float cc = __uint_as_float(rr.z);
+        add_vrow(cc, static_cast<int>((rr.x >> 16) & 63u), acc);
+        dl += cc;
+      }
+      if (n_in > 8) {   // contributions past the eight in the records (crowded chunks only)
+        const int e0 = reinterpret_cast<const uint16_t*>(varc + 16)[p];   // the position's first entry
+        auto over = [&](auto st) {
+          if (__ballot(n_in > kPrefetchContribs)) {   // crowded: contributions 8 + j, 16 + j, ... (at most 7: n_in <
+            uint2 ev[7];                                // 64), their entries loaded together first
 #pragma unroll
-          for (int t = 0; t < 7; ++t) ev[t] = 8 + j + 8 * t < n_in ? ent_at(e0 + j + 8 * t, st) : make_uint2(0u, 0u);
+            for (int t = 0; t < 7; ++t) ev[t] = 8 + j + 8 * t < n_in ? ent_at(e0 + j + 8 * t, st) : make_uint2(0u, 0u);
 #pragma unroll
-          for (int t = 0; t < 7; ++t) {
-            if (8 + j + 8 * t < n_in) {
-              const float ce = __uint_as_float(ev[t].x);
-              add_vrow(ce, static_cast<int>(ev[t].y & 63u), acc);
+            for (int t = 0; t < 7; ++t) {
+              if (8 + j + 8 * t < n_in) {
+                const float ce = __uint_as_float(ev[t].x);
+                add_vrow(ce, static_cast<int>(ev[t].y & 63u), acc);
+                dl += ce;
+              }
+            }
+          } else {
+            for (int jj = 8 + j; jj < n_in; jj += 8) {
+              const uint2 e = ent_at(e0 + jj - 8, st);
+              const float ce = __uint_as_float(e.x);
+              add_vrow(ce, static_cast<int>(e.y & 63u), acc);
               dl += ce;
             }
           }
-        } else {
-          for (int jj = 8 + j; jj < n_in; jj += 8) {
-            const uint2 e = ent_at(e0 + jj - 8, st);
-            const float ce = __uint_as_float(e.x);
-            add_vrow(ce, static_cast<int>(e.y & 63u), acc);
-            dl += ce;
+        };
+        if (all_staged) over(std::true_type{});
+        else over(std::false_type{});
+      }
+      // the owned write slot's row and count, loaded now (no other lane writes the slot in this chunk; reads of it
+      // by other lanes do not change it), so the write phase after the barrier only adds and stores
+      const int wslot = static_cast<int>(wr.x & 0x7ffu);
+      float y[32];
+      float cw_old = 0.f;
+      if (wslot != M) {
+        const unsigned char* row = A_b + wslot * (CW * 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float4 q4 = *reinterpret_cast<const float4*>(row + soff[k]);
+          y[4 * k] = q4.x;
+          y[4 * k + 1] = q4.y;
+          y[4 * k + 2] = q4.z;
+          y[4 * k + 3] = q4.w;
+        }
+        cw_old = cnt[wslot];
+      }
+      // the eight pieces of value row p in the lane's read order, from the pieces the position's eight lanes staged
+      // (lane x holds piece x): pieces j ^ 1, j ^ 2, j ^ 3 by quad permutes, j ^ 7 by the half-row mirror, and
+      // j ^ 6, j ^ 5, j ^ 4 by the mirror of the first three
+      float vp[32];
+      {
+        const float4 f = as_f4(v_cur);
+        const float x[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t1 = dppf<0xb1>(x[e]), t2 = dppf<0x4e>(x[e]), t3 = dppf<0x1b>(x[e]);
+          vp[e] = x[e];
+          vp[4 + e] = t1;
+          vp[8 + e] = t2;
+          vp[12 + e] = t3;
+          vp[16 + e] = dppf<0x141>(x[e]);
+          vp[20 + e] = dppf<0x141>(t1);
+          vp[24 + e] = dppf<0x141>(t2);
+          vp[28 + e] = dppf<0x141>(t3);
+        }
+      }
+      // reduce-scatter over the eight pick lanes of the position: 32 -> 16 -> 8 -> 4 columns
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[k] += dppf<0x141>(acc[16 + k]);   // row_half_mirror: lane 7 - j
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] += dppf<0x4e>(acc[8 + k]);      // quad_perm [2,3,0,1]: lane j ^ 2
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] += dppf<0xb1>(acc[4 + k]);      // quad_perm [1,0,3,2]: lane j ^ 1
+      float r[4] = {acc[0], acc[1], acc[2], acc[3]};
+      const float den = sum8(dl);
+      if (a.read_mean) {
+        if (a.den_out && g == 0 && j == 0 && p < L) a.den_out[(static_cast<int64_t>(b_row) * a.T + c0 + p) * a.H + h] = den;
+        const float inv = fast_rcp(den + a.read_eps);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] *= inv;
+      }
+      if (a.read_out && p < L) {
+        float* dst = a.read_out + (static_cast<int64_t>(b_row) * a.T + c0 + p) * static_cast<int64_t>(a.H) * a.dh +
+                     static_cast<int64_t>(h) * a.dh + col0 + fcol;
+        store_vals<4, float>(dst, r);
+      }
+      if (norm) {
+        const float ss = sum8(fmaf(r[3], r[3], fmaf(r[2], r[2], fmaf(r[1], r[1], r[0] * r[0]))));
+        if (xnorm) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            rq[2][k] = rq[1][k];
+            rq[1][k] = rq[0][k];
+            rq[0][k] = r[k];
+          }
+          sq[2] = sq[1];
+          sq[1] = sq[0];
+          sq[0] = ss;
+          if (j == 0)
+            __hip_atomic_store(xw + (c * G + g) * kChunk, (1ull << 32) | __float_as_uint(ss), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else if (p < L) {
+          const float inv = fast_rsqrt(ss * inv_dh + a.out_eps);
+          float o[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) o[k] = r[k] * inv * onw[k];
+          store_r(c, o);
+        }
+      } else if (p < L) {
+        store_r(c, r);
+      }
+      float mu_new;              // the slab's scale after this chunk
+      unsigned long long xo;     // the partner's word of chunk c - 2
+      if constexpr (EARLY) {
+      // ---- write, summed before the barrier: the slab is not written until every read of the chunk is done, but
+      // the owners' sums use only their loaded rows, the staged values and the plan, so each wave adds its owned
+      // rows (a crowded wave its teams' rows) while the other waves still read, and stores them after the barrier ----
+      // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
+      const bool chunk_reset = reinterpret_cast<const uint32_t*>(varc)[1] & 0x80000000u;
+      mu_new = mu * (L == kChunk ? lam_chunk : pw[L]);
+      const bool rescale = !chunk_reset && !(mu_new >= kMuFloor);
+      const float slab_scale = mu_new;
+      if (chunk_reset) {   // the slab empties, the owners' loaded rows with it
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] = 0.f;
+        cw_old = 0.f;
+        mu_new = 1.f;
+      } else if (rescale) {   // the slab is rescaled, the owners' loaded rows with it
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] *= mu_new;
+        cw_old *= mu_new;
+        mu_new = 1.f;
+      }
+      const float inv_mu = fast_rcp(mu_new);
+      // every owner adds its own faded value to its loaded row
+      float cw = cw_old;
+      if (wslot != M) {
+        const float a0 = __uint_as_float(wr.y) * inv_mu;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] = fmaf(a0, vp[k], y[k]);
+        cw += a0;
+      }
+      const int n_l_own = wslot != M ? static_cast<int>((wr.x >> 17) & 63u) : 0;
+      const bool teams = __ballot(n_l_own >= kTeamWriters);
+      // the teams of a crowded wave (as in the plain step): team j, the lanes of pick j of the wave's eight positions,
+      // sums the owned slots of its members one after another and leaves each lane one four-column piece (h4) of the
+      // member's row and the team the slot's count (ct)
+      const unsigned long long owners = __ballot(wslot != M);
+      const int mi = lane >> 3;   // the lane's member index in its team
+      auto team_member = [&](int k, float (&h4)[4], float& ct, int& mslot) {
+        const int src = 8 * k + j;
+        const uint32_t mx = static_cast<uint32_t>(__shfl(static_cast<int>(wr.x), src));
+        const uint32_t mz = static_cast<uint32_t>(__shfl(static_cast<int>(wr.z), src));
+        mslot = static_cast<int>(mx & 0x7ffu);
+        float part[32];
+        float cwp = 0.f;
+        const bool self = mi == k && mslot != M;   // the member itself: its row with its own value added
+#pragma unroll
+        for (int q = 0; q < 32; ++q) part[q] = self ? y[q] : 0.f;
+        if (self) cwp = cw;
+        if (mslot != M) {   // later writers mi, mi + 8, ...: 0 is the inline one, i > 0 entry w_e0 + i - 1
+          const int n_l = static_cast<int>((mx >> 17) & 63u);
+          const int w_e0 = static_cast<int>(mx >> 23);
+          for (int i = mi; i < n_l; i += 8) {
+            const uint2 it = i == 0 ? make_uint2(mz, (mx >> 11) & 63u) : ent_at(w_e0 + i - 1, std::false_type{});
+            const float ae = __uint_as_float(it.x) * inv_mu;
+            add_vrow(ae, static_cast<int>(it.y & 63u), part);
+            cwp += ae;
           }
         }
-      };
-      if (all_staged) over(std::true_type{});
-      else over(std::false_type{});
-    }
-    // the owned write slot's row and count, loaded now (no other lane writes the slot in this chunk; reads of it
-    // by other lanes do not change it), so the write phase after the barrier only adds and stores
-    const int wslot = static_cast<int>(wr.x & 0x7ffu);
-    float y[32];
-    float cw_old = 0.f;
-    if (wslot != M) {
-      const unsigned char* row = A_b + wslot * (CW * 4);
+        // over the team: lanes 32 apart (32 -> 16 values), 16 apart (-> 8), 8 apart (-> 4)
+        float h16[16];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float4 q4 = *reinterpret_cast<const float4*>(row + soff[k]);
-        y[4 * k] = q4.x;
-        y[4 * k + 1] = q4.y;
-        y[4 * k + 2] = q4.z;
-        y[4 * k + 3] = q4.w;
-      }
-      cw_old = cnt[wslot];
-    }
-    // the eight pieces of value row p in the lane's read order, from the pieces the position's eight lanes staged
-    // (lane x holds piece x): pieces j ^ 1, j ^ 2, j ^ 3 by quad permutes, j ^ 7 by the half-row mirror, and
-    // j ^ 6, j ^ 5, j ^ 4 by the mirror of the first three
-    float vp[32];
-    {
-      const float4 f = as_f4(v_cur);
-      const float x[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float t1 = dppf<0xb1>(x[e]), t2 = dppf<0x4e>(x[e]), t3 = dppf<0x1b>(x[e]);
-        vp[e] = x[e];
-        vp[4 + e] = t1;
-        vp[8 + e] = t2;
-        vp[12 + e] = t3;
-        vp[16 + e] = dppf<0x141>(x[e]);
-        vp[20 + e] = dppf<0x141>(t1);
-        vp[24 + e] = dppf<0x141>(t2);
-        vp[28 + e] = dppf<0x141>(t3);
-      }
-    }
-    // reduce-scatter over the eight pick lanes of the position: 32 -> 16 -> 8 -> 4 columns
-#pragma unroll
-    for (int k = 0; k < 16; ++k) acc[k] += dppf<0x141>(acc[16 + k]);   // row_half_mirror: lane 7 - j
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] += dppf<0x4e>(acc[8 + k]);      // quad_perm [2,3,0,1]: lane j ^ 2
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] += dppf<0xb1>(acc[4 + k]);      // quad_perm [1,0,3,2]: lane j ^ 1
-    float r[4] = {acc[0], acc[1], acc[2], acc[3]};
-    const float den = sum8(dl);
-    if (a.read_mean) {
-      if (a.den_out && g == 0 && j == 0 && p < L) a.den_out[(static_cast<int64_t>(b_row) * a.T + c0 + p) * a.H + h] = den;
-      const float inv = fast_rcp(den + a.read_eps);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) r[k] *= inv;
-    }
-    if (a.read_out && p < L) {
-      float* dst = a.read_out + (static_cast<int64_t>(b_row) * a.T + c0 + p) * static_cast<int64_t>(a.H) * a.dh +
-                   static_cast<int64_t>(h) * a.dh + col0 + fcol;
-      store_vals<4, float>(dst, r);
-    }
-    if (norm) {
-      const float ss = sum8(fmaf(r[3], r[3], fmaf(r[2], r[2], fmaf(r[1], r[1], r[0] * r[0]))));
-      if (xnorm) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          rq[2][k] = rq[1][k];
-          rq[1][k] = rq[0][k];
-          rq[0][k] = r[k];
+        for (int q = 0; q < 16; ++q) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[q]), __float_as_uint(part[16 + q]),
+                                                           false, false);
+          h16[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);   // lane < 32: values q, else 16 + q
         }
-        sq[2] = sq[1];
-        sq[1] = sq[0];
-        sq[0] = ss;
-        if (j == 0)
-          __hip_atomic_store(xw + (c * G + g) * kChunk, (1ull << 32) | __float_as_uint(ss), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      } else if (p < L) {
-        const float inv = fast_rsqrt(ss * inv_dh + a.out_eps);
-        float o[4];
+        const bool b4 = lane & 16, b3 = lane & 8;
+        float h8[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = r[k] * inv * onw[k];
-        store_r(c, o);
-      }
-    } else if (p < L) {
-      store_r(c, r);
-    }
-    lds_barrier();
-    // the partner's partial sums of chunk c - 2 (used when it finishes, at the end of this chunk)
-    const unsigned long long xo = (fin2 && G == 2) ? xget(c - 2, 1 - g) : 0ull;
-    // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
-    const bool chunk_reset = reinterpret_cast<const uint32_t*>(varc)[1] & 0x80000000u;
-    float mu_new = mu * (L == kChunk ? lam_chunk : pw[L]);
-    if (chunk_reset) {   // the slab empties, the owners' loaded rows with it
-      float4* a4 = reinterpret_cast<float4*>(A);
-      for (int i = tid; i < (M + 1) * CW / 4; i += NT) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int i = tid; i <= M; i += NT) cnt[i] = 0.f;
+        for (int q = 0; q < 8; ++q) {
+          const float keep = b4 ? h16[8 + q] : h16[q];
+          h8[q] = keep + __shfl_xor(b4 ? h16[q] : h16[8 + q], 16);
+        }
 #pragma unroll
-      for (int k = 0; k < 32; ++k) y[k] = 0.f;
-      cw_old = 0.f;
-      mu_new = 1.f;
-      lds_barrier();
-    } else if (!(mu_new >= kMuFloor)) {   // the slab is rescaled, the owners' loaded rows with it
-      float4* a4 = reinterpret_cast<float4*>(A);
-      for (int i = tid; i < (M + 1) * CW / 4; i += NT) {
-        const float4 t = a4[i];
-        a4[i] = make_float4(t.x * mu_new, t.y * mu_new, t.z * mu_new, t.w * mu_new);
-      }
-      for (int i = tid; i <= M; i += NT) cnt[i] *= mu_new;
+        for (int q = 0; q < 4; ++q) {
+          const float keep = b3 ? h8[4 + q] : h8[q];
+          h4[q] = keep + __int_as_float(__builtin_amdgcn_update_dpp(
+                             0, __float_as_int(b3 ? h8[q] : h8[4 + q]), 0x128, 0xf, 0xf, false));   // row_ror:8
+        }
+        ct = cwp;
+        ct += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ct), 0x128, 0xf, 0xf, false));
+        ct += __shfl_xor(ct, 16);
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
+          ct = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+      };
+      // the team's store of member k's slot: the lane's piece (number mi of the read order) and the count
+      auto team_store = [&](int k, const float (&h4)[4], float ct, int mslot) {
+        if (mslot != M) {
+          const int piece = j ^ (mi < 4 ? mi : 11 - mi);
+          *reinterpret_cast<float4*>(A_w + mslot * (CW * 4) + 16 * piece) = make_float4(h4[0], h4[1], h4[2], h4[3]);
+          if (mi == k) cnt[mslot] = ct;
+        }
+      };
+      uint32_t members = 0;   // members with owned slots (bit k: member k)
 #pragma unroll
-      for (int k = 0; k < 32; ++k) y[k] *= mu_new;
-      cw_old *= mu_new;
-      mu_new = 1.f;
-      lds_barrier();
-    }
-    // ---- write: the owner lanes add their faded values and those of the slot's later writers ----
-    const float inv_mu = fast_rcp(mu_new);
-    // every owner adds its own faded value to its loaded row
-    float cw = cw_old;
-    if (wslot != M) {
-      const float a0 = __uint_as_float(wr.y) * inv_mu;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) y[k] = fmaf(a0, vp[k], y[k]);
-      cw += a0;
-    }
-    const int n_l_own = wslot != M ? static_cast<int>((wr.x >> 17) & 63u) : 0;
-    if (!__ballot(n_l_own >= kTeamWriters)) {
-      if (wslot != M) {   // the owner adds the slot's later writers and stores the row
-        const int n_l = n_l_own;
-        unsigned char* row = A_w + wslot * (CW * 4);
-        if (n_l > 0) {
+      for (int k = 0; k < 8; ++k) members |= ((owners >> (8 * k)) & 0xffull) ? (1u << k) : 0u;
+      // a team wave of one member (where every position of the chunk writes the same slots) sums it now
+      const bool team_now = teams && __builtin_popcount(members) == 1;
+      const int k1 = members ? __builtin_ctz(members) : 0;
+      float h4a[4], cta;   // set and used only when team_now
+      int msa;
+      if (!teams) {
+        if (wslot != M && n_l_own > 0) {   // the owner adds the slot's later writers
           const float a1 = __uint_as_float(wr.z) * inv_mu;
           add_vrow(a1, static_cast<int>((wr.x >> 11) & 63u), y);
           cw += a1;
-          if (n_l > 1) {   // later writers past the first, from the variable part
-            const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
-            auto later = [&](auto st) {
-              for (int e = 0; e < n_l - 1; ++e) {
-                const uint2 en = ent_at(w_e0 + e, st);
-                const float ae = __uint_as_float(en.x) * inv_mu;
-                add_vrow(ae, static_cast<int>(en.y & 63u), y);
-                cw += ae;
-              }
-            };
-            if (all_staged) later(std::true_type{});
-            else later(std::false_type{});
+          const int w_e0 = static_cast<int>(wr.x >> 23);   // the later writers past the first, among the entries
+          for (int e = 0; e < n_l_own - 1; ++e) {
+            const uint2 en = ent_at(w_e0 + e, std::false_type{});
+            const float ae = __uint_as_float(en.x) * inv_mu;
+            add_vrow(ae, static_cast<int>(en.y & 63u), y);
+            cw += ae;
           }
         }
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
-        cnt[wslot] = cw;
+      } else if (team_now) {
+        team_member(k1, h4a, cta, msa);
       }
-    } else {
-      // A wave with a slot of many later writers (crowded addresses) writes as eight teams: team j, the lanes of
-      // pick j of the wave's eight positions, takes the owned slots of its members one after another; the member's
-      // row (its own value added) and the slot's later writers (every eighth, from the member's index in the team)
-      // are summed per lane, then over the team (lanes 8 apart) by a fixed butterfly that leaves each lane one
-      // four-column piece of the row, which it stores.
-      const unsigned long long owners = __ballot(wslot != M);
-      const int mi = lane >> 3;   // the lane's member index in its team
-      auto team = [&](auto st) {
-        for (int k = 0; k < 8; ++k) {
-          if (!((owners >> (8 * k)) & 0xffull)) continue;   // no owner among the teams' members k
-          const int src = 8 * k + j;
-          const uint32_t mx = static_cast<uint32_t>(__shfl(static_cast<int>(wr.x), src));
-          const uint32_t mz = static_cast<uint32_t>(__shfl(static_cast<int>(wr.z), src));
-          const int mslot = static_cast<int>(mx & 0x7ffu);
-          float part[32];
-          float cwp = 0.f;
-          const bool self = mi == k && mslot != M;   // the member itself: its row with its own value added
+      lds_barrier();
+      // the partner's partial sums of chunk c - 2 (used when it finishes, at the end of this chunk)
+      xo = (fin2 && G == 2) ? xget(c - 2, 1 - g) : 0ull;
+      if (chunk_reset) {
+        float4* a4 = reinterpret_cast<float4*>(A);
+        for (int i = tid; i < (M + 1) * CW / 4; i += NT) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = tid; i <= M; i += NT) cnt[i] = 0.f;
+        lds_barrier();
+      } else if (rescale) {
+        float4* a4 = reinterpret_cast<float4*>(A);
+        for (int i = tid; i < (M + 1) * CW / 4; i += NT) {
+          const float4 t = a4[i];
+          a4[i] = make_float4(t.x * slab_scale, t.y * slab_scale, t.z * slab_scale, t.w * slab_scale);
+        }
+        for (int i = tid; i <= M; i += NT) cnt[i] *= slab_scale;
+        lds_barrier();
+      }
+      // ---- write, stored: every owned slot has one owner (or one team), so the rows are written in a fixed order ----
+      if (!teams) {
+        if (wslot != M) {
+          unsigned char* row = A_w + wslot * (CW * 4);
 #pragma unroll
-          for (int q = 0; q < 32; ++q) part[q] = self ? y[q] : 0.f;
-          if (self) cwp = cw;
-          if (mslot != M) {   // later writers mi, mi + 8, ...: 0 is the inline one, i > 0 entry w_e0 + i - 1
-            const int n_l = static_cast<int>((mx >> 17) & 63u);
-            const int w_e0 = static_cast<int>(mx >> 23);
-            for (int i = mi; i < n_l; i += 8) {
-              const uint2 it = i == 0 ? make_uint2(mz, (mx >> 11) & 63u) : ent_at(w_e0 + i - 1, st);
-              const float ae = __uint_as_float(it.x) * inv_mu;
-              add_vrow(ae, static_cast<int>(it.y & 63u), part);
-              cwp += ae;
+          for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+          cnt[wslot] = cw;
+        }
+      } else if (team_now) {
+        team_store(k1, h4a, cta, msa);
+      } else {
+        for (int k = 0; k < 8; ++k) {   // several members: each summed and stored in turn, after the barrier
+          if (!((members >> k) & 1u)) continue;
+          float h4[4], ct;
+          int ms;
+          team_member(k, h4, ct, ms);
+          team_store(k, h4, ct, ms);
+        }
+      }
+      } else {
+      lds_barrier();
+      // the partner's partial sums of chunk c - 2 (used when it finishes, at the end of this chunk)
+      xo = (fin2 && G == 2) ? xget(c - 2, 1 - g) : 0ull;
+      // fade the slab by lam^L (folded into mu; rescale the slab when mu gets small); a chunk with a reset empties it
+      const bool chunk_reset = reinterpret_cast<const uint32_t*>(varc)[1] & 0x80000000u;
+      mu_new = mu * (L == kChunk ? lam_chunk : pw[L]);
+      if (chunk_reset) {   // the slab empties, the owners' loaded rows with it
+        float4* a4 = reinterpret_cast<float4*>(A);
+        for (int i = tid; i < (M + 1) * CW / 4; i += NT) a4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = tid; i <= M; i += NT) cnt[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] = 0.f;
+        cw_old = 0.f;
+        mu_new = 1.f;
+        lds_barrier();
+      } else if (!(mu_new >= kMuFloor)) {   // the slab is rescaled, the owners' loaded rows with it
+        float4* a4 = reinterpret_cast<float4*>(A);
+        for (int i = tid; i < (M + 1) * CW / 4; i += NT) {
+          const float4 t = a4[i];
+          a4[i] = make_float4(t.x * mu_new, t.y * mu_new, t.z * mu_new, t.w * mu_new);
+        }
+        for (int i = tid; i <= M; i += NT) cnt[i] *= mu_new;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] *= mu_new;
+        cw_old *= mu_new;
+        mu_new = 1.f;
+        lds_barrier();
+      }
+      // ---- write: the owner lanes add their faded values and those of the slot's later writers ----
+      const float inv_mu = fast_rcp(mu_new);
+      // every owner adds its own faded value to its loaded row
+      float cw = cw_old;
+      if (wslot != M) {
+        const float a0 = __uint_as_float(wr.y) * inv_mu;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) y[k] = fmaf(a0, vp[k], y[k]);
+        cw += a0;
+      }
+      const int n_l_own = wslot != M ? static_cast<int>((wr.x >> 17) & 63u) : 0;
+      if (!__ballot(n_l_own >= kTeamWriters)) {
+        if (wslot != M) {   // the owner adds the slot's later writers and stores the row
+          const int n_l = n_l_own;
+          unsigned char* row = A_w + wslot * (CW * 4);
+          if (n_l > 0) {
+            const float a1 = __uint_as_float(wr.z) * inv_mu;
+            add_vrow(a1, static_cast<int>((wr.x >> 11) & 63u), y);
+            cw += a1;
+            if (n_l > 1) {   // later writers past the first, from the variable part
+              const int w_e0 = static_cast<int>(wr.x >> 23);   // the first of them among the entries
+              auto later = [&](auto st) {
+                for (int e = 0; e < n_l - 1; ++e) {
+                  const uint2 en = ent_at(w_e0 + e, st);
+                  const float ae = __uint_as_float(en.x) * inv_mu;
+                  add_vrow(ae, static_cast<int>(en.y & 63u), y);
+                  cw += ae;
+                }
+              };
+              if (all_staged) later(std::true_type{});
+              else later(std::false_type{});
             }
           }
-          // over the team: lanes 32 apart (32 -> 16 values), 16 apart (-> 8), 8 apart (-> 4)
-          float h16[16];
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[q]), __float_as_uint(part[16 + q]),
-                                                             false, false);
-            h16[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);   // lane < 32: values q, else 16 + q
-          }
-          const bool b4 = lane & 16, b3 = lane & 8;
-          float h8[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float keep = b4 ? h16[8 + q] : h16[q];
-            h8[q] = keep + __shfl_xor(b4 ? h16[q] : h16[8 + q], 16);
-          }
-          float h4[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float keep = b3 ? h8[4 + q] : h8[q];
-            h4[q] = keep + __int_as_float(__builtin_amdgcn_update_dpp(
-                               0, __float_as_int(b3 ? h8[q] : h8[4 + q]), 0x128, 0xf, 0xf, false));   // row_ror:8
-          }
-          float ct = cwp;
-          ct += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ct), 0x128, 0xf, 0xf, false));
-          ct += __shfl_xor(ct, 16);
-          {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
-            ct = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-          }
-          if (mslot != M) {   // the lane's piece: number mi of the read order
-            const int piece = j ^ (mi < 4 ? mi : 11 - mi);
-            *reinterpret_cast<float4*>(A_w + mslot * (CW * 4) + 16 * piece) = make_float4(h4[0], h4[1], h4[2], h4[3]);
-            if (mi == k) cnt[mslot] = ct;
-          }
+          for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<float4*>(row + soff[k]) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+          cnt[wslot] = cw;
         }
-      };
-      team(std::false_type{});   // rare: one instance, the entries staged or not
+      } else {
+        // A wave with a slot of many later writers (crowded addresses) writes as eight teams: team j, the lanes of
+        // pick j of the wave's eight positions, takes the owned slots of its members one after another; the member's
+        // row (its own value added) and the slot's later writers (every eighth, from the member's index in the team)
+        // are summed per lane, then over the team (lanes 8 apart) by a fixed butterfly that leaves each lane one
+        // four-column piece of the row, which it stores.
+        const unsigned long long owners = __ballot(wslot != M);
+        const int mi = lane >> 3;   // the lane's member index in its team
+        auto team = [&](auto st) {
+          for (int k = 0; k < 8; ++k) {
+            if (!((owners >> (8 * k)) & 0xffull)) continue;   // no owner among the teams' members k
+            const int src = 8 * k + j;
+            const uint32_t mx = static_cast<uint32_t>(__shfl(static_cast<int>(wr.x), src));
+            const uint32_t mz = static_cast<uint32_t>(__shfl(static_cast<int>(wr.z), src));
+            const int mslot = static_cast<int>(mx & 0x7ffu);
+            float part[32];
+            float cwp = 0.f;
+            const bool self = mi == k && mslot != M;   // the member itself: its row with its own value added
+#pragma unroll
+            for (int q = 0; q < 32; ++q) part[q] = self ? y[q] : 0.f;
+            if (self) cwp = cw;
+            if (mslot != M) {   // later writers mi, mi + 8, ...: 0 is the inline one, i > 0 entry w_e0 + i - 1
+              const int n_l = static_cast<int>((mx >> 17) & 63u);
+              const int w_e0 = static_cast<int>(mx >> 23);
+              for (int i = mi; i < n_l; i += 8) {
+                const uint2 it = i == 0 ? make_uint2(mz, (mx >> 11) & 63u) : ent_at(w_e0 + i - 1, st);
+                const float ae = __uint_as_float(it.x) * inv_mu;
+                add_vrow(ae, static_cast<int>(it.y & 63u), part);
+                cwp += ae;
+              }
+            }
+            // over the team: lanes 32 apart (32 -> 16 values), 16 apart (-> 8), 8 apart (-> 4)
+            float h16[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[q]), __float_as_uint(part[16 + q]),
+                                                               false, false);
+              h16[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);   // lane < 32: values q, else 16 + q
+            }
+            const bool b4 = lane & 16, b3 = lane & 8;
+            float h8[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float keep = b4 ? h16[8 + q] : h16[q];
+              h8[q] = keep + __shfl_xor(b4 ? h16[q] : h16[8 + q], 16);
+            }
+            float h4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float keep = b3 ? h8[4 + q] : h8[q];
+              h4[q] = keep + __int_as_float(__builtin_amdgcn_update_dpp(
+                                 0, __float_as_int(b3 ? h8[q] : h8[4 + q]), 0x128, 0xf, 0xf, false));   // row_ror:8
+            }
+            float ct = cwp;
+            ct += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ct), 0x128, 0xf, 0xf, false));
+            ct += __shfl_xor(ct, 16);
+            {
+              const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
+              ct = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            }
+            if (mslot != M) {   // the lane's piece: number mi of the read order
+              const int piece = j ^ (mi < 4 ? mi : 11 - mi);
+              *reinterpret_cast<float4*>(A_w + mslot * (CW * 4) + 16 * piece) = make_float4(h4[0], h4[1], h4[2], h4[3]);
+              if (mi == k) cnt[mslot] = ct;
+            }
+          }
+        };
+        team(std::false_type{});   // rare: one instance, the entries staged or not
+      }
+      }
+      mu = mu_new;
+      rr = rr_n;
+      wr = wr_n;
+      v_cur = v_n;
+      stage(c + 1, v_n, var_n);   // buffer (c + 1) & 1 held chunk c - 1, done before the last barrier
+      if (fin2) finish(c - 2, rq[2], sq[2], xo);
+      lds_barrier();
     }
-    mu = mu_new;
-    rr = rr_n;
-    wr = wr_n;
-    v_cur = v_n;
-    stage(c + 1, v_n, var_n);   // buffer (c + 1) & 1 held chunk c - 1, done before the last barrier
-    if (fin2) finish(c - 2, rq[2], sq[2], xo);
-    lds_barrier();
-  }
+  };
+  if (crowded) chunk_loop(std::true_type{});
+  else chunk_loop(std::false_type{});
   if (xnorm) {   // the last two chunks (or one)
     const int n = a.n_chunks;
     if (n >= 2) finish(n - 2, rq[1], sq[1], G == 2 ? xget(n - 2, 1 - g) : 0ull);
