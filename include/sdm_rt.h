@@ -19,9 +19,9 @@
  *   - Every call is asynchronous on the given stream (a hipStream_t passed as void*; NULL is the null stream)
  *     and returns 0 on success or a negative status; sdm_rt_last_error() then describes the failure (a
  *     thread-local string).  Arguments are validated before anything is launched.
- *   - Calls keep their state in the caller's buffers and workspace, with two exceptions: the scratch array of
- *     sdm_rt_forward_noalloc (one per device, shared by every call of that entry point) and the wait limit of
- *     sdm_rt_set_wait_limit (one per process).
+ *   - Calls keep their state in the caller's buffers and workspace, with three exceptions: the scratch array of
+ *     sdm_rt_forward_noalloc (one per device, shared by every call of that entry point), the wait limit of
+ *     sdm_rt_set_wait_limit and the threshold of sdm_rt_set_crowded_threshold (one each per process).
  *   - Concurrency: the forward's scan runs the column groups of one (batch row, head) slab on different compute
  *     units, and each waits (a bounded spin) for the others' partial sums of the out-norm.  Calls on different
  *     streams with different workspaces compute the same results, provided the groups of a slab can be resident
@@ -159,6 +159,13 @@ int sdm_rt_status(const sdm_rt_dims* dims, const void* workspace, void* stream);
  * about a second), 0 makes every wait give up at once without looking at the partner's sum (for tests of the
  * error path: every kernel still runs to its end).  No reference counterpart. */
 void sdm_rt_set_wait_limit(int64_t polls);
+
+/* The forward's pick scan runs a (batch row, head) slab whose chunks crowd (a chunk's plan has a variable part of
+ * more than `bytes` bytes: many positions write the same slots) with its owners' write sums ahead of the barrier
+ * that ends a chunk's reads; the results are the same bits either way, only the time differs.  For the whole
+ * process: bytes < 0 restores the default (4,096, the part staged in LDS), a large value keeps every slab on the
+ * plain chunk step.  No reference counterpart. */
+void sdm_rt_set_crowded_threshold(int32_t bytes);
 
 /* Bytes of workspace sdm_rt_decode_step needs (the picks of one token per stream; 0 on invalid dims). */
 size_t sdm_rt_decode_workspace_bytes(const sdm_rt_dims* dims);

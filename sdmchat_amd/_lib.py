@@ -146,6 +146,7 @@ SIGNATURES = {
                                              c_void_p, ctypes.c_size_t, c_void_p]),
     "sdm_rt_status": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), c_void_p, c_void_p]),
     "sdm_rt_set_wait_limit": (None, [c_i64]),
+    "sdm_rt_set_crowded_threshold": (None, [ctypes.c_int32]),
     "sdm_rt_last_error": (ctypes.c_char_p, []),
 }
 

@@ -237,6 +237,13 @@ def set_wait_limit(polls):
     _lib.load().sdm_rt_set_wait_limit(-1 if polls is None else int(polls))
 
 
+def set_crowded_threshold(nbytes):
+    """The plan size above which the forward's pick scan treats a slab as crowded and sums its owners' writes before
+    the read barrier, process-wide (sdm_rt_set_crowded_threshold): None or a negative value restores the default
+    (4,096 bytes); the results are the same bits either way."""
+    _lib.load().sdm_rt_set_crowded_threshold(-1 if nbytes is None else int(nbytes))
+
+
 def table_read(slots, weights, values, k, out_dtype=torch.float32, out=None):
     """The weighted read of picked table rows (TrainedSdm.forward's embedding_bag, track4_onesdm_models.py:448-455).
 

@@ -10,6 +10,8 @@ namespace sdmrt {
 
 static std::atomic<uint32_t> g_wait_limit{kSpinLimit};
 uint32_t wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+static std::atomic<int> g_crowded_bytes{kVarStage};
+int crowded_threshold() { return g_crowded_bytes.load(std::memory_order_relaxed); }
 
 // the status word a forward's scan leaves in its workspace (after the progress counters)
 static size_t status_offset(const Plan& p) {
@@ -109,6 +111,7 @@ int run_core(const Plan& p, const sdm_rt_dims* dims, const sdm_rt_params* prm, c
   if (pick)   // the pick scan loads four values at a time
     s.v_direct = reinterpret_cast<uintptr_t>(io.v) % (4 * vb) == 0 && io.v_stride % 4 == 0;
   s.spin_limit = wait_limit();
+  s.crowded_bytes = crowded_threshold();
   s.read_mean = dims->read_mean;
   s.read_eps = dims->read_eps;
   s.out_eps = dims->out_norm_eps;
@@ -139,6 +142,10 @@ size_t sdm_rt_gate_copy_offset(const sdm_rt_dims* dims) {
 void sdm_rt_set_wait_limit(int64_t polls) {
   g_wait_limit.store(polls < 0 ? kSpinLimit : static_cast<uint32_t>(std::min<int64_t>(polls, 0xffffffffll)),
                      std::memory_order_relaxed);
+}
+
+void sdm_rt_set_crowded_threshold(int32_t bytes) {
+  g_crowded_bytes.store(bytes < 0 ? kVarStage : bytes, std::memory_order_relaxed);
 }
 
 int sdm_rt_status(const sdm_rt_dims* dims, const void* workspace, void* stream) {

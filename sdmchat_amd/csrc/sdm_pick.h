@@ -252,12 +252,13 @@ __global__ void __launch_bounds__(kPickThreads) pick_scan_kernel(ScanArgs a) {
   const unsigned char* A_b = reinterpret_cast<const unsigned char*>(A);
   unsigned char* A_w = reinterpret_cast<unsigned char*>(A);
 
-  // A slab with crowded chunks (a chunk's variable part past the LDS staging area: most positions of the chunk
-  // write the same slots) runs the chunk step whose owners sum their writes before the read barrier (EARLY), so a
-  // crowded wave's writes overlap the other waves' reads; the other slabs the plain step, whose sums after the
-  // barrier hide the partner word's load (the early sums cost varied addresses ~5%).  Both give the same bits.
+  // A slab with crowded chunks (a chunk's variable part past a.crowded_bytes, by default the LDS staging area: most
+  // positions of the chunk write the same slots) runs the chunk step whose owners sum their writes before the read
+  // barrier (EARLY), so a crowded wave's writes overlap the other waves' reads; the other slabs the plain step, whose
+  // sums after the barrier hide the partner word's load (the early sums cost varied addresses ~5%).  Both give the
+  // same bits.
   bool crowded = false;
-  for (int i = lane; i < a.n_chunks; i += 64) crowded |= s_sizes[i] > VS;
+  for (int i = lane; i < a.n_chunks; i += 64) crowded |= s_sizes[i] > a.crowded_bytes;
   crowded = __ballot(crowded) != 0ull;
   auto chunk_loop = [&](auto early_t) {
     constexpr bool EARLY = decltype(early_t)::value;

@@ -42,12 +42,15 @@ struct ScanArgs {
   int v_direct;                // 1: value rows are 16-byte aligned and copied into LDS directly
   float read_eps, out_eps;
   uint32_t spin_limit;         // polls of a partner's progress before a wait gives up (0: give up at once)
+  int crowded_bytes;           // pick scan: a chunk plan's variable part past this makes its slab crowded
 };
 
 constexpr uint32_t kSpinLimit = 1u << 20;   // the default polls of a partner's progress before a wait gives up
 
 // the polls a wait makes before it gives up, process-wide (sdm_rt_set_wait_limit)
 uint32_t wait_limit();
+// the pick scan's crowded-slab threshold in plan bytes, process-wide (sdm_rt_set_crowded_threshold)
+int crowded_threshold();
 
 // CPL consecutive float values from LDS in one access
 template <int CPL>

@@ -249,6 +249,40 @@ def test_repeated_tokens_crowd_every_chunk(pattern):
     np.testing.assert_allclose(cnt, c64, atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_crowded_slabs_early_write_sums_give_the_same_bits(dtype):
+    """A slab with a crowded chunk (a plan's variable part past 4 KB) runs the chunk step whose owners sum their
+    writes before the read barrier; that step and the plain one give the same bits.  Batch rows of one repeated
+    token (crowded) beside rows of varied tokens, with resets and a fade that rescales the slab every chunk: the
+    read-out and the final state with the default threshold, with every slab on the plain step and with every slab
+    on the early step are equal bit for bit."""
+    from sdmchat_amd import core
+    B, T, H, dh, n_sub = 4, 300, 4, 64, 16
+    kz, qz, V, g, p = core_inputs(B, T, H, dh, 32, n_sub, seed=307, decays=(0.0, 0.3, 0.97, 1.0))
+    for arr in (kz, qz, g):   # rows 0 and 2: one repeated token
+        arr[0] = arr[0, :1]
+        arr[2] = arr[2, :1]
+    reset = np.zeros((B, T), bool)
+    reset[0, [70, 200]] = True
+    reset[1, [5, 64]] = True
+    if dtype == torch.bfloat16:
+        kz, qz, V, g = (bf16_round(a) for a in (kz, qz, V, g))
+    outs = []
+    try:
+        for nbytes in (None, 1 << 30, 0):   # default, every slab plain, every slab early
+            core.set_crowded_threshold(nbytes)
+            say("crowded threshold", nbytes, dtype)
+            outs.append(gpu_core(kz, qz, V, g, p, 8, dtype=dtype, want_state=True, reset=reset))
+    finally:
+        core.set_crowded_threshold(None)
+    (r0, (m0, c0)) = outs[0]
+    for r, (m, c) in outs[1:]:
+        assert np.array_equal(r.view(np.uint32), r0.view(np.uint32))
+        assert np.array_equal(m.view(np.uint32), m0.view(np.uint32))
+        assert np.array_equal(c.view(np.uint32), c0.view(np.uint32))
+    assert np.isfinite(r0).all()
+
+
 def test_bench_shape_one_repeated_token_bf16():
     """The bench shape with one repeated token per batch row (every chunk: 8 slots of 63 later writers, positions of
     up to 63 in-chunk contributions, variable parts past the staged 4 KB), bf16: every pick against the oracle and
