@@ -545,10 +545,45 @@ __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf
 // enters through the accumulator's start value c_i = k_i . addr_b (one float32 matrix step: c_i x 1) and through
 // inv.  Lane l feeds dims 16q + 8(l/32) + e (e < 8) of sub-key row l%32 and of both address rows (HALF = 8: lanes
 // 32..63 feed zeros).  Head h's address columns start at column zcol of a row (h * 2 HALF when zcol < 0).
+// The lane's sub-key piece and address-bias piece of half_scores_bf16 (loaded ahead by a caller whose addresses
+// come from LDS, so that the loads leave the scoring's critical path).
+template <int HALF>
+struct SubKeyPiece {
+  static constexpr int Q = (HALF + 15) / 16;
+  float ka[Q][8], ab[Q][8];
+};
+template <int HALF>
+__device__ __forceinline__ void load_sub_key_piece(const AddrGeom& g, int h, int hf, int kofs, SubKeyPiece<HALF>& kp) {
+  constexpr int Q = SubKeyPiece<HALF>::Q;
+  const int l = threadIdx.x & 63;
+  const int kb = l >> 5, jl = l & 31;
+  const bool has = HALF >= 16 || kb == 0;
+  const int d0 = hf * HALF + 8 * kb;
+  const int kr = kofs + jl;
+  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + 8 * kb;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if (has) {
+      load_vals<8, float>(krow + 16 * q, kp.ka[q]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kp.ka[q][e] = 0.f;
+    }
+    if (g.addr_b && has) {
+      load_vals<8, float>(g.addr_b + h * 2 * HALF + d0 + 16 * q, kp.ab[q]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kp.ab[q][e] = 0.f;
+    }
+  }
+}
+
+// pre: the lane's sub-key piece loaded ahead (load_sub_key_piece with the same h, hf, kofs), or nullptr to load it
+// here (with the address loads)
 template <int HALF, bool FULL>
 __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
                                                  int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0,
-                                                 int zcol = -1) {
+                                                 int zcol = -1, const SubKeyPiece<HALF>* pre = nullptr) {
   static_assert(HALF % 8 == 0, "bfloat16 scoring feeds 8 dims per lane");
   constexpr int Q = (HALF + 15) / 16;
   const int l = threadIdx.x & 63;
@@ -567,6 +602,14 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
       zr[t][q] = has ? load_raw8(z0 + row * zstride + (zcol >= 0 ? zcol : static_cast<int64_t>(h) * 2 * HALF) + d0 +
                                  16 * q)
                      : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (pre) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ka[q][e] = pre->ka[q][e];
+        ab[q][e] = pre->ab[q][e];
+      }
+      continue;
     }
     if (has) {
       load_vals<8, float>(krow + 16 * q, ka[q]);

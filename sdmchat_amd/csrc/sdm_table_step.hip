@@ -71,6 +71,20 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStepGroup;
   const int nb = static_cast<int>(min<int64_t>(kStepGroup, N - n0));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the loads that do not depend on the block's rows, issued first: the wave's query-map weights (FOLD: d = 768)
+  // and its sub-key piece for the scoring
+  uint4 wpre[FOLD ? NCT : 1][kStepK];
+  if constexpr (FOLD) {
+    const int kb = wave * (kFoldD / 4) + 8 * (lane >> 5);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + (lane & 31)) * a.wq_stride + kb;
+#pragma unroll
+      for (int s = 0; s < kStepK; ++s) wpre[ct][s] = *reinterpret_cast<const uint4*>(wr + 16 * s);
+    }
+  }
+  SubKeyPiece<HALF> kpre;
+  if (wave < 2 * NT) load_sub_key_piece<HALF>(a.g, h, wave / NT, 32 * (wave % NT), kpre);
   if constexpr (FOLD) {
     static_assert(kStepGroup == 4, "two rows per wave in waves 0 and 1");
     if (wave < kStepGroup / 2) {
@@ -105,7 +119,7 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
 #pragma unroll
         for (int s = 0; s < kStepK; ++s) {
           xv[s] = *reinterpret_cast<const uint4*>(xr + 16 * s);
-          wv[s] = *reinterpret_cast<const uint4*>(wr + 16 * s);
+          wv[s] = FOLD ? wpre[ct][s] : *reinterpret_cast<const uint4*>(wr + 16 * s);
         }
         __builtin_amdgcn_sched_barrier(0);   // keep the scheduler from moving loads below the products
 #pragma unroll
@@ -145,7 +159,7 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
     const bf16_t* z0 = reinterpret_cast<const bf16_t*>(&s_q[0][0]);
     floatx16 acc[2];
     float inv[2];
-    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile, 0);
+    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile, 0, &kpre);
     // lane l: token l % 32 of tile 0, sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
     const int row = lane & 31;
     if (row < nb) {

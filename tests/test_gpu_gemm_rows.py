@@ -57,3 +57,41 @@ def test_gemm_rows_leaves_other_products_to_the_library():
     wr = w.clone().requires_grad_(True)                            # autograd recording: the library's product
     y = core.linear(x[:8], wr)
     assert y.grad_fn is not None
+
+
+def _gemm_rows(x, w, b=None):
+    """sdm_rt_gemm_rows called directly (any row count: the kernel the launcher picks for the shape)."""
+    import ctypes
+    from sdmchat_amd import _lib
+    lib = _lib.load()
+    y = torch.empty(x.shape[0], w.shape[0], dtype=torch.bfloat16, device=x.device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)   # noqa: E731
+    rc = lib.sdm_rt_gemm_rows(p(x), x.stride(0), p(w), w.stride(0), p(b), p(y), y.stride(0), x.shape[0], w.shape[0],
+                              x.shape[1], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, lib)
+    return y
+
+
+def test_gemm_rows_kernels_give_the_same_bits():
+    """k = 768: the launcher takes 32-row tiles for few column tiles (<= 256 of 64 rows x 32 columns), the walking
+    kernel for wide maps (the tied head) and the general 64-row kernel past 256 row tiles; all three sum every
+    element in the same order, so a product's bits do not depend on which one ran."""
+    g = torch.Generator(device="cpu").manual_seed(11)
+    x = torch.randn(16448, 768, generator=g).to(torch.bfloat16).cuda()          # 257 tiles of 64 rows
+    w = (torch.randn(8224, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()  # 257 column tiles
+    b = torch.randn(8224, generator=g).to(torch.bfloat16).cuda()
+    say("gemm_rows kernels: 32-row tiles, wide walk, general")
+    with torch.no_grad():
+        narrow = _gemm_rows(x[:64], w[:64], b[:64])        # 2 column tiles: 32-row tiles
+        general = _gemm_rows(x, w[:64], b[:64])            # 257 row tiles: the general kernel
+        wide = _gemm_rows(x[:64], w, b)                    # 257 column tiles: the walking kernel, 256 columns
+        wide200 = _gemm_rows(x[:200], w, b)                # 4 row tiles: 64 columns, each walking ~4 tiles
+        narrow200 = _gemm_rows(x[:200], w[4096:4160], b[4096:4160])
+        torch.cuda.synchronize()
+    assert torch.equal(general[:64].view(torch.int16), narrow.view(torch.int16))
+    assert torch.equal(wide[:, :64].view(torch.int16), narrow.view(torch.int16))
+    assert torch.equal(wide200[:64].view(torch.int16), wide.view(torch.int16))
+    assert torch.equal(wide200[:, 4096:4160].view(torch.int16), narrow200.view(torch.int16))
+    want = _ref(x[:200], w, b)
+    d = (wide200.float() - want).abs()
+    assert bool((d <= want.abs() * 2.0 ** -7 + 1e-6).all())
