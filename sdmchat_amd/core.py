@@ -630,6 +630,47 @@ def linear(x, w, bias=None, as_matmul=False):
     return y
 
 
+GEMM_ROWS_FOLD_K = 768   # the layer width of sdm_rt_gemm_rows_residual
+
+
+def linear_residual_fits(x, y, w, bias=None):
+    """Whether sdm_rt_gemm_rows_residual serves this residual add, input norm and map: x, y bf16 of one shape,
+    contiguous, with 768 columns; w [n, 768] bf16 with n a positive multiple of 32 (bias bf16 [n] or None); at most
+    256 tiles of 64 rows x 32 columns; no autograd recording."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and y.dtype == x.dtype and y.shape == x.shape
+            and x.is_contiguous() and y.is_contiguous() and x.shape[-1] == GEMM_ROWS_FOLD_K):
+        return False
+    if not (w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[1] == GEMM_ROWS_FOLD_K and w.shape[0] % 32 == 0
+            and w.shape[0] > 0 and (bias is None or (bias.dtype == torch.bfloat16 and bias.numel() == w.shape[0]))):
+        return False
+    rows = x.numel() // GEMM_ROWS_FOLD_K
+    if rows == 0 or (w.shape[0] // 32) * ((rows + 63) // 64) > 256:
+        return False
+    return not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, y, w, bias)))
+
+
+def linear_residual(x, y, norm_w, eps, w, bias=None):
+    """The residual add, the next layer's input norm and its map in one launch (sdm_rt_gemm_rows_residual):
+    s = x + y, hx = rms_norm(s, norm_w, eps) in bf16, out = linear(hx, w, bias); bit for bit add_rms_norm followed by
+    linear.  x, y [..., 768] bf16, contiguous (linear_residual_fits).  s is a new tensor (every workgroup reads x and y
+    while the first column's write the sums).  Returns (s, out)."""
+    k = GEMM_ROWS_FOLD_K
+    n = w.shape[0]
+    rows = x.numel() // k
+    w = w if _rows16(w) else w.contiguous()
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    s = torch.empty_like(x)
+    out = torch.empty(x.shape[:-1] + (n,), dtype=torch.bfloat16, device=x.device)
+    wf = _f32_weight(norm_w, x.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.sdm_rt_gemm_rows_residual(_ptr(x), k, _ptr(y), k, _ptr(wf), float(eps), _ptr(s), k, _ptr(w), w.stride(0),
+                                       _ptr(bias), _ptr(out), n, rows, n, k, ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return s, out
+
+
 def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape

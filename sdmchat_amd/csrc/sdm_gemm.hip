@@ -4,7 +4,7 @@
 // library tiles for many rows; with 64 rows the work is reading W once, so these kernels give every workgroup a
 // tile of 32 columns (64 or 32 rows) and split K over its four waves, and the waves' partial tiles are added in a
 // fixed order (the result does not depend on timing, and the three kernels give the same bits).
-#include "sdm_common.h"
+#include "sdm_norm.h"
 
 namespace sdmrt {
 
@@ -69,24 +69,68 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const bf16_t* __restrict
 // k = 768, few column tiles (a decode step's layer maps): blocks of 32 rows x 32 columns, twice the blocks of the
 // 64-row tiling for the same map, each loading half the rows of x; every operand of a wave (12 16-deep steps) is
 // loaded before its first product (one round trip).  Wave w's sums are those of gemm_rows_kernel's first accumulator.
+// FOLD: x is rms_norm(x + y) (OneSdmLM's residual add and the next layer's input norm in front of its map): the block
+// computes its 32 rows' sums and norms with the norm kernel's own code (norm_rows: the same bits as
+// sdm_rt_add_rms_norm, four rows per half-wave, every load first) into LDS, column tile 0's blocks write the sums,
+// and the operands come from LDS (rows padded by 16 bytes, so the 32 rows an operand load reads spread over the banks).
 constexpr int kRowsK = 768;
 constexpr int kRowsSteps = kRowsK / 64;   // 16-deep steps per wave
+constexpr int kFoldRow = kRowsK + 8;      // bfloat16 per LDS row of the normed tile
+
+struct RowsFold {   // the residual add and norm in front of the map (FOLD)
+  const bf16_t* y;
+  int64_t ys;
+  const float* w;
+  float eps;
+  bf16_t* sum;
+  int64_t ss;
+};
+
+template <bool FOLD>
 __global__ void __launch_bounds__(256) gemm_rows32_kernel(const bf16_t* __restrict__ x, int64_t xs,
                                                           const bf16_t* __restrict__ w, int64_t ws,
                                                           const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
-                                                          int64_t ys, int rows) {
+                                                          int64_t ys, int rows, RowsFold fold) {
   __shared__ float part[4][16][64];   // [wave][accumulator register][lane]
+  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? 32 : 1][FOLD ? kFoldRow : 8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * kGemmCols, m0 = blockIdx.y * 32;
   const int kb = wave * (kRowsK / 4) + 8 * (lane >> 5);
   const int r = lane & 31;
-  const bf16_t* a = x + static_cast<int64_t>(min(m0 + r, rows - 1)) * xs + kb;   // rows past the end: clamped
   const bf16_t* b = w + static_cast<int64_t>(n0 + r) * ws + kb;
   uint4 av[kRowsSteps], bv[kRowsSteps];
+  if constexpr (FOLD) {
 #pragma unroll
-  for (int s = 0; s < kRowsSteps; ++s) {
-    bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
-    av[s] = *reinterpret_cast<const uint4*>(a + 16 * s);
+    for (int s = 0; s < kRowsSteps; ++s) bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
+    constexpr int R = 4;   // rows 8 j + 2 wave + lane / 32 of the tile, j < 4, for half-wave (wave, lane / 32)
+    const bf16_t* xr[R];
+    const bf16_t* yr[R];
+    bf16_t* sr[R];
+    bf16_t* dr[R];
+    bool live[R], keep[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int i = 8 * j + 2 * wave + (lane >> 5);
+      live[j] = m0 + i < rows;
+      keep[j] = live[j] && blockIdx.x == 0;
+      const int64_t rr = live[j] ? m0 + i : m0;   // rows past the end: an in-bounds stand-in, nothing written
+      xr[j] = x + rr * xs;
+      yr[j] = fold.y + rr * fold.ys;
+      sr[j] = fold.sum + rr * fold.ss;
+      dr[j] = &s_hx[i][0];
+    }
+    norm_rows<bf16_t, bf16_t, true, kRowsK / 256, R>(xr, yr, sr, dr, fold.w, kRowsK, fold.eps, lane, live, keep);
+    __syncthreads();
+    const bf16_t* a = &s_hx[min(r, rows - 1 - m0)][kb];   // rows past the end: clamped
+#pragma unroll
+    for (int s = 0; s < kRowsSteps; ++s) av[s] = *reinterpret_cast<const uint4*>(a + 16 * s);
+  } else {
+    const bf16_t* a = x + static_cast<int64_t>(min(m0 + r, rows - 1)) * xs + kb;   // rows past the end: clamped
+#pragma unroll
+    for (int s = 0; s < kRowsSteps; ++s) {
+      bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
+      av[s] = *reinterpret_cast<const uint4*>(a + 16 * s);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);   // keep the scheduler from moving loads below the products
   floatx16 acc = {};
@@ -198,8 +242,9 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
   const int row_tiles = static_cast<int>((rows + kGemmRows - 1) / kGemmRows);
   if (k == kRowsK && static_cast<int64_t>(ntiles) * row_tiles <= 256) {
     // a decode step's layer maps: 32-row tiles
-    hipLaunchKernelGGL(gemm_rows32_kernel, dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + 31) / 32)),
-                       dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb, yb, y_row_stride, static_cast<int>(rows));
+    hipLaunchKernelGGL(gemm_rows32_kernel<false>,
+                       dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + 31) / 32)), dim3(256), 0, st, xb,
+                       x_row_stride, wb, w_row_stride, bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
   } else if (k == kRowsK && row_tiles <= 256) {
     // wide maps: about one block per compute unit, each walking its column tiles
     const int cols = min(ntiles, max(1, 256 / row_tiles));
@@ -212,6 +257,43 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
                        k);
   }
   return check_launch("gemm_rows");
+}
+
+int sdm_rt_gemm_rows_residual(const void* x, int64_t x_row_stride, const void* y, int64_t y_row_stride,
+                              const float* norm_w, float norm_eps, void* sum_out, int64_t sum_row_stride,
+                              const void* w, int64_t w_row_stride, const void* bias, void* out,
+                              int64_t out_row_stride, int64_t rows, int32_t n, int32_t k, void* stream) {
+  g_err[0] = 0;
+  if (rows < 0 || n < 0 || k < 0) return set_err(SDM_RT_EINVAL, "rows, n and k must be >= 0");
+  if (k != kRowsK) return set_err(SDM_RT_EUNSUPPORTED, "gemm_rows_residual: k = %d, must be %d", k, kRowsK);
+  if (n == 0 || n % kGemmCols != 0)
+    return set_err(SDM_RT_EUNSUPPORTED, "gemm_rows_residual: n = %d must be a positive multiple of %d", n, kGemmCols);
+  if (rows == 0) return SDM_RT_OK;
+  const int ntiles = n / kGemmCols;
+  if (static_cast<int64_t>(ntiles) * ((rows + kGemmRows - 1) / kGemmRows) > 256)
+    return set_err(SDM_RT_EUNSUPPORTED,
+                   "gemm_rows_residual: %lld rows x %d columns: more than 256 tiles of 64 x 32 (call "
+                   "sdm_rt_add_rms_norm, then sdm_rt_gemm_rows)", (long long)rows, n);
+  if (!x || !y || !norm_w || !sum_out || !w || !out)
+    return set_err(SDM_RT_EINVAL, "x, y, norm_w, sum_out, w and out must not be NULL");
+  if (x_row_stride < k || y_row_stride < k || sum_row_stride < k || w_row_stride < k || out_row_stride < n)
+    return set_err(SDM_RT_EINVAL, "row strides too small");
+  auto al16 = [](const void* p, int64_t stride) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (stride * 2) % 16 == 0;
+  };
+  if (!al16(x, x_row_stride) || !al16(y, y_row_stride) || !al16(sum_out, sum_row_stride) || !al16(w, w_row_stride) ||
+      reinterpret_cast<uintptr_t>(norm_w) % 16)
+    return set_err(SDM_RT_EINVAL, "x, y, sum_out and w rows and norm_w must be 16-byte aligned");
+  // every column tile's blocks read x and y while column tile 0's write the sums, and all write out
+  if (sum_out == x || sum_out == y || out == x || out == y || out == sum_out)
+    return set_err(SDM_RT_EINVAL, "gemm_rows_residual: sum_out and out must not alias x, y or each other");
+  const RowsFold fold{static_cast<const bf16_t*>(y), y_row_stride, norm_w, norm_eps, static_cast<bf16_t*>(sum_out),
+                      sum_row_stride};
+  hipLaunchKernelGGL(gemm_rows32_kernel<true>, dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + 31) / 32)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x), x_row_stride,
+                     static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(bias),
+                     static_cast<bf16_t*>(out), out_row_stride, static_cast<int>(rows), fold);
+  return check_launch("gemm_rows_residual");
 }
 
 }  // extern "C"

@@ -52,48 +52,111 @@ __device__ __forceinline__ float half_wave_sum(float v, int lane) {
   return lane < 32 ? lo : hi;
 }
 
-// One row of the norm: the 32 lanes of a half-wave (l % 32) each hold KC pieces of 8 consecutive values,
-// c = 8 (l % 32 + 32 k), d <= 256 KC; the row, the residual and the weights are all loaded before any use.  ADD: the
-// row is x + y rounded to InT (a residual add), also written to sum when keep_sum (in place over x is allowed: each
-// value is read and written by the same lane).  out = (s * rsqrt(mean(s^2) + eps) rounded to InT) * w, written
-// when live.  Both halves of the wave take part (the sum crosses lanes): a half without a row passes in-bounds
-// pointers and live = keep_sum = false.
+// 8 values of T as one load brings them (bfloat16: one 16-byte piece; float32: two), unpacked when used
+template <typename T>
+struct Piece8 {
+  uint4 q[sizeof(T) == 2 ? 1 : 2];
+};
+template <typename T>
+__device__ __forceinline__ Piece8<T> load_piece8(const T* p) {
+  Piece8<T> r;
+#pragma unroll
+  for (int i = 0; i < (sizeof(T) == 2 ? 1 : 2); ++i) r.q[i] = reinterpret_cast<const uint4*>(p)[i];
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void unpack8(const Piece8<T>& pc, float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w[4] = {pc.q[0].x, pc.q[0].y, pc.q[0].z, pc.q[0].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = __uint_as_float(w[e] << 16);
+      v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      v[4 * i] = __uint_as_float(pc.q[i].x);
+      v[4 * i + 1] = __uint_as_float(pc.q[i].y);
+      v[4 * i + 2] = __uint_as_float(pc.q[i].z);
+      v[4 * i + 3] = __uint_as_float(pc.q[i].w);
+    }
+  }
+}
+
+// R rows of the norm per half-wave: the 32 lanes of a half-wave (l % 32) each hold KC pieces of 8 consecutive values
+// of every row, c = 8 (l % 32 + 32 k), d <= 256 KC; the rows, the residuals and the weights are all loaded before
+// any use.  ADD: a row is x + y rounded to InT (a residual add), also written to sum when keep_sum (in place over x
+// is allowed: each value is read and written by the same lane).  out = (s * rsqrt(mean(s^2) + eps) rounded to InT)
+// * w, written when live.  Both halves of the wave take part (the sums cross lanes): a half without a row passes
+// in-bounds pointers and live = keep_sum = false.  Each row's arithmetic does not depend on R.
+template <typename InT, typename OutT, bool ADD, int KC, int R>
+__device__ __forceinline__ void norm_rows(const InT* const (&xr)[R], const InT* const (&yr)[R], InT* const (&sr)[R],
+                                          OutT* const (&dst)[R], const float* __restrict__ w, int d, float eps,
+                                          int lane, const bool (&live)[R], const bool (&keep_sum)[R]) {
+  const int hl = lane & 31;
+  Piece8<InT> xp[R][KC], yp[R][ADD ? KC : 1];
+  Piece8<float> wp[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int c = 8 * (hl + 32 * k);
+    if (c < d) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        xp[r][k] = load_piece8<InT>(xr[r] + c);
+        if constexpr (ADD) yp[r][k] = load_piece8<InT>(yr[r] + c);
+      }
+      wp[k] = load_piece8<float>(w + c);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float v[KC][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int c = 8 * (hl + 32 * k);
+      if (c < d) {
+        unpack8<InT>(xp[r][k], v[k]);
+        if constexpr (ADD) {
+          float u[8];
+          unpack8<InT>(yp[r][k], u);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[k][e] = round_to<InT>(v[k][e] + u[e]);   // x + y in the input type
+          if (keep_sum[r]) store8<InT>(sr[r] + c, v[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+      }
+    }
+    ss = half_wave_sum(ss, lane);
+    const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
+    if (live[r]) {
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int c = 8 * (hl + 32 * k);
+        if (c < d) {
+          float wv[8], o[8];
+          unpack8<float>(wp[k], wv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = round_to<InT>(v[k][e] * rs) * wv[e];   // .to(x.dtype) * w
+          store8<OutT>(dst[r] + c, o);
+        }
+      }
+    }
+  }
+}
+
+// One row of the norm per half-wave (norm_rows with R = 1)
 template <typename InT, typename OutT, bool ADD, int KC>
 __device__ __forceinline__ void norm_row(const InT* xr, const InT* yr, InT* sr, OutT* dst, const float* __restrict__ w,
                                          int d, float eps, int lane, bool live, bool keep_sum) {
-  const int hl = lane & 31;
-  float v[KC][8], wv[KC][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < KC; ++k) {
-    const int c = 8 * (hl + 32 * k);
-    if (c < d) {
-      load8<InT>(xr + c, v[k]);
-      load8<float>(w + c, wv[k]);
-      if constexpr (ADD) {
-        float u[8];
-        load8<InT>(yr + c, u);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[k][e] = round_to<InT>(v[k][e] + u[e]);   // x + y in the input type
-        if (keep_sum) store8<InT>(sr + c, v[k]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
-    }
-  }
-  ss = half_wave_sum(ss, lane);
-  const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
-  if (!live) return;
-#pragma unroll
-  for (int k = 0; k < KC; ++k) {
-    const int c = 8 * (hl + 32 * k);
-    if (c < d) {
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = round_to<InT>(v[k][e] * rs) * wv[k][e];   // .to(x.dtype) * w
-      store8<OutT>(dst + c, o);
-    }
-  }
+  const InT* const xa[1] = {xr};
+  const InT* const ya[1] = {yr};
+  InT* const sa[1] = {sr};
+  OutT* const da[1] = {dst};
+  const bool la[1] = {live}, ka[1] = {keep_sum};
+  norm_rows<InT, OutT, ADD, KC, 1>(xa, ya, sa, da, w, d, eps, lane, la, ka);
 }
 
 }  // namespace sdmrt

@@ -181,22 +181,24 @@ class OneSdmLM(nn.Module):
         norm = self.mnorms[i] if kind == "mlp" else self.nf
         return torch.promote_types(x.dtype, norm.w.dtype)
 
-    def _run(self, x, apply):
+    def _run(self, x, apply, apply_res=None):
         """Inference: the residual stream through every stage with each residual add fused into the next stage's
         input norm (core.add_rms_norm: one kernel for x = x + y and its RMSNorm, the same roundings as the add and
         the norm apart); in front of a TrainedSdm stage that takes it (a few tokens, TrainedSdm.residual_fits) the
-        add and the norm run inside that stage's table step instead (TrainedSdm.forward_residual, the same bits).
-        apply(kind, i, x, hx) gives a stage's output.  Returns nf(x)."""
+        add and the norm run inside that stage's table step instead (TrainedSdm.forward_residual, the same bits), and
+        in front of a mixer whose decode step takes it (apply_res given, RunTimeSdm.residual_fits) inside the
+        mixer's projection map (RunTimeSdm.step_residual, the same bits).  apply(kind, i, x, hx) gives a stage's
+        output, apply_res(kind, i, x, y) a mixer's (x + y, output).  Returns nf(x)."""
         stages = self._stages()
         if not stages:
             return _norm(x, self.nf)
         kind, i, norm = stages[0]
         x = x.contiguous()   # the residual stream (enfold's fresh output), updated in place
         hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
-        pending = None       # the last stage's output, to be added in front of this (TrainedSdm) stage
+        pending = None       # the last stage's output, to be added in front of this (TrainedSdm or mixer) stage
         for n, (kind, i, norm) in enumerate(stages):
             if pending is not None:
-                x, y = self.sdms[i].forward_residual(x, pending)
+                x, y = self.sdms[i].forward_residual(x, pending) if kind == "sdm" else apply_res(kind, i, x, pending)
                 pending = None
             else:
                 y = apply(kind, i, x, hx)
@@ -207,6 +209,9 @@ class OneSdmLM(nn.Module):
                 continue
             y = y.contiguous()
             if nxt[0] == "sdm" and self.sdms[nxt[1]].residual_fits(x, y):
+                pending = y
+                continue
+            if nxt[0] == "mem" and apply_res is not None and self.mems[nxt[1]].residual_fits(x, y):
                 pending = y
                 continue
             x, hx = core.add_rms_norm(x, y, nxt[2].w, nxt[2].eps, out_dtype=self._norm_dtype(nxt[0], nxt[1], x))
@@ -292,7 +297,10 @@ class OneSdmLM(nn.Module):
             if kind == "mlp":
                 return self.mlps[i](hx)
             return self.sdms[i](x[:, None], hx=hx[:, None])[:, 0]   # per token
-        h = self._run(self.enfold(idx_t), apply)
+
+        def apply_res(kind, i, x, y):   # a mixer's step on x + y, the add and its norm in the projection map
+            return self.mems[i].step_residual(x, y, state.layers[i], reset)
+        h = self._run(self.enfold(idx_t), apply, apply_res)
         state.pos += 1
         return self.project(h)
 

@@ -323,23 +323,59 @@ class RunTimeSdm(nn.Module):
         dt = self._compute_dtype(x2)
         with torch.autocast("cuda", enabled=False):
             kz, qz, V, g = self._project(x2.unsqueeze(1), dt, None if hx is None else hx.reshape(x2.shape[0], 1, -1))
-            wo = self._fused_weight(dt)[2]
-            r = core.decode_step(
-                kz[:, 0], qz[:, 0], V[:, 0], None if g is None else g[:, 0], state, keys1=self.keys1,
-                keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(), addr_b=self.addr_b,
-                onorm_w=self.onorm_w if self.out_norm else None, gate_bias=None,
-                k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
-                out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
-                params=self._core_params(x.device))
-            y = core.linear(r, wo, as_matmul=True).to(x.dtype)
-            if self.keep_picks:   # the addressing kernels on the step's rows: the decode step's own picks
-                prm = self._core_params(x.device)
-                self.last_addresses = (kz, qz)
-                self.last_projections = (kz, qz, V, g)
-                self.last_picks = tuple(
-                    core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
-                                 params=prm)[0] for z in (kz, qz))
+            y = self._step_projected(kz, qz, V, g, state, reset, dt, x.dtype)
         return y.reshape(x.shape)
+
+    def _step_projected(self, kz, qz, V, g, state, reset, dt, out_dtype):
+        """The step after the projections (kz, qz, V, g: [B, 1, ...] views): the decode step, then wo."""
+        wo = self._fused_weight(dt)[2]
+        r = core.decode_step(
+            kz[:, 0], qz[:, 0], V[:, 0], None if g is None else g[:, 0], state, keys1=self.keys1,
+            keys2=self.keys2, log_scale=self.log_scale, decay=self.decay(), addr_b=self.addr_b,
+            onorm_w=self.onorm_w if self.out_norm else None, gate_bias=None,
+            k=self.k, read_mode=self.read_mode, out_norm=self.out_norm, read_eps=self.read_eps,
+            out_norm_eps=self.out_norm_eps, reset=reset, out_dtype=dt, workspace=self._ws,
+            params=self._core_params(kz.device))
+        y = core.linear(r, wo, as_matmul=True).to(out_dtype)
+        if self.keep_picks:   # the addressing kernels on the step's rows: the decode step's own picks
+            prm = self._core_params(kz.device)
+            self.last_addresses = (kz, qz)
+            self.last_projections = (kz, qz, V, g)
+            self.last_picks = tuple(
+                core.address(z, self.keys1, self.keys2, self.k, self.log_scale, addr_b=self.addr_b,
+                             params=prm)[0] for z in (kz, qz))
+        return y
+
+    def residual_fits(self, x, y):
+        """Whether step_residual serves a step on x + y: bf16 rows of the layer width, few enough for the folded
+        map (core.linear_residual_fits on the whole projection buffer), inference."""
+        if not self.enabled or x.dim() not in (2, 3) or x.shape[-1] != self.d or x.device.type != "cuda":
+            return False
+        if x.dtype != torch.bfloat16 or self._training(x) or torch.is_autocast_enabled("cuda"):
+            return False
+        W, bias = self._fused_weight(torch.bfloat16)[:2]
+        return core.linear_residual_fits(x, y, W, bias)
+
+    def step_residual(self, x, y, state, reset=None):
+        """step() on the residual stream's next value s = x + y (OneSdmLM's x = x + layer(x) in front of this mixer,
+        track4_onesdm_models.py:540-547): the add, the input norm and the whole projection map run in one launch
+        (core.linear_residual), bit for bit add_rms_norm followed by step(s, hx=...).  x, y [B, d] (or [B, 1, d])
+        bf16 (residual_fits).  Returns (s, out), each of x's shape."""
+        if not self.residual_fits(x, y):
+            raise ValueError("step_residual: the folded map does not take these rows (see residual_fits)")
+        x2 = x.reshape(-1, self.d)
+        B = x2.shape[0]
+        H, d_a = self.h, self.d_a
+        dt = torch.bfloat16
+        W, bias = self._fused_weight(dt)[:2]
+        ra = self._rows_a()
+        s, proj = core.linear_residual(x2, y.reshape(-1, self.d), self.norm.w, self.norm.eps, W, bias)
+        proj = proj.view(B, 1, -1)
+        pa, V = proj[..., :ra], proj[..., ra:]
+        o_q, o_g = H * d_a, 2 * H * d_a
+        g = pa[..., o_g:o_g + H] if self.write_gate else None
+        out = self._step_projected(pa[..., :o_q], pa[..., o_q:o_g], V, g, state, reset, dt, x.dtype)
+        return s.reshape(x.shape), out.reshape(x.shape)
 
     def forward_sequential(self, x, reset=None):
         """The token recurrence of the reference (track4_onesdm_models.py:276-300).  It is the same function as

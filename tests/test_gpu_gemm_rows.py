@@ -95,3 +95,40 @@ def test_gemm_rows_kernels_give_the_same_bits():
     want = _ref(x[:200], w, b)
     d = (wide200.float() - want).abs()
     assert bool((d <= want.abs() * 2.0 ** -7 + 1e-6).all())
+
+
+@pytest.mark.parametrize("rows,n,bias", [(64, 2560, True), (1, 2560, True), (5, 768, False), (37, 2560, True),
+                                         (100, 768, False), (192, 2560, True)])
+def test_gemm_rows_residual_equals_add_norm_then_gemm_rows(rows, n, bias):
+    """sdm_rt_gemm_rows_residual (the residual add and the next mixer's input norm folded into its projection map)
+    against sdm_rt_add_rms_norm followed by sdm_rt_gemm_rows on the same inputs: the sums and the products bit for
+    bit, x and y untouched."""
+    g = torch.Generator(device="cpu").manual_seed(rows * 3 + n)
+    x = torch.randn(rows, 768, generator=g).to(torch.bfloat16).cuda()
+    y = (torch.randn(rows, 768, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    nw = (torch.rand(768, generator=g) + 0.5).cuda()
+    w = (torch.randn(n, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()
+    b = torch.randn(n, generator=g).to(torch.bfloat16).cuda() if bias else None
+    x0, y0 = x.clone(), y.clone()
+    say("gemm_rows_residual", rows, n, bias)
+    with torch.no_grad():
+        assert core.linear_residual_fits(x, y, w, b)
+        s1, o1 = core.linear_residual(x, y, nw, 1e-6, w, b)
+        s0, hx = core.add_rms_norm(x, y, nw, 1e-6, out_dtype=torch.bfloat16, inplace=False)
+        o0 = core.linear(hx, w, b)
+        torch.cuda.synchronize()
+    assert torch.equal(x, x0) and torch.equal(y, y0)
+    assert torch.equal(s1.view(torch.int16), s0.view(torch.int16))
+    assert torch.equal(o1.view(torch.int16), o0.view(torch.int16))
+
+
+def test_gemm_rows_residual_declines_large_maps():
+    """More than 256 tiles of 64 rows x 32 columns: linear_residual_fits says no, and the entry point returns
+    SDM_RT_EUNSUPPORTED without launching."""
+    from sdmchat_amd import _lib
+    x = torch.zeros(193, 768, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(2560, 768, dtype=torch.bfloat16, device="cuda")
+    assert not core.linear_residual_fits(x, x.clone(), w)
+    assert core.linear_residual_fits(x[:192], x[:192].clone(), w)
+    with pytest.raises(_lib.SdmRtError):
+        core.linear_residual(x, x.clone(), torch.ones(768, device="cuda"), 1e-6, w)

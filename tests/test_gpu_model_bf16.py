@@ -28,7 +28,7 @@ import pytest
 import torch
 
 from oracle import sdm_fp64 as O
-from sdmchat_amd import DecodeGraph, synthetic as S
+from sdmchat_amd import DecodeGraph, core, synthetic as S
 from tests._gpu_util import assert_close, bf16_round, core_inputs, gpu_address, gpu_decode, half_ulp_bf16, say
 
 pytestmark = pytest.mark.gpu
@@ -93,6 +93,7 @@ class _Stages:
             mm.keep_picks = True
             for name in ("forward", "step"):
                 self._wrap(mm, name, ("mem", i))
+            self._wrap_step_residual(mm, ("mem", i))
         for i, sd in enumerate(getattr(m, "sdms", [])):
             sd.keep_picks = True
             self._wrap(sd, "forward", ("sdm", i))
@@ -131,6 +132,22 @@ class _Stages:
             self.rec.setdefault(key, []).append(r)
             return s, out
         mod.forward_residual = f
+
+    def _wrap_step_residual(self, mod, key):
+        """RunTimeSdm.step_residual (the add in front of the mixer folded into its projection map): the mixer's input
+        is the returned sum; its normed input, which the folded map keeps on chip, is the norm kernel's on that sum
+        (the same bits: test_gemm_rows_residual_equals_add_norm_then_gemm_rows)."""
+        orig = mod.step_residual
+
+        def f(x, y, *a, **kw):
+            s, out = orig(x, y, *a, **kw)
+            hx = core.rms_norm(s, mod.norm.w, mod.norm.eps, out_dtype=torch.bfloat16)
+            r = dict(x=s.detach().clone(), hx=hx, y=out.detach().clone(),
+                     proj=tuple(t.detach().clone() for t in mod.last_projections),
+                     picks=tuple(s_[..., :mod.k] for s_ in mod.last_picks))
+            self.rec.setdefault(key, []).append(r)
+            return s, out
+        mod.step_residual = f
 
     def get(self, key, B):
         rec = self.rec[key]

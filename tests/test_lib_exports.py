@@ -181,3 +181,20 @@ def test_table_step_residual_arguments_are_checked_before_launch():
     dims2 = core.make_dims(1, 64, 2, 384, 32, 32, 8, out_norm=False, write_gate=False)
     assert call(dims2, 768, one) != 0 and "one head" in lib.sdm_rt_last_error().decode()
     assert call(dims1, 768, ctypes.c_void_p(32)) != 0 and "alias y" in lib.sdm_rt_last_error().decode()
+
+
+def test_gemm_rows_residual_arguments_are_checked_before_launch():
+    """The folded projection map takes k = 768, at most 256 tiles of 64 x 32, and no aliasing of its outputs with
+    x, y or each other."""
+    lib = _lib.load()
+    x, y, nw, s, w, o = (ctypes.c_void_p(16 * i) for i in range(1, 7))   # never dereferenced: validation fails first
+
+    def call(rows, n, k, s_out=s, out=o):
+        return lib.sdm_rt_gemm_rows_residual(x, k, y, k, nw, 1e-6, s_out, k, w, k, None, out, n, rows, n, k, None)
+    assert call(64, 2560, 512) != 0 and "768" in lib.sdm_rt_last_error().decode()
+    assert call(64, 100, 768) != 0 and "multiple of 32" in lib.sdm_rt_last_error().decode()
+    assert call(193, 2560, 768) != 0 and "256 tiles" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, s_out=x) != 0 and "alias" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, out=y) != 0 and "alias" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, out=s) != 0 and "alias" in lib.sdm_rt_last_error().decode()
+    assert call(0, 2560, 768) == 0   # no rows: nothing to do
