@@ -213,7 +213,7 @@ int sdm_rt_table_read(const sdm_rt_dims* dims, const int32_t* slots, const float
  * for at most 256 tokens.  All arrays bfloat16 except the picks.
  *   hx       [B*T rows] of d (the layer width, a multiple of 64), row stride hx_row_stride
  *   wq       [H * addr_dim][d] (addr_dim 32 or 64), row stride wq_row_stride
- *   values   [H][M][head_dim] (head_dim a multiple of 8), rows contiguous
+ *   values   [H][M][head_dim] (head_dim a multiple of 8 up to 1,024), rows contiguous
  *   q_out    [B*T rows] of H * addr_dim, or NULL
  *   slot_out, score_out, weight_out   [B][H][T][pitch] as sdm_rt_address writes them (score_out, weight_out may be
  *            NULL)

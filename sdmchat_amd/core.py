@@ -288,12 +288,13 @@ TABLE_STEP_MAX = 256   # token counts up to this take sdm_rt_table_step (the que
 
 def table_step_fits(hx, wq, values, d_a):
     """Whether sdm_rt_table_step serves this TrainedSdm read: bfloat16 inputs, map and tables, at most
-    TABLE_STEP_MAX tokens, d_a 32 or 64, the layer width a multiple of 64, head_dim a multiple of 8, no autograd."""
+    TABLE_STEP_MAX tokens, d_a 32 or 64, the layer width a multiple of 64, head_dim a multiple of 8 up to 1,024, no
+    autograd."""
     d = hx.shape[-1]
     rows = hx.numel() // d if d else 0
     return (hx.is_cuda and hx.dtype == torch.bfloat16 and wq.dtype == torch.bfloat16
             and values.dtype == torch.bfloat16 and 0 < rows <= TABLE_STEP_MAX and d % 64 == 0 and d_a in (32, 64)
-            and values.shape[-1] % 8 == 0
+            and values.shape[-1] % 8 == 0 and values.shape[-1] <= 1024
             and not (torch.is_grad_enabled() and any(t.requires_grad for t in (hx, wq, values))))
 
 

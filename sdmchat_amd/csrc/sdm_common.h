@@ -881,11 +881,35 @@ __device__ __forceinline__ unsigned long long sort_lanes_desc(unsigned long long
   return x;
 }
 
+// sort_lanes_desc of two independent keys per lane at once (each exchange step moves both), so that the two chains
+// of dependent steps overlap
+template <int N>
+__device__ __forceinline__ void sort_lanes_desc2(unsigned long long& x0, unsigned long long& x1, int lane) {
+  const int idx = lane & (N - 1);
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int a_lo = xor_lanes32(static_cast<int>(x0), j, lane);
+      const int a_hi = xor_lanes32(static_cast<int>(x0 >> 32), j, lane);
+      const int b_lo = xor_lanes32(static_cast<int>(x1), j, lane);
+      const int b_hi = xor_lanes32(static_cast<int>(x1 >> 32), j, lane);
+      const unsigned long long y0 = (static_cast<unsigned long long>(static_cast<uint32_t>(a_hi)) << 32) |
+                                    static_cast<uint32_t>(a_lo);
+      const unsigned long long y1 = (static_cast<unsigned long long>(static_cast<uint32_t>(b_hi)) << 32) |
+                                    static_cast<uint32_t>(b_lo);
+      const bool keep_max = ((idx & j) == 0) == ((idx & k) == 0);
+      x0 = ((x0 > y0) == keep_max) ? x0 : y0;
+      x1 = ((x1 > y1) == keep_max) ? x1 : y1;
+    }
+  }
+}
+
 // The picks of one address by a whole wave: address_wave's selection (the same keys, so the same picks, order,
 // weights and scores) with the candidates spread over the lanes instead of sorted per lane.  sc: the NS raw sub-key
 // scores of each half ([2][NS], as half_scores leaves them: score * inv = cosine), inv: the two halves' factors.
 // NS = 32: lanes 32 hf + i key sub-key i of half hf and each half sorts across its 32 lanes; NS = 64: lane i keys
-// sub-key i of each half in turn, each sorted across the wave.  Lane x < n_pairs(CAP) then keys grid pair x of the
+// sub-key i of each half, both sorted across the wave together.  Lane x < n_pairs(CAP) then keys grid pair x of the
 // dominance-pruned grid (address_one) and the 64 lanes sort.  Lane p < CAP returns pick p.
 template <int CAP, bool FULL, int NS = 32>
 __device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale, const float* sc, const float* inv,
@@ -914,8 +938,11 @@ __device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale,
       c0 = key_invalid(c0);
       c1 = key_invalid(c1);
     }
-    c0 = sort64(c0, std::integral_constant<int, 64>{});
-    c1 = sort64(c1, std::integral_constant<int, 64>{});
+    unsigned long long u0 = static_cast<unsigned long long>(__double_as_longlong(c0));
+    unsigned long long u1 = static_cast<unsigned long long>(__double_as_longlong(c1));
+    sort_lanes_desc2<64>(u0, u1, lane);   // both halves at once
+    c0 = __longlong_as_double(static_cast<long long>(u0));
+    c1 = __longlong_as_double(static_cast<long long>(u1));
     hk0 = lane < 16 ? key_or(c0, static_cast<uint32_t>(15 - lane) << KL::RS1) : c0;
     hk1 = lane < 16 ? key_or(c1, static_cast<uint32_t>(15 - lane) << KL::RS2) : c1;
   }

@@ -41,6 +41,7 @@ constexpr int kStepGroup = 4;          // tokens per block
 constexpr int kTableStepTokens = 256;  // at most this many tokens (sdm_rt_gemm_rows' row range, whose sums it repeats)
 constexpr int kStepK = 12;             // 16-deep steps per wave of the query map when d = 768
 constexpr int kFoldD = 768;            // the layer width of the folded residual add and norm (FOLD)
+constexpr int kPieces = 2;             // 16-byte pieces of a picked row per lane in the read: head_dim <= 1,024
 
 // Block (4 tokens, head), 4 waves.
 //  1. the head's d_a query columns of the block's rows: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
@@ -48,8 +49,8 @@ constexpr int kFoldD = 768;            // the layer width of the folded residual
 //     0..31), the four partial sums are added in wave order and rounded to bfloat16 once;
 //  2. wave q < 2 NS / 32 scores half q / (NS / 32) of the block's queries against sub-key tile q % (NS / 32)
 //     (half_scores, reading the queries from LDS), and wave j selects token j across its lanes (select_lanes);
-//  3. wave j reads its token's picked rows, 16 bytes of a row per lane, and sums them in pick order over the pitch
-//     (pads: slot 0, weight 0) in float32, as the table read does.
+//  3. wave j reads its token's picked rows, 16 bytes of a row per lane (two such pieces of every row loaded at once),
+//     and sums them in pick order over the pitch (pads: slot 0, weight 0) in float32, as the table read does.
 // FOLD (d = 768): before 1., half-wave i of waves 0 and 1 computes row i's residual sum rx + ry and its norm with the
 // norm kernel's own code (norm_row: the same bits as sdm_rt_add_rms_norm), writes the sum (head 0's blocks only)
 // and leaves the normed row in LDS, from which the query map reads it.
@@ -184,30 +185,40 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
     if (a.s_out) a.s_out[base + lane] = sc;
   }
   const bf16_t* tab = a.values + static_cast<int64_t>(h) * a.M * a.dh;
-  for (int c0 = 8 * lane; c0 < a.dh; c0 += 512) {
-    uint4 raw[CAP];
+  {   // head_dim <= 512 kPieces: every 16-byte piece of the picked rows in flight at once
+    uint4 raw[kPieces][CAP];
 #pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      const int sj = __builtin_amdgcn_readlane(slot, j);   // lanes past kk: slot 0 (weight 0)
-      raw[j] = j < a.pitch ? *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(sj) * a.dh + c0)
-                           : make_uint4(0u, 0u, 0u, 0u);
-    }
-    float acc[8];
+    for (int it = 0; it < kPieces; ++it) {
+      const int c0 = 512 * it + 8 * lane;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      if (j < a.pitch) {
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-        const uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[2 * q] = fmaf(wj, __uint_as_float(wd[q] << 16), acc[2 * q]);
-          acc[2 * q + 1] = fmaf(wj, __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
-        }
+      for (int j = 0; j < CAP; ++j) {
+        const int sj = __builtin_amdgcn_readlane(slot, j);   // lanes past kk: slot 0 (weight 0)
+        raw[it][j] = j < a.pitch && c0 < a.dh
+                         ? *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(sj) * a.dh + c0)
+                         : make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    store_vals<8, bf16_t>(a.r_out + n * a.r_stride + static_cast<int64_t>(h) * a.dh + c0, acc);
+#pragma unroll
+    for (int it = 0; it < kPieces; ++it) {
+      const int c0 = 512 * it + 8 * lane;
+      if (c0 >= a.dh) continue;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int j = 0; j < CAP; ++j) {
+        if (j < a.pitch) {
+          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+          const uint32_t wd[4] = {raw[it][j].x, raw[it][j].y, raw[it][j].z, raw[it][j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[2 * q] = fmaf(wj, __uint_as_float(wd[q] << 16), acc[2 * q]);
+            acc[2 * q + 1] = fmaf(wj, __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
+          }
+        }
+      }
+      store_vals<8, bf16_t>(a.r_out + n * a.r_stride + static_cast<int64_t>(h) * a.dh + c0, acc);
+    }
   }
 }
 
@@ -275,7 +286,9 @@ int table_step_impl(const sdm_rt_dims* dims, const sdm_rt_params* params, const 
   if (d <= 0 || d % 64 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: d = %d must be a positive multiple of 64", d);
   if (p.d_a % 32 != 0 || p.d_a > 64)
     return set_err(SDM_RT_EUNSUPPORTED, "table_step: addr_dim = %d must be 32 or 64", p.d_a);
-  if (p.dh % 8 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: head_dim = %d must be a multiple of 8", p.dh);
+  if (p.dh % 8 != 0 || p.dh > 512 * kPieces)
+    return set_err(SDM_RT_EUNSUPPORTED, "table_step: head_dim = %d must be a multiple of 8 up to %d", p.dh,
+                   512 * kPieces);
   if (p.pitch != p.cap) return set_err(SDM_RT_EUNSUPPORTED, "table_step: pick pitch %d", p.pitch);
   if ((!res && !hx) || !wq || !values || !slot_out || !out)
     return set_err(SDM_RT_EINVAL, "hx, wq, values, slot_out and out must not be NULL");
