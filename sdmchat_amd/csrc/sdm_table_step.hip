@@ -37,23 +37,23 @@ struct TableStepArgs {
   int64_t hx_out_stride;
 };
 
-constexpr int kStepGroup = 4;          // tokens per block
 constexpr int kTableStepTokens = 256;  // at most this many tokens (sdm_rt_gemm_rows' row range, whose sums it repeats)
 constexpr int kStepK = 12;             // 16-deep steps per wave of the query map when d = 768
 constexpr int kFoldD = 768;            // the layer width of the folded residual add and norm (FOLD)
-constexpr int kPieces = 2;             // 16-byte pieces of a picked row per lane in the read: head_dim <= 1,024
+constexpr int kMaxHeadDim = 1024;      // the read's 16-byte pieces of a head's row: at most 32 per wave
 
-// Block (4 tokens, head), 4 waves.
-//  1. the head's d_a query columns of the block's rows: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
-//     with the operand layout of gemm_rows_kernel (rows 0..3 of a 32-row tile: accumulator registers 0..3 of lanes
-//     0..31), the four partial sums are added in wave order and rounded to bfloat16 once;
-//  2. wave q < 2 NS / 32 scores half q / (NS / 32) of the block's queries against sub-key tile q % (NS / 32)
-//     (half_scores, reading the queries from LDS), and wave j selects token j across its lanes (select_lanes);
-//  3. wave j reads its token's picked rows, 16 bytes of a row per lane (two such pieces of every row loaded at once),
-//     and sums them in pick order over the pitch (pads: slot 0, weight 0) in float32, as the table read does.
-// FOLD (d = 768): before 1., half-wave i of waves 0 and 1 computes row i's residual sum rx + ry and its norm with the
-// norm kernel's own code (norm_row: the same bits as sdm_rt_add_rms_norm), writes the sum (head 0's blocks only)
-// and leaves the normed row in LDS, from which the query map reads it.
+// Block (token, head), 4 waves.
+//  1. the head's d_a query columns of the token's row: wave w sums k in [w d/4, (w + 1) d/4) on the matrix cores
+//     with the operand layout of gemm_rows_kernel (row 0 of a 32-row tile: accumulator register 0 of lanes 0..31),
+//     the four partial sums are added in wave order and rounded to bfloat16 once;
+//  2. wave q < 2 NS / 32 scores half q / (NS / 32) of the query against sub-key tile q % (NS / 32) (half_scores,
+//     reading the query from LDS), and wave 0 selects the picks across its lanes (select_lanes);
+//  3. the picks pass through LDS; wave w reads its quarter of the 16-byte pieces of the picked rows, every pick's
+//     piece in flight at once, and sums them in pick order over the pitch (pads: slot 0, weight 0) in float32, as the
+//     table read does.  (A block per token spreads the read over as many compute units as there are tokens.)
+// FOLD (d = 768): before 1., the first half of wave 0 computes the token's residual sum rx + ry and its norm with the
+// norm kernel's own code (norm_row: the same bits as sdm_rt_add_rms_norm), writes the sum (head 0's block only) and
+// leaves the normed row in LDS, from which the query map reads it.
 template <int HALF, int CAP, int MODE, bool FOLD>
 __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   constexpr int NS = MODE >= 3 ? 64 : 32;
@@ -62,17 +62,17 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   constexpr int DA = 2 * HALF;   // query columns of a head
   constexpr int NCT = DA / 32;   // 32-column tiles of the query map per head
   static_assert(DA % 32 == 0, "the query map runs on 32-column tiles");
-  __shared__ float s_part[4][NCT][kStepGroup][32];   // [wave][column tile][row][column]
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[kStepGroup][DA];
-  __shared__ float s_sc[kStepGroup][2][NS];
-  __shared__ float s_inv[kStepGroup][2];
-  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? kStepGroup : 1][FOLD ? kFoldD : 8];
+  __shared__ float s_part[4][NCT][32];   // [wave][column tile][column]
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[DA];
+  __shared__ float s_sc[2][NS];
+  __shared__ float s_inv[2];
+  __shared__ int s_slot[CAP];
+  __shared__ float s_w[CAP];
+  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? kFoldD : 8];
   const int h = blockIdx.y;
-  const int64_t N = static_cast<int64_t>(a.B) * a.T;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStepGroup;
-  const int nb = static_cast<int>(min<int64_t>(kStepGroup, N - n0));
+  const int64_t n = blockIdx.x;   // the token
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // the loads that do not depend on the block's rows, issued first: the wave's query-map weights (FOLD: d = 768)
+  // the loads that do not depend on the token's row, issued first: the wave's query-map weights (FOLD: d = 768)
   // and its sub-key piece for the scoring
   uint4 wpre[FOLD ? NCT : 1][kStepK];
   if constexpr (FOLD) {
@@ -87,19 +87,16 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   SubKeyPiece<HALF> kpre;
   if (wave < 2 * NT) load_sub_key_piece<HALF>(a.g, h, wave / NT, 32 * (wave % NT), kpre);
   if constexpr (FOLD) {
-    static_assert(kStepGroup == 4, "two rows per wave in waves 0 and 1");
-    if (wave < kStepGroup / 2) {
-      const int i = 2 * wave + (lane >> 5);
-      const bool live = i < nb;
-      const int64_t rr = n0 + (live ? i : 0);
-      norm_row<bf16_t, bf16_t, true, kFoldD / 256>(a.rx + rr * a.rx_stride, a.ry + rr * a.ry_stride,
-                                                   a.rsum + rr * a.rsum_stride, &s_hx[live ? i : 0][0], a.rw, kFoldD,
-                                                   a.reps, lane, live, live && h == 0);
+    if (wave == 0) {   // both halves take part in the norm's sums; the second passes the same row, not live
+      const bool live = lane < 32;
+      norm_row<bf16_t, bf16_t, true, kFoldD / 256>(a.rx + n * a.rx_stride, a.ry + n * a.ry_stride,
+                                                   a.rsum + n * a.rsum_stride, s_hx, a.rw, kFoldD, a.reps, lane, live,
+                                                   live && h == 0);
       if (a.hx_out && live && h == 0) {   // the lane's own pieces, as norm_row stored them
 #pragma unroll
         for (int k = 0; k < kFoldD / 256; ++k) {
-          const int c = 8 * ((lane & 31) + 32 * k);
-          *reinterpret_cast<uint4*>(a.hx_out + rr * a.hx_out_stride + c) = *reinterpret_cast<const uint4*>(&s_hx[i][c]);
+          const int c = 8 * (lane + 32 * k);
+          *reinterpret_cast<uint4*>(a.hx_out + n * a.hx_out_stride + c) = *reinterpret_cast<const uint4*>(&s_hx[c]);
         }
       }
     }
@@ -108,12 +105,11 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
   {
     const int kq = a.d / 4;
     const int kb = wave * kq + 8 * (lane >> 5);
-    const int r = lane & 31;
-    // rows past the block: clamped, unused; FOLD: the normed rows in LDS
-    const bf16_t* xr = FOLD ? &s_hx[min(r, nb - 1)][0] + kb : a.hx + (n0 + min(r, nb - 1)) * a.hx_stride + kb;
+    // every row of the tile is the token's (the rows past the first are unused); FOLD: the normed row in LDS
+    const bf16_t* xr = FOLD ? s_hx + kb : a.hx + n * a.hx_stride + kb;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
-      const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + r) * a.wq_stride + kb;
+      const bf16_t* wr = a.wq + static_cast<int64_t>(h * DA + 32 * ct + (lane & 31)) * a.wq_stride + kb;
       floatx16 acc = {};
       if (kq == 16 * kStepK) {   // d = 768: every operand of the wave loaded before the first product
         uint4 xv[kStepK], wv[kStepK];
@@ -135,91 +131,80 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
                                                         acc, 0, 0, 0);
         }
       }
-      if (lane < 32) {
-#pragma unroll
-        for (int i = 0; i < kStepGroup; ++i) s_part[wave][ct][i][lane] = acc[i];
-      }
+      if (lane < 32) s_part[wave][ct][lane] = acc[0];   // row 0, column lane
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < kStepGroup * DA; t += 256) {
-    const int i = t / DA, c = t - i * DA;
+  for (int c = threadIdx.x; c < DA; c += 256) {
     const int ct = c >> 5, cl = c & 31;
-    float v = s_part[0][ct][i][cl];
-    v += s_part[1][ct][i][cl];
-    v += s_part[2][ct][i][cl];
-    v += s_part[3][ct][i][cl];
+    float v = s_part[0][ct][cl];
+    v += s_part[1][ct][cl];
+    v += s_part[2][ct][cl];
+    v += s_part[3][ct][cl];
     const uint16_t bits = static_cast<uint16_t>(pack_bf16(v + 0.f, 0.f));   // as gemm_rows adds a zero bias
-    s_q[i][c] = bits;
-    if (a.q_out && i < nb) reinterpret_cast<uint16_t*>(a.q_out)[(n0 + i) * a.q_stride + h * DA + c] = bits;
+    s_q[c] = bits;
+    if (a.q_out) reinterpret_cast<uint16_t*>(a.q_out)[n * a.q_stride + h * DA + c] = bits;
   }
   __syncthreads();
   if (wave < 2 * NT) {
     const int hf = wave / NT, tile = wave % NT;
-    // the LDS rows hold head h's columns only: they start at column 0
-    const bf16_t* z0 = reinterpret_cast<const bf16_t*>(&s_q[0][0]);
     floatx16 acc[2];
     float inv[2];
-    half_scores_bf16<HALF, FULL>(a.g, h, hf, z0, DA, nb, acc, inv, 32 * tile, 0, &kpre);
-    // lane l: token l % 32 of tile 0, sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
-    const int row = lane & 31;
-    if (row < nb) {
+    half_scores_bf16<HALF, FULL>(a.g, h, hf, reinterpret_cast<const bf16_t*>(s_q), DA, 1, acc, inv, 32 * tile, 0,
+                                 &kpre);
+    // lane l < 32 of the address row 0: sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
+    if ((lane & 31) == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_sc[row][hf][32 * tile + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3)] = acc[0][r];
-      if (lane < 32 && tile == 0) s_inv[row][hf] = inv[0];
+      for (int r = 0; r < 16; ++r) s_sc[hf][32 * tile + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3)] = acc[0][r];
+      if (lane == 0 && tile == 0) s_inv[hf] = inv[0];
     }
   }
   __syncthreads();
-  if (wave >= nb) return;
-  const int64_t n = n0 + wave;
-  int slot;
-  float w, sc;
-  select_lanes<CAP, FULL, NS>(a.g, a.g.log_scale[h], &s_sc[wave][0][0], &s_inv[wave][0], 1.f, slot, w, sc);
-  const int b = static_cast<int>(n / a.T);
-  const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
-  const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
-  if (lane < CAP && lane < a.pitch) {
-    const bool live = lane < a.g.kk;
-    a.slot_out[base + lane] = live ? slot : -1;
-    if (a.w_out) a.w_out[base + lane] = w;
-    if (a.s_out) a.s_out[base + lane] = sc;
+  if (wave == 0) {
+    int slot;
+    float w, sc;
+    select_lanes<CAP, FULL, NS>(a.g, a.g.log_scale[h], &s_sc[0][0], s_inv, 1.f, slot, w, sc);
+    if (lane < CAP) {   // lanes past kk: slot 0, weight 0
+      s_slot[lane] = slot;
+      s_w[lane] = w;
+    }
+    const int b = static_cast<int>(n / a.T);
+    const int t = static_cast<int>(n - static_cast<int64_t>(b) * a.T);
+    const int64_t base = ((static_cast<int64_t>(b) * a.g.H + h) * a.T + t) * a.pitch;
+    if (lane < CAP && lane < a.pitch) {
+      const bool live = lane < a.g.kk;
+      a.slot_out[base + lane] = live ? slot : -1;
+      if (a.w_out) a.w_out[base + lane] = w;
+      if (a.s_out) a.s_out[base + lane] = sc;
+    }
   }
-  const bf16_t* tab = a.values + static_cast<int64_t>(h) * a.M * a.dh;
-  {   // head_dim <= 512 kPieces: every 16-byte piece of the picked rows in flight at once
-    uint4 raw[kPieces][CAP];
+  __syncthreads();
+  const int pieces = a.dh / 8;
+  const int per_wave = (pieces + 3) / 4;
+  const int pc = wave * per_wave + lane;
+  if (lane >= per_wave || pc >= pieces) return;
+  const bf16_t* tab = a.values + static_cast<int64_t>(h) * a.M * a.dh + 8 * pc;
+  uint4 raw[CAP];
 #pragma unroll
-    for (int it = 0; it < kPieces; ++it) {
-      const int c0 = 512 * it + 8 * lane;
-#pragma unroll
-      for (int j = 0; j < CAP; ++j) {
-        const int sj = __builtin_amdgcn_readlane(slot, j);   // lanes past kk: slot 0 (weight 0)
-        raw[it][j] = j < a.pitch && c0 < a.dh
-                         ? *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(sj) * a.dh + c0)
+  for (int j = 0; j < CAP; ++j)
+    raw[j] = j < a.pitch ? *reinterpret_cast<const uint4*>(tab + static_cast<int64_t>(s_slot[j]) * a.dh)
                          : make_uint4(0u, 0u, 0u, 0u);
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    if (j < a.pitch) {
+      const float wj = s_w[j];
+      const uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] = fmaf(wj, __uint_as_float(wd[q] << 16), acc[2 * q]);
+        acc[2 * q + 1] = fmaf(wj, __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
       }
-    }
-#pragma unroll
-    for (int it = 0; it < kPieces; ++it) {
-      const int c0 = 512 * it + 8 * lane;
-      if (c0 >= a.dh) continue;
-      float acc[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll
-      for (int j = 0; j < CAP; ++j) {
-        if (j < a.pitch) {
-          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-          const uint32_t wd[4] = {raw[it][j].x, raw[it][j].y, raw[it][j].z, raw[it][j].w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[2 * q] = fmaf(wj, __uint_as_float(wd[q] << 16), acc[2 * q]);
-            acc[2 * q + 1] = fmaf(wj, __uint_as_float(wd[q] & 0xffff0000u), acc[2 * q + 1]);
-          }
-        }
-      }
-      store_vals<8, bf16_t>(a.r_out + n * a.r_stride + static_cast<int64_t>(h) * a.dh + c0, acc);
     }
   }
+  store_vals<8, bf16_t>(a.r_out + n * a.r_stride + static_cast<int64_t>(h) * a.dh + 8 * pc, acc);
 }
 
 template <int HALF>
@@ -227,7 +212,7 @@ struct TableStepLaunch {
   template <int CAP, int MODE>
   static int go(const Plan& p, const TableStepArgs& a, hipStream_t st) {
     const int64_t N = static_cast<int64_t>(p.B) * p.T;
-    const dim3 grid(static_cast<unsigned>((N + kStepGroup - 1) / kStepGroup), p.H);
+    const dim3 grid(static_cast<unsigned>(N), p.H);
     if (a.rx)
       hipLaunchKernelGGL((table_step_kernel<HALF, CAP, MODE, true>), grid, dim3(256), 0, st, a);
     else
@@ -286,9 +271,9 @@ int table_step_impl(const sdm_rt_dims* dims, const sdm_rt_params* params, const 
   if (d <= 0 || d % 64 != 0) return set_err(SDM_RT_EUNSUPPORTED, "table_step: d = %d must be a positive multiple of 64", d);
   if (p.d_a % 32 != 0 || p.d_a > 64)
     return set_err(SDM_RT_EUNSUPPORTED, "table_step: addr_dim = %d must be 32 or 64", p.d_a);
-  if (p.dh % 8 != 0 || p.dh > 512 * kPieces)
+  if (p.dh % 8 != 0 || p.dh > kMaxHeadDim)
     return set_err(SDM_RT_EUNSUPPORTED, "table_step: head_dim = %d must be a multiple of 8 up to %d", p.dh,
-                   512 * kPieces);
+                   kMaxHeadDim);
   if (p.pitch != p.cap) return set_err(SDM_RT_EUNSUPPORTED, "table_step: pick pitch %d", p.pitch);
   if ((!res && !hx) || !wq || !values || !slot_out || !out)
     return set_err(SDM_RT_EINVAL, "hx, wq, values, slot_out and out must not be NULL");
