@@ -272,7 +272,7 @@ int sdm_rt_silu_mul(const void* gate_up, int64_t gate_up_row_stride, sdm_rt_dtyp
  * track4_onesdm_models.py:199-207, :247; TrainedSdm's wq and wo, :443-455) when x holds one token per stream.
  *   x  [rows][k] bf16, row stride >= k;  W  [n][k] bf16 (a Linear's weight), row stride >= k;  bias  [n] bf16 or NULL;
  *   y  [rows][n] bf16, row stride >= n.  n a multiple of 32, k a positive multiple of 64, x and W rows 16-byte
- *   aligned.  Every workgroup takes 32 columns (and 32 or 64 rows) and splits k over four waves, whose sums are
+ *   aligned.  Every workgroup takes 32 columns (and 16, 32 or 64 rows) and splits k over four waves, whose sums are
  *   added in a fixed order (deterministic, and the same bits for every tiling). */
 int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, const void* bias,
                      void* y, int64_t y_row_stride, int64_t rows, int32_t n, int32_t k, void* stream);
@@ -282,7 +282,7 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
  * normalises the sum before its projections (RunTimeSdm.prepare's norm and maps, :197-206; RMSNorm,
  * track4_sdmllm_models.py:69-71).  Here sum_out = x + y (bf16) and out = rms_norm(sum_out, norm_w, norm_eps) W^T
  * (+ bias), bit for bit sdm_rt_add_rms_norm (bf16 in and out) followed by sdm_rt_gemm_rows, in one launch: each
- * workgroup normalises its 32 rows on chip.
+ * workgroup normalises its rows (16 or 32) on chip.
  *   x, y, sum_out  [rows][k] bf16, row strides >= k;  norm_w  [k] float32;  W, bias, out  as sdm_rt_gemm_rows
  * k = 768, n a positive multiple of 32, at most 256 tiles of 64 rows x 32 columns (a decode step's map; larger
  * calls return SDM_RT_EUNSUPPORTED).  x, y, sum_out and W rows and norm_w 16-byte aligned; sum_out and out must not

@@ -66,12 +66,14 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const bf16_t* __restrict
   }
 }
 
-// k = 768, few column tiles (a decode step's layer maps): blocks of 32 rows x 32 columns, twice the blocks of the
-// 64-row tiling for the same map, each loading half the rows of x; every operand of a wave (12 16-deep steps) is
-// loaded before its first product (one round trip).  Wave w's sums are those of gemm_rows_kernel's first accumulator.
+// k = 768, few column tiles (a decode step's layer maps): blocks of TR = 32 or 16 rows x 32 columns, two or four
+// times the blocks of the 64-row tiling for the same map, each loading a half or a quarter of the rows of x (the
+// launcher takes the smaller tile while the blocks still fit the compute units at once); every operand of a wave
+// (12 16-deep steps) is loaded before its first product (one round trip).  Wave w's sums are those of
+// gemm_rows_kernel's first accumulator (with TR = 16 the operand rows past the tile repeat its last row, unused).
 // FOLD: x is rms_norm(x + y) (OneSdmLM's residual add and the next layer's input norm in front of its map): the block
-// computes its 32 rows' sums and norms with the norm kernel's own code (norm_rows: the same bits as
-// sdm_rt_add_rms_norm, four rows per half-wave, every load first) into LDS, column tile 0's blocks write the sums,
+// computes its TR rows' sums and norms with the norm kernel's own code (norm_rows: the same bits as
+// sdm_rt_add_rms_norm, TR / 8 rows per half-wave, every load first) into LDS, column tile 0's blocks write the sums,
 // and the operands come from LDS (rows padded by 16 bytes, so the 32 rows an operand load reads spread over the banks).
 constexpr int kRowsK = 768;
 constexpr int kRowsSteps = kRowsK / 64;   // 16-deep steps per wave
@@ -86,23 +88,25 @@ struct RowsFold {   // the residual add and norm in front of the map (FOLD)
   int64_t ss;
 };
 
-template <bool FOLD>
-__global__ void __launch_bounds__(256) gemm_rows32_kernel(const bf16_t* __restrict__ x, int64_t xs,
+template <int TR, bool FOLD>
+__global__ void __launch_bounds__(256) gemm_rows_tile_kernel(const bf16_t* __restrict__ x, int64_t xs,
                                                           const bf16_t* __restrict__ w, int64_t ws,
                                                           const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
                                                           int64_t ys, int rows, RowsFold fold) {
   __shared__ float part[4][16][64];   // [wave][accumulator register][lane]
-  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? 32 : 1][FOLD ? kFoldRow : 8];
+  static_assert(TR == 16 || TR == 32, "tiles of 16 or 32 rows");
+  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? TR : 1][FOLD ? kFoldRow : 8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * kGemmCols, m0 = blockIdx.y * 32;
+  const int n0 = blockIdx.x * kGemmCols, m0 = blockIdx.y * TR;
   const int kb = wave * (kRowsK / 4) + 8 * (lane >> 5);
   const int r = lane & 31;
+  const int ra = min(min(r, TR - 1), rows - 1 - m0);   // the operand row in the tile: past it or past the end clamped
   const bf16_t* b = w + static_cast<int64_t>(n0 + r) * ws + kb;
   uint4 av[kRowsSteps], bv[kRowsSteps];
   if constexpr (FOLD) {
 #pragma unroll
     for (int s = 0; s < kRowsSteps; ++s) bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
-    constexpr int R = 4;   // rows 8 j + 2 wave + lane / 32 of the tile, j < 4, for half-wave (wave, lane / 32)
+    constexpr int R = TR / 8;   // rows 8 j + 2 wave + lane / 32 of the tile, j < R, for half-wave (wave, lane / 32)
     const bf16_t* xr[R];
     const bf16_t* yr[R];
     bf16_t* sr[R];
@@ -121,11 +125,11 @@ __global__ void __launch_bounds__(256) gemm_rows32_kernel(const bf16_t* __restri
     }
     norm_rows<bf16_t, bf16_t, true, kRowsK / 256, R>(xr, yr, sr, dr, fold.w, kRowsK, fold.eps, lane, live, keep);
     __syncthreads();
-    const bf16_t* a = &s_hx[min(r, rows - 1 - m0)][kb];   // rows past the end: clamped
+    const bf16_t* a = &s_hx[ra][kb];
 #pragma unroll
     for (int s = 0; s < kRowsSteps; ++s) av[s] = *reinterpret_cast<const uint4*>(a + 16 * s);
   } else {
-    const bf16_t* a = x + static_cast<int64_t>(min(m0 + r, rows - 1)) * xs + kb;   // rows past the end: clamped
+    const bf16_t* a = x + static_cast<int64_t>(m0 + ra) * xs + kb;
 #pragma unroll
     for (int s = 0; s < kRowsSteps; ++s) {
       bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
@@ -151,9 +155,13 @@ __global__ void __launch_bounds__(256) gemm_rows32_kernel(const bf16_t* __restri
     v += part[1][reg][lane];
     v += part[2][reg][lane];
     v += part[3][reg][lane];
-    if (m < rows) reinterpret_cast<uint16_t*>(y)[static_cast<int64_t>(m) * ys + n] = static_cast<uint16_t>(pack_bf16(v + bb, 0.f));
+    if (m < rows && m - m0 < TR)
+      reinterpret_cast<uint16_t*>(y)[static_cast<int64_t>(m) * ys + n] = static_cast<uint16_t>(pack_bf16(v + bb, 0.f));
   }
 }
+
+// the row tile of a few-rows map: 16 rows while the blocks fit the compute units at once, else 32
+inline int map_tile_rows(int ntiles, int64_t rows) { return static_cast<int64_t>(ntiles) * ((rows + 15) / 16) <= 256 ? 16 : 32; }
 
 // k = 768, many column tiles (the tied head over the vocabulary): a block per 64-row tile and 256 / (row tiles)
 // column positions; its waves load their x operands once and walk the column tiles blockIdx.x, blockIdx.x +
@@ -241,10 +249,15 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
   const int ntiles = n / kGemmCols;
   const int row_tiles = static_cast<int>((rows + kGemmRows - 1) / kGemmRows);
   if (k == kRowsK && static_cast<int64_t>(ntiles) * row_tiles <= 256) {
-    // a decode step's layer maps: 32-row tiles
-    hipLaunchKernelGGL(gemm_rows32_kernel<false>,
-                       dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + 31) / 32)), dim3(256), 0, st, xb,
-                       x_row_stride, wb, w_row_stride, bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
+    // a decode step's layer maps: 16- or 32-row tiles
+    const int tr = map_tile_rows(ntiles, rows);
+    const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + tr - 1) / tr));
+    if (tr == 16)
+      hipLaunchKernelGGL((gemm_rows_tile_kernel<16, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
+                         bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
+    else
+      hipLaunchKernelGGL((gemm_rows_tile_kernel<32, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
+                         bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
   } else if (k == kRowsK && row_tiles <= 256) {
     // wide maps: about one block per compute unit, each walking its column tiles
     const int cols = min(ntiles, max(1, 256 / row_tiles));
@@ -289,10 +302,19 @@ int sdm_rt_gemm_rows_residual(const void* x, int64_t x_row_stride, const void* y
     return set_err(SDM_RT_EINVAL, "gemm_rows_residual: sum_out and out must not alias x, y or each other");
   const RowsFold fold{static_cast<const bf16_t*>(y), y_row_stride, norm_w, norm_eps, static_cast<bf16_t*>(sum_out),
                       sum_row_stride};
-  hipLaunchKernelGGL(gemm_rows32_kernel<true>, dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + 31) / 32)),
-                     dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x), x_row_stride,
-                     static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(bias),
-                     static_cast<bf16_t*>(out), out_row_stride, static_cast<int>(rows), fold);
+  const int tr = map_tile_rows(ntiles, rows);
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + tr - 1) / tr));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t* xb = static_cast<const bf16_t*>(x);
+  const bf16_t* wb = static_cast<const bf16_t*>(w);
+  const bf16_t* bb = static_cast<const bf16_t*>(bias);
+  bf16_t* ob = static_cast<bf16_t*>(out);
+  if (tr == 16)
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<16, true>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+                       ob, out_row_stride, static_cast<int>(rows), fold);
+  else
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<32, true>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+                       ob, out_row_stride, static_cast<int>(rows), fold);
   return check_launch("gemm_rows_residual");
 }
 

@@ -73,16 +73,18 @@ def _gemm_rows(x, w, b=None):
 
 
 def test_gemm_rows_kernels_give_the_same_bits():
-    """k = 768: the launcher takes 32-row tiles for few column tiles (<= 256 of 64 rows x 32 columns), the walking
-    kernel for wide maps (the tied head) and the general 64-row kernel past 256 row tiles; all three sum every
-    element in the same order, so a product's bits do not depend on which one ran."""
+    """k = 768: the launcher takes tiles of 16 rows while they fit the compute units at once and of 32 rows past that
+    (few column tiles: <= 256 of 64 rows x 32 columns), the walking kernel for wide maps (the tied head) and the
+    general 64-row kernel past 256 row tiles; all sum every element in the same order, so a product's bits do not
+    depend on which one ran."""
     g = torch.Generator(device="cpu").manual_seed(11)
     x = torch.randn(16448, 768, generator=g).to(torch.bfloat16).cuda()          # 257 tiles of 64 rows
     w = (torch.randn(8224, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()  # 257 column tiles
     b = torch.randn(8224, generator=g).to(torch.bfloat16).cuda()
-    say("gemm_rows kernels: 32-row tiles, wide walk, general")
+    say("gemm_rows kernels: 16- and 32-row tiles, wide walk, general")
     with torch.no_grad():
-        narrow = _gemm_rows(x[:64], w[:64], b[:64])        # 2 column tiles: 32-row tiles
+        narrow = _gemm_rows(x[:64], w[:64], b[:64])        # 2 column tiles: 16-row tiles
+        narrow32 = _gemm_rows(x[:64], w[:2560], b[:2560])  # 80 column tiles: 32-row tiles
         general = _gemm_rows(x, w[:64], b[:64])            # 257 row tiles: the general kernel
         wide = _gemm_rows(x[:64], w, b)                    # 257 column tiles: the walking kernel, 256 columns
         wide200 = _gemm_rows(x[:200], w, b)                # 4 row tiles: 64 columns, each walking ~4 tiles
@@ -90,6 +92,7 @@ def test_gemm_rows_kernels_give_the_same_bits():
         torch.cuda.synchronize()
     assert torch.equal(general[:64].view(torch.int16), narrow.view(torch.int16))
     assert torch.equal(wide[:, :64].view(torch.int16), narrow.view(torch.int16))
+    assert torch.equal(wide[:, :2560].view(torch.int16), narrow32.view(torch.int16))
     assert torch.equal(wide200[:64].view(torch.int16), wide.view(torch.int16))
     assert torch.equal(wide200[:, 4096:4160].view(torch.int16), narrow200.view(torch.int16))
     want = _ref(x[:200], w, b)
