@@ -77,7 +77,19 @@ typedef struct {
                            * sdm_rt_address (may be NULL there) */
   const float* onorm_w;   /* [H][dh]; read only when out_norm */
   const float* gate_bias; /* [H] bias of the gate projection; may be NULL (zero) */
+  const void* key_pieces; /* the bfloat16 scoring's sub-key pieces, prepared by sdm_rt_prepare_key_pieces from these
+                           * keys1, keys2 and addr_b for the same heads, addr_dim and n_sub (and prepared again
+                           * after any of them changes), or NULL: the scoring then derives them itself */
 } sdm_rt_params;
+
+/* No reference counterpart: the unit normalisation of the sub-keys (F.normalize of keys1/keys2,
+ * track4_onesdm_models.py:137-140), their three-term bfloat16 split and their dot products with addr_b, which every
+ * bfloat16 scoring of an address set otherwise recomputes, prepared once per parameter version into a caller-owned
+ * buffer of sdm_rt_key_pieces_bytes(dims) bytes (0: the shape's scoring does not use them).  The same values the
+ * scoring derives, so the same picks.  params->key_pieces is ignored here. */
+size_t sdm_rt_key_pieces_bytes(const sdm_rt_dims* dims);
+int sdm_rt_prepare_key_pieces(const sdm_rt_dims* dims, const sdm_rt_params* params, void* out, size_t out_bytes,
+                              void* stream);
 
 /* Bytes of workspace sdm_rt_forward needs for these dimensions (0 on invalid dims): the chunk plans (33 KB per
  * 64 positions of one head at k <= 8) and their sizes, the scan's progress counters and status word and, with

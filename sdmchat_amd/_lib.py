@@ -42,6 +42,7 @@ class SdmRtParams(ctypes.Structure):
         ("decay", c_void_p),
         ("onorm_w", c_void_p),
         ("gate_bias", c_void_p),
+        ("key_pieces", c_void_p),
     ]
 
 
@@ -122,6 +123,9 @@ SIGNATURES = {
                                            c_void_p]),
     "sdm_rt_silu_mul": (ctypes.c_int, [c_void_p, c_i64, ctypes.c_int, c_i64, ctypes.c_int32, c_void_p, c_i64,
                                        c_void_p]),
+    "sdm_rt_key_pieces_bytes": (ctypes.c_size_t, [ctypes.POINTER(SdmRtDims)]),
+    "sdm_rt_prepare_key_pieces": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams), c_void_p,
+                                                 ctypes.c_size_t, c_void_p]),
     "sdm_rt_gemm_rows": (ctypes.c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_i64,
                                         ctypes.c_int32, ctypes.c_int32, c_void_p]),
     "sdm_rt_gemm_rows_residual": (ctypes.c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, ctypes.c_float,

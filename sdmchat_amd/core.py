@@ -64,8 +64,22 @@ def _rows2(x, name, B, width):
 
 
 def _params(device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias):
+    """The SdmRtParams of these parameters (float32, contiguous copies where needed) with the sub-key pieces of the
+    bfloat16 scoring prepared from them (sdm_rt_prepare_key_pieces, one launch).  Returns (params, held tensors);
+    build them again after a parameter changes (ParamCache does)."""
     held = [_f32(t, device) for t in (keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias)]
     prm = _lib.SdmRtParams(*[_ptr(t) for t in held])
+    H, n_sub, half = held[0].shape
+    dims = make_dims(1, 1, H, 8, 2 * half, n_sub, 1)
+    lib = _lib.load()
+    nbytes = lib.sdm_rt_key_pieces_bytes(ctypes.byref(dims))
+    if nbytes:
+        pieces = torch.empty(nbytes, dtype=torch.uint8, device=held[0].device)
+        stream = torch.cuda.current_stream(pieces.device).cuda_stream
+        _lib.check(lib.sdm_rt_prepare_key_pieces(ctypes.byref(dims), ctypes.byref(prm), _ptr(pieces), nbytes,
+                                                 ctypes.c_void_p(stream)), lib)
+        prm.key_pieces = _ptr(pieces)
+        held.append(pieces)
     return prm, held
 
 

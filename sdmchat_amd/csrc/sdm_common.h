@@ -83,6 +83,9 @@ struct AddrGeom {
   const float* addr_b;     // [H][d_a] or nullptr
   const float* log_scale;  // [H]
   const float* gate_bias;  // [H] or nullptr
+  // the bfloat16 scoring's sub-key pieces prepared once for these keys and addr_b (sdm_rt_prepare_key_pieces,
+  // KeyPieces below), or nullptr: every scoring wave then normalises and splits its sub-keys itself
+  const uint32_t* kpieces;
   int H, n_sub, c1, kk;
 };
 
@@ -545,13 +548,30 @@ __device__ __forceinline__ void half_scores_f32(const AddrGeom& g, int h, int hf
 // enters through the accumulator's start value c_i = k_i . addr_b (one float32 matrix step: c_i x 1) and through
 // inv.  Lane l feeds dims 16q + 8(l/32) + e (e < 8) of sub-key row l%32 and of both address rows (HALF = 8: lanes
 // 32..63 feed zeros).  Head h's address columns start at column zcol of a row (h * 2 HALF when zcol < 0).
-// The lane's sub-key piece and address-bias piece of half_scores_bf16 (loaded ahead by a caller whose addresses
-// come from LDS, so that the loads leave the scoring's critical path).
+// The layout of the prepared sub-key pieces of the bfloat16 scoring (HALF: half width, NSP: sub-key rows per half
+// rounded up to 32): per (head, half, sub-key row, lane half) the 3 Q x 4 words of the three bfloat16 terms that
+// lane feeds the matrix cores, then per (head, half, sub-key row) the float32 c = k . addr_b.
+template <int HALF>
+struct KeyPieces {
+  static constexpr int Q = (HALF + 15) / 16;
+  static constexpr int kWords = 3 * Q * 4;   // per lane
+  __host__ __device__ static constexpr int64_t term_words(int H, int nsp) { return static_cast<int64_t>(H) * 2 * nsp * 2 * kWords; }
+  __host__ __device__ static constexpr int64_t bytes(int H, int nsp) { return 4 * (term_words(H, nsp) + static_cast<int64_t>(H) * 2 * nsp); }
+};
+__host__ __device__ constexpr int key_piece_rows(int n_sub) { return (n_sub + 31) / 32 * 32; }
+
+// The lane's part of the bfloat16 scoring of half hf against sub-key tile kofs (lane l: sub-key row kofs + l % 32,
+// dims 16 q + 8 (l / 32) + e): the three bfloat16 terms of its unit sub-key piece (k = k0 + k1 + k2 + r, each term
+// the nearest bfloat16 to what is left), c = k . addr_b over the whole row, and its address-bias piece.
 template <int HALF>
 struct SubKeyPiece {
   static constexpr int Q = (HALF + 15) / 16;
-  float ka[Q][8], ab[Q][8];
+  uint32_t kt[3][Q][4];   // the terms, packed in pairs
+  float c;
+  float ab[Q][8];
 };
+// computes the lane's piece from the sub-keys (sub-key rows past n_sub: zero terms; all 64 lanes take part), or
+// loads it when g.kpieces holds the prepared pieces (the same values: sdm_rt_prepare_key_pieces computes them here)
 template <int HALF>
 __device__ __forceinline__ void load_sub_key_piece(const AddrGeom& g, int h, int hf, int kofs, SubKeyPiece<HALF>& kp) {
   constexpr int Q = SubKeyPiece<HALF>::Q;
@@ -560,15 +580,8 @@ __device__ __forceinline__ void load_sub_key_piece(const AddrGeom& g, int h, int
   const bool has = HALF >= 16 || kb == 0;
   const int d0 = hf * HALF + 8 * kb;
   const int kr = kofs + jl;
-  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + 8 * kb;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
-    if (has) {
-      load_vals<8, float>(krow + 16 * q, kp.ka[q]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kp.ka[q][e] = 0.f;
-    }
     if (g.addr_b && has) {
       load_vals<8, float>(g.addr_b + h * 2 * HALF + d0 + 16 * q, kp.ab[q]);
     } else {
@@ -576,24 +589,90 @@ __device__ __forceinline__ void load_sub_key_piece(const AddrGeom& g, int h, int
       for (int e = 0; e < 8; ++e) kp.ab[q][e] = 0.f;
     }
   }
+  if (g.kpieces) {
+    const int nsp = key_piece_rows(g.n_sub);
+    const int64_t row = (static_cast<int64_t>(h) * 2 + hf) * nsp + min(kr, nsp - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(g.kpieces + (row * 2 + kb) * KeyPieces<HALF>::kWords);
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const uint4 v = src[t * Q + q];
+        kp.kt[t][q][0] = v.x;
+        kp.kt[t][q][1] = v.y;
+        kp.kt[t][q][2] = v.z;
+        kp.kt[t][q][3] = v.w;
+      }
+    kp.c = reinterpret_cast<const float*>(g.kpieces + KeyPieces<HALF>::term_words(g.H, nsp))[row];
+    return;
+  }
+  float ka[Q][8];
+  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + 8 * kb;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if (has) {
+      load_vals<8, float>(krow + 16 * q, ka[q]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ka[q][e] = 0.f;
+    }
+  }
+  {   // unit-normalised sub-key row (rows past n_sub: zero)
+    float ks = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ks = fmaf(ka[q][e], ka[q][e], ks);
+    const auto kpv = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
+    const float kinv = kr < g.n_sub ? inv_norm(__uint_as_float(kpv[0]) + __uint_as_float(kpv[1])) : 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ka[q][e] *= kinv;
+  }
+  {   // c = k . addr_b (the address bias enters the scores through the accumulator's start value)
+    float cp = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cp = fmaf(ka[q][e], kp.ab[q][e], cp);
+    const auto cw = __builtin_amdgcn_permlane32_swap(__float_as_uint(cp), __float_as_uint(cp), false, false);
+    kp.c = __uint_as_float(cw[0]) + __uint_as_float(cw[1]);
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float x0 = ka[q][2 * e2], x1 = ka[q][2 * e2 + 1];
+#pragma unroll
+      for (int term = 0; term < 3; ++term) {
+        const uint32_t pk = pack_bf16(x0, x1);
+        kp.kt[term][q][e2] = pk;
+        x0 -= __uint_as_float(pk << 16);   // exact
+        x1 -= __uint_as_float(pk & 0xffff0000u);
+      }
+    }
+  }
 }
 
-// pre: the lane's sub-key piece loaded ahead (load_sub_key_piece with the same h, hf, kofs), or nullptr to load it
-// here (with the address loads)
+// bfloat16 matrix cores (bfloat16 addresses, HALF a multiple of 8): each unit sub-key is split into three bfloat16
+// terms k = k0 + k1 + k2 + r (k0 the nearest bfloat16 to k, k1 to k - k0, k2 to k - k0 - k1; |r| <= 2^-27 |k|), the
+// address values are bfloat16 already, so every product is exact in the float32 accumulation.  The address bias
+// enters through the accumulator's start value c_i = k_i . addr_b (one float32 matrix step: c_i x 1) and through
+// inv.  Lane l feeds dims 16q + 8(l/32) + e (e < 8) of sub-key row l%32 and of both address rows (HALF = 8: lanes
+// 32..63 feed zeros).  Head h's address columns start at column zcol of a row (h * 2 HALF when zcol < 0).  kp: the
+// lane's sub-key piece (load_sub_key_piece with the same h, hf and sub-key tile).  Sub-key rows past n_sub score 0.
 template <int HALF, bool FULL>
-__device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
-                                                 int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0,
-                                                 int zcol = -1, const SubKeyPiece<HALF>* pre = nullptr) {
+__device__ __forceinline__ void half_scores_bf16_with(const AddrGeom& g, int h, int hf, const bf16_t* z0,
+                                                      int64_t zstride, int rows, floatx16 (&acc)[2], float (&inv)[2],
+                                                      int zcol, const SubKeyPiece<HALF>& kp) {
   static_assert(HALF % 8 == 0, "bfloat16 scoring feeds 8 dims per lane");
   constexpr int Q = (HALF + 15) / 16;
   const int l = threadIdx.x & 63;
   const int kb = l >> 5, jl = l & 31;
   const bool has = HALF >= 16 || kb == 0;
   const int d0 = hf * HALF + 8 * kb;   // first dim of the address this lane feeds
-  float ka[Q][8], ab[Q][8];
   uint4 zr[2][Q];
-  const int kr = kofs + jl;   // this lane's sub-key row (kofs: the sub-key tile, 0 or 32)
-  const float* krow = g.keys[hf] + (static_cast<int64_t>(h) * g.n_sub + min(kr, g.n_sub - 1)) * HALF + 8 * kb;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
 #pragma unroll
@@ -603,66 +682,9 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
                                  16 * q)
                      : make_uint4(0u, 0u, 0u, 0u);
     }
-    if (pre) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ka[q][e] = pre->ka[q][e];
-        ab[q][e] = pre->ab[q][e];
-      }
-      continue;
-    }
-    if (has) {
-      load_vals<8, float>(krow + 16 * q, ka[q]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ka[q][e] = 0.f;
-    }
-    if (g.addr_b && has) {
-      load_vals<8, float>(g.addr_b + h * 2 * HALF + d0 + 16 * q, ab[q]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ab[q][e] = 0.f;
-    }
-  }
-  {   // unit-normalised sub-key row
-    float ks = 0.f;
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ks = fmaf(ka[q][e], ka[q][e], ks);
-    const auto kp = __builtin_amdgcn_permlane32_swap(__float_as_uint(ks), __float_as_uint(ks), false, false);
-    const float kinv = (FULL || kr < g.n_sub) ? inv_norm(__uint_as_float(kp[0]) + __uint_as_float(kp[1])) : 0.f;
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ka[q][e] *= kinv;
   }
   floatx16 init = {};
-  if (g.addr_b) {
-    float cp = 0.f;
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cp = fmaf(ka[q][e], ab[q][e], cp);
-    const auto cw = __builtin_amdgcn_permlane32_swap(__float_as_uint(cp), __float_as_uint(cp), false, false);
-    const float c = __uint_as_float(cw[0]) + __uint_as_float(cw[1]);
-    init = __builtin_amdgcn_mfma_f32_32x32x2f32(kb == 0 ? c : 0.f, kb == 0 ? 1.f : 0.f, init, 0, 0, 0);
-  }
-  uint32_t kt[3][Q][4];   // the three bfloat16 terms, packed in pairs
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      float x0 = ka[q][2 * e2], x1 = ka[q][2 * e2 + 1];
-#pragma unroll
-      for (int term = 0; term < 3; ++term) {
-        const uint32_t p = pack_bf16(x0, x1);
-        kt[term][q][e2] = p;
-        x0 -= __uint_as_float(p << 16);   // exact
-        x1 -= __uint_as_float(p & 0xffff0000u);
-      }
-    }
-  }
+  if (g.addr_b) init = __builtin_amdgcn_mfma_f32_32x32x2f32(kb == 0 ? kp.c : 0.f, kb == 0 ? 1.f : 0.f, init, 0, 0, 0);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     float ss = 0.f;
@@ -671,8 +693,8 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
       const uint32_t wd[4] = {zr[t][q].x, zr[t][q].y, zr[t][q].z, zr[t][q].w};
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const float v0 = __uint_as_float(wd[e2] << 16) + ab[q][2 * e2];
-        const float v1 = __uint_as_float(wd[e2] & 0xffff0000u) + ab[q][2 * e2 + 1];
+        const float v0 = __uint_as_float(wd[e2] << 16) + kp.ab[q][2 * e2];
+        const float v1 = __uint_as_float(wd[e2] & 0xffff0000u) + kp.ab[q][2 * e2 + 1];
         ss = fmaf(v0, v0, ss);
         ss = fmaf(v1, v1, ss);
       }
@@ -684,12 +706,22 @@ __device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int h
     for (int q = 0; q < Q; ++q) {
 #pragma unroll
       for (int term = 2; term >= 0; --term) {
-        const uint4 kq = make_uint4(kt[term][q][0], kt[term][q][1], kt[term][q][2], kt[term][q][3]);
+        const uint4 kq = make_uint4(kp.kt[term][q][0], kp.kt[term][q][1], kp.kt[term][q][2], kp.kt[term][q][3]);
         acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kq),
                                                          __builtin_bit_cast(bf16x8, zr[t][q]), acc[t], 0, 0, 0);
       }
     }
   }
+}
+
+// half_scores_bf16_with on the lane's sub-key piece of tile kofs, loaded here after the address loads issue
+template <int HALF, bool FULL>
+__device__ __forceinline__ void half_scores_bf16(const AddrGeom& g, int h, int hf, const bf16_t* z0, int64_t zstride,
+                                                 int rows, floatx16 (&acc)[2], float (&inv)[2], int kofs = 0,
+                                                 int zcol = -1) {
+  SubKeyPiece<HALF> kp;
+  load_sub_key_piece<HALF>(g, h, hf, kofs, kp);
+  half_scores_bf16_with<HALF, FULL>(g, h, hf, z0, zstride, rows, acc, inv, zcol, kp);
 }
 
 // The CAP best offset keys (descending) of half hf of the wave's 64 addresses over sub-key tile `tile` (sub-keys
@@ -1259,6 +1291,8 @@ inline AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm) {
   g.addr_b = prm->addr_b;
   g.log_scale = prm->log_scale;
   g.gate_bias = prm->gate_bias;
+  const bool mf = p.half == 8 || p.half == 16 || p.half == 32;   // the bfloat16 matrix-core scoring's widths
+  g.kpieces = mf && p.n_sub <= 64 ? static_cast<const uint32_t*>(prm->key_pieces) : nullptr;
   g.H = p.H;
   g.n_sub = p.n_sub;
   g.c1 = p.c1;

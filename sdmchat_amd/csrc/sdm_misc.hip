@@ -184,11 +184,72 @@ int norm_launch(int kc, unsigned blocks, hipStream_t st, Args... args) {
   return SDM_RT_OK;
 }
 
+// sdm_rt_prepare_key_pieces: block (head, half, sub-key tile of 32 rows), one wave; each lane computes its piece as
+// the scoring does (load_sub_key_piece) and stores it in the KeyPieces layout
+template <int HALF>
+__global__ void __launch_bounds__(64) key_pieces_kernel(AddrGeom g, uint32_t* __restrict__ out) {
+  constexpr int Q = SubKeyPiece<HALF>::Q;
+  const int h = blockIdx.x, hf = blockIdx.y, tile = blockIdx.z;
+  g.kpieces = nullptr;
+  SubKeyPiece<HALF> kp;
+  load_sub_key_piece<HALF>(g, h, hf, 32 * tile, kp);
+  const int l = threadIdx.x & 63, kb = l >> 5;
+  const int nsp = key_piece_rows(g.n_sub);
+  const int64_t row = (static_cast<int64_t>(h) * 2 + hf) * nsp + 32 * tile + (l & 31);
+  uint4* dst = reinterpret_cast<uint4*>(out + (row * 2 + kb) * KeyPieces<HALF>::kWords);
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int q = 0; q < Q; ++q) dst[t * Q + q] = make_uint4(kp.kt[t][q][0], kp.kt[t][q][1], kp.kt[t][q][2], kp.kt[t][q][3]);
+  if (kb == 0) reinterpret_cast<float*>(out + KeyPieces<HALF>::term_words(g.H, nsp))[row] = kp.c;
+}
+
+inline int64_t key_pieces_bytes(const Plan& p) {
+  if (!mf_half(p.half) || p.n_sub > 64) return 0;
+  const int nsp = key_piece_rows(p.n_sub);
+  switch (p.half) {
+    case 8: return KeyPieces<8>::bytes(p.H, nsp);
+    case 16: return KeyPieces<16>::bytes(p.H, nsp);
+    default: return KeyPieces<32>::bytes(p.H, nsp);
+  }
+}
+
 }  // namespace sdmrt
 
 using namespace sdmrt;
 
 extern "C" {
+
+size_t sdm_rt_key_pieces_bytes(const sdm_rt_dims* dims) {
+  Plan p;
+  if (!dims || make_plan(dims, &p, false)) return 0;
+  return static_cast<size_t>(key_pieces_bytes(p));
+}
+
+int sdm_rt_prepare_key_pieces(const sdm_rt_dims* dims, const sdm_rt_params* params, void* out, size_t out_bytes,
+                              void* stream) {
+  g_err[0] = 0;
+  if (!dims || !params) return set_err(SDM_RT_EINVAL, "dims and params must not be NULL");
+  Plan p;
+  int rc = make_plan(dims, &p, false);
+  if (rc) return rc;
+  if (!params->keys1 || !params->keys2) return set_err(SDM_RT_EINVAL, "keys1 and keys2 must not be NULL");
+  const int64_t need = key_pieces_bytes(p);
+  if (need == 0) return set_err(SDM_RT_EUNSUPPORTED, "key pieces: no bfloat16 matrix-core scoring for this shape");
+  if (!out || static_cast<int64_t>(out_bytes) < need)
+    return set_err(SDM_RT_ENOSPACE, "key pieces: %zu bytes given, %lld needed", out_bytes, (long long)need);
+  if (reinterpret_cast<uintptr_t>(out) % 16) return set_err(SDM_RT_EINVAL, "key pieces: out must be 16-byte aligned");
+  AddrGeom g = addr_geom(p, params);
+  const dim3 grid(static_cast<unsigned>(p.H), 2, static_cast<unsigned>(key_piece_rows(p.n_sub) / 32));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint32_t* o = static_cast<uint32_t*>(out);
+  switch (p.half) {
+    case 8: hipLaunchKernelGGL(key_pieces_kernel<8>, grid, dim3(64), 0, st, g, o); break;
+    case 16: hipLaunchKernelGGL(key_pieces_kernel<16>, grid, dim3(64), 0, st, g, o); break;
+    default: hipLaunchKernelGGL(key_pieces_kernel<32>, grid, dim3(64), 0, st, g, o); break;
+  }
+  return check_launch("prepare_key_pieces");
+}
 
 int sdm_rt_rms_norm(const void* x, int64_t x_row_stride, sdm_rt_dtype in_dtype, int64_t rows, int32_t d,
                     const float* w, float eps, void* out, int64_t out_row_stride, sdm_rt_dtype out_dtype,

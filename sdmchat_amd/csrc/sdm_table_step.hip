@@ -150,8 +150,7 @@ __global__ void __launch_bounds__(256) table_step_kernel(TableStepArgs a) {
     const int hf = wave / NT, tile = wave % NT;
     floatx16 acc[2];
     float inv[2];
-    half_scores_bf16<HALF, FULL>(a.g, h, hf, reinterpret_cast<const bf16_t*>(s_q), DA, 1, acc, inv, 32 * tile, 0,
-                                 &kpre);
+    half_scores_bf16_with<HALF, FULL>(a.g, h, hf, reinterpret_cast<const bf16_t*>(s_q), DA, 1, acc, inv, 0, kpre);
     // lane l < 32 of the address row 0: sub-keys 32 tile + 8 (r / 4) + 4 (l / 32) + r % 4
     if ((lane & 31) == 0) {
 #pragma unroll

@@ -198,3 +198,18 @@ def test_gemm_rows_residual_arguments_are_checked_before_launch():
     assert call(64, 2560, 768, out=y) != 0 and "alias" in lib.sdm_rt_last_error().decode()
     assert call(64, 2560, 768, out=s) != 0 and "alias" in lib.sdm_rt_last_error().decode()
     assert call(0, 2560, 768) == 0   # no rows: nothing to do
+
+
+def test_prepare_key_pieces_checks_its_buffer():
+    """The prepared sub-key pieces: their size for a shape, none for a shape without matrix-core scoring, and a
+    buffer too small refused before launch."""
+    lib = _lib.load()
+    dims = core.make_dims(1, 1, 4, 8, 64, 32, 1)
+    need = lib.sdm_rt_key_pieces_bytes(ctypes.byref(dims))
+    assert need == 4 * (4 * 2 * 32 * 2 * 24 + 4 * 2 * 32)
+    one = ctypes.c_void_p(16)
+    prm = _lib.SdmRtParams(one, one, None, one, None, None, None)
+    assert lib.sdm_rt_prepare_key_pieces(ctypes.byref(dims), ctypes.byref(prm), one, need - 16, None) != 0
+    assert "needed" in lib.sdm_rt_last_error().decode()
+    wide = core.make_dims(1, 1, 4, 8, 64, 128, 1)   # 128 sub-keys per half: no matrix-core scoring
+    assert lib.sdm_rt_key_pieces_bytes(ctypes.byref(wide)) == 0
