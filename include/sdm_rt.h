@@ -80,6 +80,8 @@ typedef struct {
   const void* key_pieces; /* the bfloat16 scoring's sub-key pieces, prepared by sdm_rt_prepare_key_pieces from these
                            * keys1, keys2 and addr_b for the same heads, addr_dim and n_sub (and prepared again
                            * after any of them changes), or NULL: the scoring then derives them itself */
+  size_t key_pieces_bytes; /* the size of that buffer; pieces smaller than sdm_rt_key_pieces_bytes(dims) of a call
+                            * are not read (the scoring derives them instead) */
 } sdm_rt_params;
 
 /* No reference counterpart: the unit normalisation of the sub-keys (F.normalize of keys1/keys2,

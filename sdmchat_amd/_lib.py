@@ -43,6 +43,7 @@ class SdmRtParams(ctypes.Structure):
         ("onorm_w", c_void_p),
         ("gate_bias", c_void_p),
         ("key_pieces", c_void_p),
+        ("key_pieces_bytes", ctypes.c_size_t),
     ]
 
 

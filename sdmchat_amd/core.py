@@ -79,6 +79,7 @@ def _params(device, keys1, keys2, addr_b, log_scale, decay, onorm_w, gate_bias):
         _lib.check(lib.sdm_rt_prepare_key_pieces(ctypes.byref(dims), ctypes.byref(prm), _ptr(pieces), nbytes,
                                                  ctypes.c_void_p(stream)), lib)
         prm.key_pieces = _ptr(pieces)
+        prm.key_pieces_bytes = nbytes
         held.append(pieces)
     return prm, held
 

@@ -1284,6 +1284,17 @@ inline int lds_err(const char* what) {
   return set_err(SDM_RT_ELAUNCH, "%s: cannot enable %zu bytes of LDS", what, kLdsBytes);
 }
 
+// bytes of the prepared sub-key pieces of a shape (0: no bfloat16 matrix-core scoring)
+inline int64_t key_pieces_bytes(const Plan& p) {
+  if (!(p.half == 8 || p.half == 16 || p.half == 32) || p.n_sub > 64) return 0;
+  const int nsp = key_piece_rows(p.n_sub);
+  switch (p.half) {
+    case 8: return KeyPieces<8>::bytes(p.H, nsp);
+    case 16: return KeyPieces<16>::bytes(p.H, nsp);
+    default: return KeyPieces<32>::bytes(p.H, nsp);
+  }
+}
+
 inline AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm) {
   AddrGeom g;
   g.keys[0] = prm->keys1;
@@ -1291,8 +1302,10 @@ inline AddrGeom addr_geom(const Plan& p, const sdm_rt_params* prm) {
   g.addr_b = prm->addr_b;
   g.log_scale = prm->log_scale;
   g.gate_bias = prm->gate_bias;
-  const bool mf = p.half == 8 || p.half == 16 || p.half == 32;   // the bfloat16 matrix-core scoring's widths
-  g.kpieces = mf && p.n_sub <= 64 ? static_cast<const uint32_t*>(prm->key_pieces) : nullptr;
+  const int64_t need = key_pieces_bytes(p);   // pieces too small for this shape are not read
+  g.kpieces = need > 0 && prm->key_pieces && static_cast<int64_t>(prm->key_pieces_bytes) >= need
+                  ? static_cast<const uint32_t*>(prm->key_pieces)
+                  : nullptr;
   g.H = p.H;
   g.n_sub = p.n_sub;
   g.c1 = p.c1;

@@ -204,16 +204,6 @@ __global__ void __launch_bounds__(64) key_pieces_kernel(AddrGeom g, uint32_t* __
   if (kb == 0) reinterpret_cast<float*>(out + KeyPieces<HALF>::term_words(g.H, nsp))[row] = kp.c;
 }
 
-inline int64_t key_pieces_bytes(const Plan& p) {
-  if (!mf_half(p.half) || p.n_sub > 64) return 0;
-  const int nsp = key_piece_rows(p.n_sub);
-  switch (p.half) {
-    case 8: return KeyPieces<8>::bytes(p.H, nsp);
-    case 16: return KeyPieces<16>::bytes(p.H, nsp);
-    default: return KeyPieces<32>::bytes(p.H, nsp);
-  }
-}
-
 }  // namespace sdmrt
 
 using namespace sdmrt;

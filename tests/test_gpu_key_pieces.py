@@ -12,13 +12,16 @@ pytestmark = pytest.mark.gpu
 
 
 def _both(p, dev):
-    """(params with prepared pieces, the same params without)."""
+    """(params with prepared pieces, the same params without, and with pieces whose stated size is too small for the
+    shape: not read)."""
     tp = {n: (torch.from_numpy(v).to(dev) if v is not None else None) for n, v in p.items()}
     with_p = core._params(dev, tp["keys1"], tp["keys2"], tp["addr_b"], tp["log_scale"], tp["decay"], tp["onorm_w"],
                           tp["gate_bias"])
-    assert with_p[0].key_pieces, "pieces prepared"
-    prm = _lib.SdmRtParams(*[getattr(with_p[0], f) for f, _ in _lib.SdmRtParams._fields_[:-1]])
-    return tp, with_p, (prm, with_p[1])
+    assert with_p[0].key_pieces and with_p[0].key_pieces_bytes > 0, "pieces prepared"
+    prm = _lib.SdmRtParams(*[getattr(with_p[0], f) for f, _ in _lib.SdmRtParams._fields_[:-2]])
+    short = _lib.SdmRtParams(*[getattr(with_p[0], f) for f, _ in _lib.SdmRtParams._fields_])
+    short.key_pieces_bytes = with_p[0].key_pieces_bytes - 16
+    return tp, with_p, (prm, with_p[1]), (short, with_p[1])
 
 
 @pytest.mark.parametrize("n_sub,d_a", [(32, 64), (64, 32), (16, 32), (32, 16)])
@@ -26,25 +29,26 @@ def test_address_with_prepared_pieces_equals_derived(n_sub, d_a):
     dev = torch.device("cuda")
     H, k = 4, 8
     kz, qz, V, g, p = core_inputs(2, 96, H, 32, d_a, n_sub, seed=n_sub + d_a, addr_bias=0.3)
-    tp, with_p, without = _both(p, dev)
+    tp, with_p, without, short = _both(p, dev)
     z = torch.from_numpy(kz).to(dev).to(torch.bfloat16)
     gl = torch.from_numpy(g).to(dev).to(torch.bfloat16)
     say("key pieces: address", n_sub, d_a)
     outs = []
-    for prm in (with_p, without):
+    for prm in (with_p, without, short):
         with torch.no_grad():
             outs.append(core.address(z, tp["keys1"], tp["keys2"], k, tp["log_scale"], addr_b=tp["addr_b"],
                                      gate_logits=gl, gate_bias=tp["gate_bias"], params=prm))
         torch.cuda.synchronize()
-    for a, b in zip(*outs):
-        assert torch.equal(a, b)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
 
 
 def test_core_forward_and_decode_with_prepared_pieces_equal_derived():
     dev = torch.device("cuda")
     B, T, H, dh, d_a, n_sub, k = 2, 256, 4, 64, 64, 32, 8
     kz, qz, V, g, p = core_inputs(B, T, H, dh, d_a, n_sub, seed=5, addr_bias=0.2)
-    tp, with_p, without = _both(p, dev)
+    tp, with_p, without, _ = _both(p, dev)
     t = [torch.from_numpy(a).to(dev).to(torch.bfloat16) for a in (kz, qz, V, g)]
     kw = dict(keys1=tp["keys1"], keys2=tp["keys2"], log_scale=tp["log_scale"], decay=tp["decay"],
               addr_b=tp["addr_b"], onorm_w=tp["onorm_w"], gate_bias=tp["gate_bias"], k=k)
