@@ -18,7 +18,8 @@ pytestmark = pytest.mark.gpu
                                                   (2, 32, 32, 8, 256, 37),     # full 32 x 32 grid
                                                   (3, 20, 64, 12, 192, 5),     # masked grid, 16 picks
                                                   (2, 48, 64, 8, 128, 64),     # 64 sub-keys, masked
-                                                  (1, 64, 64, 8, 64, 9)])      # 64 sub-keys, full, 8 picks
+                                                  (1, 64, 64, 8, 64, 9),       # 64 sub-keys, full, 8 picks
+                                                  (1, 32, 32, 8, 1024, 5)])    # head_dim 1,024: the read's limit
 def test_table_step_equals_map_address_and_read(H, n_sub, d_a, k, d, rows):
     g = torch.Generator(device="cpu").manual_seed(H * 1000 + n_sub + d_a + k + rows)
     dh = d // H
@@ -72,7 +73,7 @@ def test_trained_sdm_decode_shape_takes_the_one_launch_read():
 @pytest.mark.parametrize("H,n_sub,d_a,k,rows,inplace", [(1, 64, 32, 16, 64, True),    # the FULL model's table layer
                                                         (1, 64, 32, 16, 1, True),
                                                         (1, 64, 32, 16, 256, False),
-                                                        (1, 64, 32, 16, 7, True),     # a partial group
+                                                        (1, 64, 32, 16, 7, True),     # an odd token count
                                                         (2, 32, 32, 8, 37, False),    # two heads: not in place
                                                         (3, 20, 64, 12, 5, False)])
 def test_table_step_residual_equals_add_norm_then_table_step(H, n_sub, d_a, k, rows, inplace):
