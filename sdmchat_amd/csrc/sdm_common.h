@@ -895,11 +895,13 @@ __device__ __forceinline__ int xor_lanes32(int v, int j, int lane) {
 // Descending bitonic sort of one selection key per lane over aligned groups of N lanes (N a power of two <= 64):
 // lane i of a group ends with the group's i-th largest key.  The keys are non-negative doubles (their order is the
 // unsigned order of their bits) and are compared as 64-bit integers.  Every lane of the wave takes part.
-template <int N>
+// K0 > 2: the steps before the merge of K0-lane blocks are skipped; every aligned block of K0 lanes must then hold a
+// bitonic sequence (non-increasing, then non-decreasing, or the reverse).
+template <int N, int K0 = 2>
 __device__ __forceinline__ unsigned long long sort_lanes_desc(unsigned long long x, int lane) {
   const int idx = lane & (N - 1);
 #pragma unroll
-  for (int k = 2; k <= N; k <<= 1) {
+  for (int k = K0; k <= N; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
       const int ylo = xor_lanes32(static_cast<int>(x), j, lane);
@@ -911,6 +913,33 @@ __device__ __forceinline__ unsigned long long sort_lanes_desc(unsigned long long
     }
   }
   return x;
+}
+
+// The grid pair (ra, rb) of a lane in the layout of sorted runs select_lanes uses for a full grid (ra = -1: none).
+// CAP = 8 (20 pairs, lanes 0..31): lanes 0-7 row 0 (rb 0..7); 8-14 column 0 (ra 1..7); 16-18 row 1 (rb 1..3);
+// 22-23 column 1 reversed (ra 3, 2).  CAP = 16 (50 pairs, lanes 0..63): 0-15 row 0; 16-30 column 0 (ra 1..15),
+// 31 (3, 3); 32-38 row 1 (rb 1..7); 42-47 column 1 reversed (ra 7..2); 48-50 row 2 (rb 2..4); 62-63 column 2
+// reversed (ra 4, 3).  Each run descends (rows and columns of the grid do), so every block of CAP lanes is one
+// descending run, then an ascending one (or none), with key 0 between: a bitonic sequence.
+template <int CAP>
+__device__ __forceinline__ void grid_run_pair(int lane, int& ra, int& rb) {
+  static_assert(CAP == 8 || CAP == 16, "run layouts for 8 and 16 picks");
+  ra = -1;
+  rb = 0;
+  if constexpr (CAP == 8) {
+    if (lane < 8) { ra = 0; rb = lane; }
+    else if (lane < 15) { ra = lane - 7; rb = 0; }
+    else if (lane >= 16 && lane < 19) { ra = 1; rb = lane - 15; }
+    else if (lane == 22 || lane == 23) { ra = 25 - lane; rb = 1; }
+  } else {
+    if (lane < 16) { ra = 0; rb = lane; }
+    else if (lane < 31) { ra = lane - 15; rb = 0; }
+    else if (lane == 31) { ra = 3; rb = 3; }
+    else if (lane < 39) { ra = 1; rb = lane - 31; }
+    else if (lane >= 42 && lane < 48) { ra = 49 - lane; rb = 1; }
+    else if (lane >= 48 && lane < 51) { ra = 2; rb = lane - 46; }
+    else if (lane >= 62) { ra = 66 - lane; rb = 2; }
+  }
 }
 
 // sort_lanes_desc of two independent keys per lane at once (each exchange step moves both), so that the two chains
@@ -978,17 +1007,27 @@ __device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale,
     hk0 = lane < 16 ? key_or(c0, static_cast<uint32_t>(15 - lane) << KL::RS1) : c0;
     hk1 = lane < 16 ? key_or(c1, static_cast<uint32_t>(15 - lane) << KL::RS2) : c1;
   }
-  // grid pair of this lane: pairs (ra, rb) with (ra + 1)(rb + 1) <= CAP, row by row
-  int x = lane, ra = -1, rb = 0;
+  // grid pair of this lane: pairs (ra, rb) with (ra + 1)(rb + 1) <= CAP
+  constexpr int kGridLanes = n_pairs(CAP) <= 32 ? 32 : 64;
+  int ra = -1, rb = 0;
+  if constexpr (FULL && (CAP == 8 || CAP == 16)) {
+    // laid out as sorted runs (the grid's rows and columns descend: both halves' keys are sorted), two per aligned
+    // block of CAP lanes, the second reversed, so that every block is a bitonic sequence and the sort can start at
+    // its merge of CAP-lane blocks: CAP = 8: row 0 | column 0 below it | row 1 right of column 0 and, reversed,
+    // column 1 below row 1; CAP = 16 likewise with one more pair (row 2, column 2) and cell (3, 3) after column 0
+    grid_run_pair<CAP>(lane, ra, rb);
+  } else {   // row by row in lanes < n_pairs(CAP)
+    int x = lane;
 #pragma unroll
-  for (int a = 0; a < CAP; ++a) {
-    const int n_a = CAP / (a + 1);
-    if (ra < 0) {
-      if (x < n_a) {
-        ra = a;
-        rb = x;
-      } else {
-        x -= n_a;
+    for (int a = 0; a < CAP; ++a) {
+      const int n_a = CAP / (a + 1);
+      if (ra < 0) {
+        if (x < n_a) {
+          ra = a;
+          rb = x;
+        } else {
+          x -= n_a;
+        }
       }
     }
   }
@@ -997,8 +1036,12 @@ __device__ __forceinline__ void select_lanes(const AddrGeom& g, float log_scale,
   double k = k0 + k1;
   if (ra < 0) k = 0.0;   // no candidate: below every key
   else if (!FULL && !(ra < g.c1 && rb < g.c1 && (ra + 1) * (rb + 1) <= g.kk)) k = key_invalid(k);
-  // the candidates sit in lanes < n_pairs(CAP)
-  k = sort64(k, std::integral_constant<int, (n_pairs(CAP) <= 32 ? 32 : 64)>{});
+  if constexpr (FULL && (CAP == 8 || CAP == 16)) {
+    k = __longlong_as_double(static_cast<long long>(sort_lanes_desc<kGridLanes, CAP>(
+        static_cast<unsigned long long>(__double_as_longlong(k)), lane)));
+  } else {
+    k = sort64(k, std::integral_constant<int, kGridLanes>{});
+  }
   const float cv = grid_score<NS>(k);
   const uint32_t f = static_cast<uint32_t>(__double_as_longlong(k));
   int si;
