@@ -306,6 +306,21 @@ int sdm_rt_gemm_rows_residual(const void* x, int64_t x_row_stride, const void* y
                               const void* w, int64_t w_row_stride, const void* bias, void* out,
                               int64_t out_row_stride, int64_t rows, int32_t n, int32_t k, void* stream);
 
+/* sdm_rt_gemm_rows with the embedding gather and the first layer's input norm folded in front: OneSdmLM embeds the
+ * tokens (x = emb(idx), track4_onesdm_models.py:534-535) and the first mixer normalises them before its projections
+ * (RunTimeSdm.prepare, :197-206).  Here x_out[r] = table[tokens[r]] (the residual stream, an exact copy) and
+ * out = rms_norm(x_out, norm_w, norm_eps) W^T (+ bias), bit for bit the gather followed by sdm_rt_rms_norm (bf16 in
+ * and out) and sdm_rt_gemm_rows, in one launch.
+ *   tokens  [rows] int64, each in [0, vocab) (a token outside is clamped into it: the host does not read them);
+ *   table  [vocab][k] bf16;  x_out  [rows][k] bf16;  norm_w  [k] float32;  W, bias, out  as sdm_rt_gemm_rows
+ * k = 768, n a positive multiple of 32, at most 256 tiles of 64 rows x 32 columns (larger calls return
+ * SDM_RT_EUNSUPPORTED).  table, x_out and W rows and norm_w 16-byte aligned; x_out and out must not alias the table
+ * or each other. */
+int sdm_rt_gemm_rows_embed(const int64_t* tokens, const void* table, int64_t table_row_stride, int64_t vocab,
+                           const float* norm_w, float norm_eps, void* x_out, int64_t x_row_stride, const void* w,
+                           int64_t w_row_stride, const void* bias, void* out, int64_t out_row_stride, int64_t rows,
+                           int32_t n, int32_t k, void* stream);
+
 /* ---- training: forward with saved tensors, and the backward ------------------------------------------------
  * The reference trains RunTimeSdm through torch autograd of its chunked dense forward (RunTimeSdm.forward under
  * torch.utils.checkpoint, track4_onesdm_models.py:259-268).  These two entry points replace that autograd for the

@@ -132,6 +132,9 @@ SIGNATURES = {
     "sdm_rt_gemm_rows_residual": (ctypes.c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, ctypes.c_float,
                                                  c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_i64,
                                                  ctypes.c_int32, ctypes.c_int32, c_void_p]),
+    "sdm_rt_gemm_rows_embed": (ctypes.c_int, [c_void_p, c_void_p, c_i64, c_i64, c_void_p, ctypes.c_float, c_void_p,
+                                              c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_i64, ctypes.c_int32,
+                                              ctypes.c_int32, c_void_p]),
     "sdm_rt_forward_train": (ctypes.c_int, [ctypes.POINTER(SdmRtDims), ctypes.POINTER(SdmRtParams),
                                             c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
                                             ctypes.c_int, c_void_p,

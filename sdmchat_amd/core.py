@@ -687,6 +687,47 @@ def linear_residual(x, y, norm_w, eps, w, bias=None):
     return s, out
 
 
+def linear_embed_fits(idx, table, w, bias=None):
+    """Whether sdm_rt_gemm_rows_embed serves this embedding, first norm and map: idx int64 [rows] on the GPU, table
+    [vocab, 768] bf16 with 16-byte aligned rows, w and bias as linear_residual_fits takes them, at most 256 tiles of
+    64 rows x 32 columns, no autograd recording."""
+    if not (idx.is_cuda and idx.dtype == torch.int64 and idx.dim() == 1 and idx.numel() > 0):
+        return False
+    if not (table.is_cuda and table.dtype == torch.bfloat16 and table.dim() == 2
+            and table.shape[1] == GEMM_ROWS_FOLD_K and _rows16(table)):
+        return False
+    if not (w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[1] == GEMM_ROWS_FOLD_K and w.shape[0] % 32 == 0
+            and w.shape[0] > 0 and (bias is None or (bias.dtype == torch.bfloat16 and bias.numel() == w.shape[0]))):
+        return False
+    if (w.shape[0] // 32) * ((idx.numel() + 63) // 64) > 256:
+        return False
+    return not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (table, w, bias)))
+
+
+def linear_embed(idx, table, norm_w, eps, w, bias=None):
+    """The embedding gather, the first layer's input norm and its map in one launch (sdm_rt_gemm_rows_embed):
+    x = table[idx], hx = rms_norm(x, norm_w, eps) in bf16, out = linear(hx, w, bias); bit for bit the gather, rms_norm
+    and linear.  idx int64 [rows], each in [0, vocab) (one outside is clamped into it, not reported)
+    (linear_embed_fits).  Returns (x, out), x [rows, 768] a new tensor."""
+    k = GEMM_ROWS_FOLD_K
+    n = w.shape[0]
+    rows = idx.numel()
+    idx = idx.contiguous()
+    w = w if _rows16(w) else w.contiguous()
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    x = torch.empty(rows, k, dtype=torch.bfloat16, device=idx.device)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=idx.device)
+    wf = _f32_weight(norm_w, idx.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(idx.device).cuda_stream
+    rc = lib.sdm_rt_gemm_rows_embed(_ptr(idx), _ptr(table), table.stride(0), table.shape[0], _ptr(wf), float(eps),
+                                    _ptr(x), k, _ptr(w), w.stride(0), _ptr(bias), _ptr(out), n, rows, n, k,
+                                    ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    return x, out
+
+
 def _dims_of(kz, v, keys1, k, read_mode, out_norm, gated, read_eps, out_norm_eps):
     B, T = v.shape[0], v.shape[1]
     H, n_sub, half = keys1.shape

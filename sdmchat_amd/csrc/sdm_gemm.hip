@@ -71,31 +71,37 @@ __global__ void __launch_bounds__(256) gemm_rows_kernel(const bf16_t* __restrict
 // launcher takes the smaller tile while the blocks still fit the compute units at once); every operand of a wave
 // (12 16-deep steps) is loaded before its first product (one round trip).  Wave w's sums are those of
 // gemm_rows_kernel's first accumulator (with TR = 16 the operand rows past the tile repeat its last row, unused).
-// FOLD: x is rms_norm(x + y) (OneSdmLM's residual add and the next layer's input norm in front of its map): the block
-// computes its TR rows' sums and norms with the norm kernel's own code (norm_rows: the same bits as
+// FOLD kFoldAdd: x is rms_norm(x + y) (OneSdmLM's residual add and the next layer's input norm in front of its map):
+// the block computes its TR rows' sums and norms with the norm kernel's own code (norm_rows: the same bits as
 // sdm_rt_add_rms_norm, TR / 8 rows per half-wave, every load first) into LDS, column tile 0's blocks write the sums,
 // and the operands come from LDS (rows padded by 16 bytes, so the 32 rows an operand load reads spread over the banks).
+// FOLD kFoldEmbed: the same with x's rows gathered from a table by token (OneSdmLM's embedding in front of the first
+// layer's norm and map) and no add: column tile 0's blocks write the gathered rows, the residual stream.
 constexpr int kRowsK = 768;
 constexpr int kRowsSteps = kRowsK / 64;   // 16-deep steps per wave
 constexpr int kFoldRow = kRowsK + 8;      // bfloat16 per LDS row of the normed tile
 
-struct RowsFold {   // the residual add and norm in front of the map (FOLD)
+constexpr int kFoldNone = 0, kFoldAdd = 1, kFoldEmbed = 2;
+
+struct RowsFold {   // what runs in front of the map (FOLD): the residual add or the embedding gather, then the norm
   const bf16_t* y;
   int64_t ys;
   const float* w;
   float eps;
-  bf16_t* sum;
+  bf16_t* sum;        // the sums (kFoldAdd) or the gathered rows (kFoldEmbed)
   int64_t ss;
+  const int64_t* idx; // kFoldEmbed: the token of each row, clamped to [0, vocab)
+  int64_t vocab;
 };
 
-template <int TR, bool FOLD>
+template <int TR, int FOLD>
 __global__ void __launch_bounds__(256) gemm_rows_tile_kernel(const bf16_t* __restrict__ x, int64_t xs,
                                                           const bf16_t* __restrict__ w, int64_t ws,
                                                           const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
                                                           int64_t ys, int rows, RowsFold fold) {
   __shared__ float part[4][16][64];   // [wave][accumulator register][lane]
   static_assert(TR == 16 || TR == 32, "tiles of 16 or 32 rows");
-  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD ? TR : 1][FOLD ? kFoldRow : 8];
+  __shared__ __attribute__((aligned(16))) bf16_t s_hx[FOLD != kFoldNone ? TR : 1][FOLD != kFoldNone ? kFoldRow : 8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * kGemmCols, m0 = blockIdx.y * TR;
   const int kb = wave * (kRowsK / 4) + 8 * (lane >> 5);
@@ -103,7 +109,7 @@ __global__ void __launch_bounds__(256) gemm_rows_tile_kernel(const bf16_t* __res
   const int ra = min(min(r, TR - 1), rows - 1 - m0);   // the operand row in the tile: past it or past the end clamped
   const bf16_t* b = w + static_cast<int64_t>(n0 + r) * ws + kb;
   uint4 av[kRowsSteps], bv[kRowsSteps];
-  if constexpr (FOLD) {
+  if constexpr (FOLD != kFoldNone) {
 #pragma unroll
     for (int s = 0; s < kRowsSteps; ++s) bv[s] = *reinterpret_cast<const uint4*>(b + 16 * s);
     constexpr int R = TR / 8;   // rows 8 j + 2 wave + lane / 32 of the tile, j < R, for half-wave (wave, lane / 32)
@@ -118,12 +124,19 @@ __global__ void __launch_bounds__(256) gemm_rows_tile_kernel(const bf16_t* __res
       live[j] = m0 + i < rows;
       keep[j] = live[j] && blockIdx.x == 0;
       const int64_t rr = live[j] ? m0 + i : m0;   // rows past the end: an in-bounds stand-in, nothing written
-      xr[j] = x + rr * xs;
-      yr[j] = fold.y + rr * fold.ys;
+      if constexpr (FOLD == kFoldEmbed) {
+        const int64_t t = min(max(fold.idx[rr], static_cast<int64_t>(0)), fold.vocab - 1);
+        xr[j] = x + t * xs;
+        yr[j] = x;   // unused
+      } else {
+        xr[j] = x + rr * xs;
+        yr[j] = fold.y + rr * fold.ys;
+      }
       sr[j] = fold.sum + rr * fold.ss;
       dr[j] = &s_hx[i][0];
     }
-    norm_rows<bf16_t, bf16_t, true, kRowsK / 256, R>(xr, yr, sr, dr, fold.w, kRowsK, fold.eps, lane, live, keep);
+    norm_rows<bf16_t, bf16_t, FOLD == kFoldAdd, kRowsK / 256, R>(xr, yr, sr, dr, fold.w, kRowsK, fold.eps, lane, live,
+                                                                 keep);
     __syncthreads();
     const bf16_t* a = &s_hx[ra][kb];
 #pragma unroll
@@ -253,10 +266,10 @@ int sdm_rt_gemm_rows(const void* x, int64_t x_row_stride, const void* w, int64_t
     const int tr = map_tile_rows(ntiles, rows);
     const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + tr - 1) / tr));
     if (tr == 16)
-      hipLaunchKernelGGL((gemm_rows_tile_kernel<16, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
+      hipLaunchKernelGGL((gemm_rows_tile_kernel<16, kFoldNone>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
                          bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
     else
-      hipLaunchKernelGGL((gemm_rows_tile_kernel<32, false>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
+      hipLaunchKernelGGL((gemm_rows_tile_kernel<32, kFoldNone>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride,
                          bb, yb, y_row_stride, static_cast<int>(rows), RowsFold{});
   } else if (k == kRowsK && row_tiles <= 256) {
     // wide maps: about one block per compute unit, each walking its column tiles
@@ -301,7 +314,7 @@ int sdm_rt_gemm_rows_residual(const void* x, int64_t x_row_stride, const void* y
   if (sum_out == x || sum_out == y || out == x || out == y || out == sum_out)
     return set_err(SDM_RT_EINVAL, "gemm_rows_residual: sum_out and out must not alias x, y or each other");
   const RowsFold fold{static_cast<const bf16_t*>(y), y_row_stride, norm_w, norm_eps, static_cast<bf16_t*>(sum_out),
-                      sum_row_stride};
+                      sum_row_stride, nullptr, 0};
   const int tr = map_tile_rows(ntiles, rows);
   const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + tr - 1) / tr));
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -310,12 +323,57 @@ int sdm_rt_gemm_rows_residual(const void* x, int64_t x_row_stride, const void* y
   const bf16_t* bb = static_cast<const bf16_t*>(bias);
   bf16_t* ob = static_cast<bf16_t*>(out);
   if (tr == 16)
-    hipLaunchKernelGGL((gemm_rows_tile_kernel<16, true>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<16, kFoldAdd>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
                        ob, out_row_stride, static_cast<int>(rows), fold);
   else
-    hipLaunchKernelGGL((gemm_rows_tile_kernel<32, true>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<32, kFoldAdd>), grid, dim3(256), 0, st, xb, x_row_stride, wb, w_row_stride, bb,
                        ob, out_row_stride, static_cast<int>(rows), fold);
   return check_launch("gemm_rows_residual");
+}
+
+int sdm_rt_gemm_rows_embed(const int64_t* tokens, const void* table, int64_t table_row_stride, int64_t vocab,
+                           const float* norm_w, float norm_eps, void* x_out, int64_t x_row_stride, const void* w,
+                           int64_t w_row_stride, const void* bias, void* out, int64_t out_row_stride, int64_t rows,
+                           int32_t n, int32_t k, void* stream) {
+  g_err[0] = 0;
+  if (rows < 0 || n < 0 || k < 0) return set_err(SDM_RT_EINVAL, "rows, n and k must be >= 0");
+  if (k != kRowsK) return set_err(SDM_RT_EUNSUPPORTED, "gemm_rows_embed: k = %d, must be %d", k, kRowsK);
+  if (n == 0 || n % kGemmCols != 0)
+    return set_err(SDM_RT_EUNSUPPORTED, "gemm_rows_embed: n = %d must be a positive multiple of %d", n, kGemmCols);
+  if (vocab < 1) return set_err(SDM_RT_EINVAL, "gemm_rows_embed: vocab must be >= 1");
+  if (rows == 0) return SDM_RT_OK;
+  const int ntiles = n / kGemmCols;
+  if (static_cast<int64_t>(ntiles) * ((rows + kGemmRows - 1) / kGemmRows) > 256)
+    return set_err(SDM_RT_EUNSUPPORTED,
+                   "gemm_rows_embed: %lld rows x %d columns: more than 256 tiles of 64 x 32 (gather, call "
+                   "sdm_rt_rms_norm, then sdm_rt_gemm_rows)", (long long)rows, n);
+  if (!tokens || !table || !norm_w || !x_out || !w || !out)
+    return set_err(SDM_RT_EINVAL, "tokens, table, norm_w, x_out, w and out must not be NULL");
+  if (table_row_stride < k || x_row_stride < k || w_row_stride < k || out_row_stride < n)
+    return set_err(SDM_RT_EINVAL, "row strides too small");
+  auto al16 = [](const void* p, int64_t stride) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (stride * 2) % 16 == 0;
+  };
+  if (!al16(table, table_row_stride) || !al16(x_out, x_row_stride) || !al16(w, w_row_stride) ||
+      reinterpret_cast<uintptr_t>(norm_w) % 16)
+    return set_err(SDM_RT_EINVAL, "table, x_out and w rows and norm_w must be 16-byte aligned");
+  if (out == x_out || x_out == table || out == table)
+    return set_err(SDM_RT_EINVAL, "gemm_rows_embed: x_out and out must not alias the table or each other");
+  const RowsFold fold{nullptr, 0, norm_w, norm_eps, static_cast<bf16_t*>(x_out), x_row_stride, tokens, vocab};
+  const int tr = map_tile_rows(ntiles, rows);
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>((rows + tr - 1) / tr));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t* tb = static_cast<const bf16_t*>(table);
+  const bf16_t* wb = static_cast<const bf16_t*>(w);
+  const bf16_t* bb = static_cast<const bf16_t*>(bias);
+  bf16_t* ob = static_cast<bf16_t*>(out);
+  if (tr == 16)
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<16, kFoldEmbed>), grid, dim3(256), 0, st, tb, table_row_stride, wb,
+                       w_row_stride, bb, ob, out_row_stride, static_cast<int>(rows), fold);
+  else
+    hipLaunchKernelGGL((gemm_rows_tile_kernel<32, kFoldEmbed>), grid, dim3(256), 0, st, tb, table_row_stride, wb,
+                       w_row_stride, bb, ob, out_row_stride, static_cast<int>(rows), fold);
+  return check_launch("gemm_rows_embed");
 }
 
 }  // extern "C"

@@ -19,7 +19,7 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const InT* x, int64_t x_s
   const bool live = row < rows;   // both halves of a wave take part in the sums
   const int64_t r = live ? row : 0;
   norm_row<InT, OutT, ADD, KC>(x + r * x_stride, ADD ? y + r * y_stride : nullptr, ADD ? sum + r * sum_stride : nullptr,
-                               out + r * out_stride, w, d, eps, lane, live, live);
+                               out + r * out_stride, w, d, eps, lane, live, ADD && live);
 }
 
 // SwiGLU's gate: out = silu(g) * u with g, u the two halves of a row of the fused [gate | up] projection, each

@@ -86,8 +86,8 @@ __device__ __forceinline__ void unpack8(const Piece8<T>& pc, float (&v)[8]) {
 
 // R rows of the norm per half-wave: the 32 lanes of a half-wave (l % 32) each hold KC pieces of 8 consecutive values
 // of every row, c = 8 (l % 32 + 32 k), d <= 256 KC; the rows, the residuals and the weights are all loaded before
-// any use.  ADD: a row is x + y rounded to InT (a residual add), also written to sum when keep_sum (in place over x
-// is allowed: each value is read and written by the same lane).  out = (s * rsqrt(mean(s^2) + eps) rounded to InT)
+// any use.  ADD: a row is x + y rounded to InT (a residual add); the row (the sum, or x unchanged without ADD) is
+// written to sum when keep_sum (in place over x is allowed: each value is read and written by the same lane).  out = (s * rsqrt(mean(s^2) + eps) rounded to InT)
 // * w, written when live.  Both halves of the wave take part (the sums cross lanes): a half without a row passes
 // in-bounds pointers and live = keep_sum = false.  Each row's arithmetic does not depend on R.
 template <typename InT, typename OutT, bool ADD, int KC, int R>
@@ -123,8 +123,8 @@ __device__ __forceinline__ void norm_rows(const InT* const (&xr)[R], const InT* 
           unpack8<InT>(yp[r][k], u);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[k][e] = round_to<InT>(v[k][e] + u[e]);   // x + y in the input type
-          if (keep_sum[r]) store8<InT>(sr[r] + c, v[k]);
         }
+        if (keep_sum[r]) store8<InT>(sr[r] + c, v[k]);   // the sum (ADD), or x itself (a gathered row's copy)
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
       }

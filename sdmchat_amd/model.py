@@ -181,23 +181,27 @@ class OneSdmLM(nn.Module):
         norm = self.mnorms[i] if kind == "mlp" else self.nf
         return torch.promote_types(x.dtype, norm.w.dtype)
 
-    def _run(self, x, apply, apply_res=None):
+    def _run(self, x, apply, apply_res=None, y0=None):
         """Inference: the residual stream through every stage with each residual add fused into the next stage's
         input norm (core.add_rms_norm: one kernel for x = x + y and its RMSNorm, the same roundings as the add and
         the norm apart); in front of a TrainedSdm stage that takes it (a few tokens, TrainedSdm.residual_fits) the
         add and the norm run inside that stage's table step instead (TrainedSdm.forward_residual, the same bits), and
         in front of a mixer whose decode step takes it (apply_res given, RunTimeSdm.residual_fits) inside the
         mixer's projection map (RunTimeSdm.step_residual, the same bits).  apply(kind, i, x, hx) gives a stage's
-        output, apply_res(kind, i, x, y) a mixer's (x + y, output).  Returns nf(x)."""
+        output, apply_res(kind, i, x, y) a mixer's (x + y, output).  y0: the first stage's output, already computed
+        from x by the caller (RunTimeSdm.step_embed).  Returns nf(x)."""
         stages = self._stages()
         if not stages:
             return _norm(x, self.nf)
         kind, i, norm = stages[0]
         x = x.contiguous()   # the residual stream (enfold's fresh output), updated in place
-        hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
+        if y0 is None:
+            hx = core.rms_norm(x, norm.w, norm.eps, out_dtype=self._norm_dtype(kind, i, x))
         pending = None       # the last stage's output, to be added in front of this (TrainedSdm or mixer) stage
         for n, (kind, i, norm) in enumerate(stages):
-            if pending is not None:
+            if n == 0 and y0 is not None:
+                y = y0
+            elif pending is not None:
                 x, y = self.sdms[i].forward_residual(x, pending) if kind == "sdm" else apply_res(kind, i, x, pending)
                 pending = None
             else:
@@ -300,7 +304,12 @@ class OneSdmLM(nn.Module):
 
         def apply_res(kind, i, x, y):   # a mixer's step on x + y, the add and its norm in the projection map
             return self.mems[i].step_residual(x, y, state.layers[i], reset)
-        h = self._run(self.enfold(idx_t), apply, apply_res)
+        stages = self._stages()
+        first = None   # a first mixer's step on the embedded tokens, the gather and its norm in the projection map
+        if (stages and stages[0][0] == "mem" and type(self).enfold is OneSdmLM.enfold
+                and self.mems[stages[0][1]].embed_fits(idx_t, self.emb.weight)):
+            first = self.mems[stages[0][1]].step_embed(idx_t, self.emb.weight, state.layers[stages[0][1]], reset)
+        h = self._run(first[0] if first else self.enfold(idx_t), apply, apply_res, y0=first[1] if first else None)
         state.pos += 1
         return self.project(h)
 

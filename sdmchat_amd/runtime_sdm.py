@@ -377,6 +377,36 @@ class RunTimeSdm(nn.Module):
         out = self._step_projected(pa[..., :o_q], pa[..., o_q:o_g], V, g, state, reset, dt, x.dtype)
         return s.reshape(x.shape), out.reshape(x.shape)
 
+    def embed_fits(self, idx, table):
+        """Whether step_embed serves a step on table[idx]: bf16 rows of the layer width, few enough for the folded
+        map (core.linear_embed_fits on the whole projection buffer), inference."""
+        if not self.enabled or self.d != core.GEMM_ROWS_FOLD_K or self._training(table):
+            return False
+        if torch.is_autocast_enabled("cuda") or table.dtype != torch.bfloat16:
+            return False
+        W, bias = self._fused_weight(torch.bfloat16)[:2]
+        return core.linear_embed_fits(idx, table, W, bias)
+
+    def step_embed(self, idx, table, state, reset=None):
+        """step() on the embedded tokens x = table[idx] (OneSdmLM's embedding in front of its first layer,
+        track4_onesdm_models.py:534-535): the gather, the input norm and the whole projection map run in one launch
+        (core.linear_embed), bit for bit the gather, rms_norm and step(x, hx=...).  idx [B] int64, table [vocab, d]
+        bf16 (embed_fits).  Returns (x, out), each [B, d]."""
+        if not self.embed_fits(idx, table):
+            raise ValueError("step_embed: the folded map does not take these tokens (see embed_fits)")
+        B = idx.shape[0]
+        H, d_a = self.h, self.d_a
+        dt = torch.bfloat16
+        W, bias = self._fused_weight(dt)[:2]
+        ra = self._rows_a()
+        x, proj = core.linear_embed(idx, table, self.norm.w, self.norm.eps, W, bias)
+        proj = proj.view(B, 1, -1)
+        pa, V = proj[..., :ra], proj[..., ra:]
+        o_q, o_g = H * d_a, 2 * H * d_a
+        g = pa[..., o_g:o_g + H] if self.write_gate else None
+        out = self._step_projected(pa[..., :o_q], pa[..., o_q:o_g], V, g, state, reset, dt, dt)
+        return x, out.reshape(B, self.d)
+
     def forward_sequential(self, x, reset=None):
         """The token recurrence of the reference (track4_onesdm_models.py:276-300).  It is the same function as
         forward; the HIP core computes it once, so this is forward."""

@@ -125,6 +125,33 @@ def test_gemm_rows_residual_equals_add_norm_then_gemm_rows(rows, n, bias):
     assert torch.equal(o1.view(torch.int16), o0.view(torch.int16))
 
 
+@pytest.mark.parametrize("rows,n,bias", [(64, 2560, True), (64, 768, False), (1, 2560, True), (37, 768, True),
+                                         (192, 2560, False)])
+def test_gemm_rows_embed_equals_gather_norm_then_gemm_rows(rows, n, bias):
+    """sdm_rt_gemm_rows_embed (the embedding gather and the first mixer's input norm folded into its projection map)
+    against the gather, sdm_rt_rms_norm and sdm_rt_gemm_rows on the same tokens: the gathered rows and the products
+    bit for bit, with repeated tokens and the table's first and last rows among them."""
+    g = torch.Generator(device="cpu").manual_seed(rows * 5 + n)
+    vocab = 1000
+    table = torch.randn(vocab, 768, generator=g).to(torch.bfloat16).cuda()
+    idx = torch.randint(0, vocab, (rows,), generator=g)
+    idx[: min(rows, 3)] = torch.tensor([0, vocab - 1, 0])[: min(rows, 3)]
+    idx = idx.cuda()
+    nw = (torch.rand(768, generator=g) + 0.5).cuda()
+    w = (torch.randn(n, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()
+    b = torch.randn(n, generator=g).to(torch.bfloat16).cuda() if bias else None
+    say("gemm_rows_embed", rows, n, bias)
+    with torch.no_grad():
+        assert core.linear_embed_fits(idx, table, w, b)
+        x1, o1 = core.linear_embed(idx, table, nw, 1e-6, w, b)
+        x0 = table[idx]
+        hx = core.rms_norm(x0, nw, 1e-6, out_dtype=torch.bfloat16)
+        o0 = core.linear(hx, w, b)
+        torch.cuda.synchronize()
+    assert torch.equal(x1.view(torch.int16), x0.view(torch.int16))
+    assert torch.equal(o1.view(torch.int16), o0.view(torch.int16))
+
+
 def test_gemm_rows_residual_declines_large_maps():
     """More than 256 tiles of 64 rows x 32 columns: linear_residual_fits says no, and the entry point returns
     SDM_RT_EUNSUPPORTED without launching."""

@@ -112,9 +112,10 @@ def test_table_step_residual_equals_add_norm_then_table_step(H, n_sub, d_a, k, r
 
 def test_onesdm_decode_with_the_folded_add_equals_the_separate_add():
     """A OneSdmLM with TrainedSdm layers of width 768 decoding in bfloat16: the steps whose residual adds run inside
-    the table step (TrainedSdm.forward_residual) and inside the mixers' projection maps (RunTimeSdm.step_residual)
-    give the same logits, bit for bit, as the steps with the separate add-and-norm kernel, with either fold alone and
-    with neither."""
+    the table step (TrainedSdm.forward_residual) and inside the mixers' projection maps (RunTimeSdm.step_residual),
+    and whose embedding gather and first norm run inside the first mixer's map (RunTimeSdm.step_embed), give the same
+    logits, bit for bit, as the steps with the separate gather, norm and add-and-norm kernels, with the folds in
+    several combinations and with none."""
     from sdmchat_amd import OneSdmLM
     torch.manual_seed(11)
     m = OneSdmLM(512, d=768, layers=3, heads=4, n_sub=16, d_a=32, k=8, ffn="sdm", sdm_n_sub=32, sdm_heads=1,
@@ -127,29 +128,33 @@ def test_onesdm_decode_with_the_folded_add_equals_the_separate_add():
             mm.wo.weight.normal_(std=0.03)
     toks = torch.randint(0, 512, (6, 24), device="cuda")
     say("onesdm decode, folded adds against separate adds")
-    calls = {"table": 0, "mixer": 0}
+    calls = {"table": 0, "mixer": 0, "embed": 0}
 
-    def counting(mod, key):
-        fits = type(mod).residual_fits
+    def counting(mod, key, name="residual_fits"):
+        fits = getattr(type(mod), name)
 
-        def f(x, y):
-            ok = fits(mod, x, y)
+        def f(a, b):
+            ok = fits(mod, a, b)
             calls[key] += int(ok)
             return ok
         return f
 
     outs = []
-    for table_fold, mixer_fold in ((True, True), (True, False), (False, True), (False, False)):
+    for table_fold, mixer_fold, embed_fold in ((True, True, True), (True, False, False), (False, True, True),
+                                               (False, False, False), (False, False, True)):
         for sd in m.sdms:
             sd.residual_fits = counting(sd, "table") if table_fold else (lambda x, y: False)
         for mm in m.mems:
             mm.residual_fits = counting(mm, "mixer") if mixer_fold else (lambda x, y: False)
+            mm.embed_fits = counting(mm, "embed", "embed_fits") if embed_fold else (lambda idx, table: False)
         st = m.decode_state(24)
         with torch.no_grad():
             outs.append(torch.stack([m.step(toks[t], st) for t in range(6)]))
     for mod in list(m.sdms) + list(m.mems):
         del mod.residual_fits
-    assert calls["table"] > 0 and calls["mixer"] > 0, calls   # both folds ran
+    for mm in m.mems:
+        del mm.embed_fits
+    assert calls["table"] > 0 and calls["mixer"] > 0 and calls["embed"] > 0, calls   # every fold ran
     for o in outs[1:]:
         assert torch.equal(outs[0], o)
     assert torch.isfinite(outs[0].float()).all()

@@ -200,6 +200,23 @@ def test_gemm_rows_residual_arguments_are_checked_before_launch():
     assert call(0, 2560, 768) == 0   # no rows: nothing to do
 
 
+def test_gemm_rows_embed_arguments_are_checked_before_launch():
+    """The folded embedding map takes k = 768, n a multiple of 32, at most 256 tiles of 64 x 32, a vocabulary of at
+    least one row and no aliasing of its outputs with the table or each other."""
+    lib = _lib.load()
+    idx, t, nw, xo, w, o = (ctypes.c_void_p(16 * i) for i in range(1, 7))   # never dereferenced
+
+    def call(rows, n, k, vocab=100, x_out=xo, out=o):
+        return lib.sdm_rt_gemm_rows_embed(idx, t, k, vocab, nw, 1e-6, x_out, k, w, k, None, out, n, rows, n, k, None)
+    assert call(64, 2560, 512) != 0 and "768" in lib.sdm_rt_last_error().decode()
+    assert call(64, 100, 768) != 0 and "multiple of 32" in lib.sdm_rt_last_error().decode()
+    assert call(193, 2560, 768) != 0 and "256 tiles" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, vocab=0) != 0 and "vocab" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, x_out=t) != 0 and "alias" in lib.sdm_rt_last_error().decode()
+    assert call(64, 2560, 768, out=xo) != 0 and "alias" in lib.sdm_rt_last_error().decode()
+    assert call(0, 2560, 768) == 0   # no rows: nothing to do
+
+
 def test_prepare_key_pieces_checks_its_buffer():
     """The prepared sub-key pieces: their size for a shape, none for a shape without matrix-core scoring, and a
     buffer too small refused before launch."""
