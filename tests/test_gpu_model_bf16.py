@@ -94,6 +94,7 @@ class _Stages:
             for name in ("forward", "step"):
                 self._wrap(mm, name, ("mem", i))
             self._wrap_step_residual(mm, ("mem", i))
+            self._wrap_step_embed(mm, ("mem", i))
         for i, sd in enumerate(getattr(m, "sdms", [])):
             sd.keep_picks = True
             self._wrap(sd, "forward", ("sdm", i))
@@ -148,6 +149,22 @@ class _Stages:
             self.rec.setdefault(key, []).append(r)
             return s, out
         mod.step_residual = f
+
+    def _wrap_step_embed(self, mod, key):
+        """RunTimeSdm.step_embed (the embedding gather and the first norm folded into the first mixer's projection
+        map): the mixer's input is the returned gathered rows; its normed input is the norm kernel's on them (the
+        same bits: test_gemm_rows_embed_equals_gather_norm_then_gemm_rows)."""
+        orig = mod.step_embed
+
+        def f(idx, table, *a, **kw):
+            x, out = orig(idx, table, *a, **kw)
+            hx = core.rms_norm(x, mod.norm.w, mod.norm.eps, out_dtype=torch.bfloat16)
+            r = dict(x=x.detach().clone(), hx=hx, y=out.detach().clone(),
+                     proj=tuple(t.detach().clone() for t in mod.last_projections),
+                     picks=tuple(s_[..., :mod.k] for s_ in mod.last_picks))
+            self.rec.setdefault(key, []).append(r)
+            return x, out
+        mod.step_embed = f
 
     def get(self, key, B):
         rec = self.rec[key]
