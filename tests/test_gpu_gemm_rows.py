@@ -152,6 +152,23 @@ def test_gemm_rows_embed_equals_gather_norm_then_gemm_rows(rows, n, bias):
     assert torch.equal(o1.view(torch.int16), o0.view(torch.int16))
 
 
+def test_gemm_rows_embed_clamps_tokens_outside_the_table():
+    """A token below 0 or past the table reads the table's first or last row (the kernel's own bounds check; the host
+    never reads the tokens), as the clamped tokens do."""
+    g = torch.Generator(device="cpu").manual_seed(12)
+    vocab = 50
+    table = torch.randn(vocab, 768, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(64, 768, generator=g) * 0.04).to(torch.bfloat16).cuda()
+    nw = torch.ones(768).cuda()
+    idx = torch.tensor([-3, vocab + 7, 5, vocab - 1, 0], device="cuda")
+    with torch.no_grad():
+        x1, o1 = core.linear_embed(idx, table, nw, 1e-6, w)
+        x0, o0 = core.linear_embed(idx.clamp(0, vocab - 1), table, nw, 1e-6, w)
+        torch.cuda.synchronize()
+    assert torch.equal(x1, x0) and torch.equal(o1, o0)
+    assert torch.equal(x1[0], table[0]) and torch.equal(x1[1], table[vocab - 1])
+
+
 def test_gemm_rows_residual_declines_large_maps():
     """More than 256 tiles of 64 rows x 32 columns: linear_residual_fits says no, and the entry point returns
     SDM_RT_EUNSUPPORTED without launching."""
